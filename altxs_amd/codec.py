@@ -1,0 +1,211 @@
+"""Mixed-bit weight format: group-64 symmetric quantisation + the MFMA-tiled layout.
+
+Math (per tensor W[N, K], bits b in {2, 3, 4, 6}, groups of 64 along K):
+
+    w[n, k] = (code[n, k] - (2^b - 1) / 2) * scale[n, k // 64],  scale in fp16
+
+This is the reference's "symmetric" codebook mode
+(src/hyperflow_distillation/mixed_bit_delta.py:147-152, dequantize_channels
+172-229) with the channel width set to 64 and b = 6 added (the reference
+accepts only b in {2, 3, 4}, mixed_bit_delta.py:100-101).
+
+Device layout (``pack_tiled``), consumed by libaltxs_hip's MFMA GEMM:
+
+* the tensor is cut into blocks of 16 rows x 256 columns, block (nb, kb) at
+  index ``nb * (K // 256) + kb``;
+* inside a block, wave lane ``l`` (0..63) owns row ``l % 16`` and the columns
+  ``32*s + 8*(l // 16) + i`` for k-step ``s`` = 0..7 and ``i`` = 0..7 -- the B
+  operand of one v_mfma_f32_16x16x32 per k-step;
+* each code splits into bit planes (b=2: 2; b=3: 2+1; b=4: 4; b=6: 4+2); plane
+  ``p`` of width ``pb`` stores, per lane, the 64 codes LSB-first (code index
+  ``8*s + i`` at bit ``pb * (8*s + i)``) in ``8*pb`` bytes, lanes contiguous,
+  so a block is ``512*b`` bytes and each lane's share is whole 16/8-byte words;
+* scales per block: 16 rows x 4 groups fp16, row-major (128 bytes).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+
+BITS = (2, 3, 4, 6)
+PLANES = {2: (2,), 3: (2, 1), 4: (4,), 6: (4, 2)}
+GROUP = 64
+BLOCK_N = 16
+BLOCK_K = 256
+
+
+def quantize_group64(w: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """fp32 [N, K] -> (codes uint8 [N, K], scales fp16 [N, K // 64]).
+
+    scale = fp16(max|w_g| / ((2^b - 1) / 2)); code = clip(rint(w/scale + c), 0, 2^b - 1)
+    with c = (2^b - 1) / 2, computed against the fp16-rounded scale.
+    """
+    if bits not in BITS:
+        raise ValueError(f"bits must be one of {BITS}, got {bits}")
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    if k % GROUP:
+        raise ValueError(f"K={k} is not a multiple of {GROUP}")
+    c = (2 ** bits - 1) / 2.0
+    g = w.reshape(n, k // GROUP, GROUP)
+    amax = np.abs(g).max(axis=-1)
+    scale = (amax / c).astype(np.float16)
+    s32 = scale.astype(np.float32)
+    safe = np.where(s32 > 0, s32, 1.0).astype(np.float32)
+    q = np.rint(g / safe[..., None] + c)
+    q = np.where(s32[..., None] > 0, q, np.floor(c))
+    codes = np.clip(q, 0, 2 ** bits - 1).astype(np.uint8).reshape(n, k)
+    return codes, scale
+
+
+def dequantize_group64(codes: np.ndarray, scales: np.ndarray, bits: int) -> np.ndarray:
+    """(codes [N, K], scales fp16 [N, K//64]) -> fp32 [N, K] (exact)."""
+    n, k = codes.shape
+    c = np.float32((2 ** bits - 1) / 2.0)
+    v = codes.astype(np.float32) - c
+    s = np.repeat(scales.astype(np.float32), GROUP, axis=1)
+    return (v * s).astype(np.float32)
+
+
+def _lane_order(n: int, k: int) -> np.ndarray:
+    """Index array mapping tiled (block, lane, code) order -> flat [N*K] index."""
+    nb, kb = n // BLOCK_N, k // BLOCK_K
+    blk_n = np.arange(nb)[:, None, None, None, None]
+    blk_k = np.arange(kb)[None, :, None, None, None]
+    lane = np.arange(64)[None, None, :, None, None]
+    s = np.arange(8)[None, None, None, :, None]
+    i = np.arange(8)[None, None, None, None, :]
+    row = blk_n * BLOCK_N + lane % 16
+    col = blk_k * BLOCK_K + 32 * s + 8 * (lane // 16) + i
+    return (row * k + col).reshape(nb * kb, 64, 64)  # [block, lane, code j = 8s+i]
+
+
+def _pack_plane(vals: np.ndarray, pb: int) -> np.ndarray:
+    """vals uint [blocks, 64 lanes, 64 codes] (each < 2^pb) -> bytes [blocks, 64*8*pb]."""
+    nblk = vals.shape[0]
+    per_word = 32 // pb
+    v = vals.astype(np.uint32).reshape(nblk, 64, 64 // per_word, per_word)
+    shifts = (np.arange(per_word, dtype=np.uint32) * pb)[None, None, None, :]
+    words = np.bitwise_or.reduce(v << shifts, axis=-1).astype("<u4")  # [blk, lane, 2*pb]
+    return words.view(np.uint8).reshape(nblk, 64 * 8 * pb)
+
+
+def _unpack_plane(raw: np.ndarray, pb: int) -> np.ndarray:
+    nblk = raw.shape[0]
+    per_word = 32 // pb
+    words = np.ascontiguousarray(raw).view("<u4").reshape(nblk, 64, 2 * pb).astype(np.uint32)
+    shifts = (np.arange(per_word, dtype=np.uint32) * pb)[None, None, None, :]
+    v = (words[..., None] >> shifts) & np.uint32((1 << pb) - 1)
+    return v.reshape(nblk, 64, 64)
+
+
+def pack_tiled(codes: np.ndarray, scales: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """(codes [N, K] uint8, scales fp16 [N, K//64]) -> (tiled code bytes, tiled fp16 scales)."""
+    n, k = codes.shape
+    if n % BLOCK_N or k % BLOCK_K:
+        raise ValueError(f"tensor [{n}, {k}] must be a multiple of [{BLOCK_N}, {BLOCK_K}]")
+    if bits not in BITS:
+        raise ValueError(f"bits must be one of {BITS}")
+    if int(codes.max(initial=0)) >= 2 ** bits:
+        raise ValueError("code out of range for the bit width")
+    order = _lane_order(n, k)
+    lane_codes = codes.reshape(-1)[order].astype(np.uint32)  # [blk, lane, 64]
+    planes = []
+    shift = 0
+    for pb in PLANES[bits]:
+        planes.append(_pack_plane((lane_codes >> shift) & ((1 << pb) - 1), pb))
+        shift += pb
+    packed = np.concatenate(planes, axis=1).reshape(-1)
+    nb, kb = n // BLOCK_N, k // BLOCK_K
+    sc = scales.astype(np.float16).reshape(nb, BLOCK_N, kb, BLOCK_K // GROUP)
+    sc = np.ascontiguousarray(sc.transpose(0, 2, 1, 3)).reshape(-1)
+    return packed, sc
+
+
+def unpack_tiled(packed: np.ndarray, scales_t: np.ndarray, n: int, k: int,
+                 bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """Inverse of :func:`pack_tiled`."""
+    nb, kb = n // BLOCK_N, k // BLOCK_K
+    blk = np.asarray(packed, dtype=np.uint8).reshape(nb * kb, 512 * bits)
+    lane_codes = np.zeros((nb * kb, 64, 64), dtype=np.uint32)
+    off = 0
+    shift = 0
+    for pb in PLANES[bits]:
+        lane_codes |= _unpack_plane(blk[:, off:off + 512 * pb], pb) << shift
+        off += 512 * pb
+        shift += pb
+    codes = np.zeros(n * k, dtype=np.uint8)
+    codes[_lane_order(n, k).reshape(-1)] = lane_codes.reshape(-1).astype(np.uint8)
+    sc = np.asarray(scales_t, dtype=np.float16).reshape(nb, kb, BLOCK_N, BLOCK_K // GROUP)
+    sc = np.ascontiguousarray(sc.transpose(0, 2, 1, 3)).reshape(n, k // GROUP)
+    return codes.reshape(n, k), sc
+
+
+@dataclasses.dataclass
+class PackedTensor:
+    """One quantised tensor on the host: logical codes/scales + the device layout."""
+
+    name: str
+    bits: int
+    codes: np.ndarray   # uint8 [N, K]
+    scales: np.ndarray  # fp16 [N, K//64]
+    tiled: np.ndarray   # uint8 bytes
+    tiled_scales: np.ndarray  # fp16
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return tuple(self.codes.shape)  # type: ignore[return-value]
+
+    @property
+    def nbytes_codes(self) -> int:
+        return int(self.tiled.size)
+
+    @property
+    def nbytes_scales(self) -> int:
+        return int(self.tiled_scales.size * 2)
+
+    def dense(self) -> np.ndarray:
+        return dequantize_group64(self.codes, self.scales, self.bits)
+
+    @classmethod
+    def from_dense(cls, name: str, w: np.ndarray, bits: int) -> "PackedTensor":
+        codes, scales = quantize_group64(w, bits)
+        tiled, tsc = pack_tiled(codes, scales, bits)
+        return cls(name, bits, codes, scales, tiled, tsc)
+
+
+def allocate_bits(sizes: list[tuple[str, int]], target: float) -> dict[str, int]:
+    """Deterministic per-tensor widths from {2,3,4,6} near a mean of ``target`` bits.
+
+    Role recipe (names as in altxs_amd.synth.tensor_list): the first layer's
+    QKV at 6 bits, other QKV at 4, out-projection / MLP-up / embedding at 3,
+    MLP-down at 2; then MLP-down tensors are raised to 3 bits, in layer order,
+    while that moves the weighted mean closer to ``target``.
+    """
+    total = sum(n for _, n in sizes)
+    bits: dict[str, int] = {}
+    for name, _ in sizes:
+        role = name.rsplit(".", 1)[-1]
+        if name == "l0.qkv":
+            bits[name] = 6
+        elif role == "qkv":
+            bits[name] = 4
+        elif role == "down":
+            bits[name] = 2
+        else:
+            bits[name] = 3
+
+    def err() -> float:
+        return abs(sum(bits[nm] * n for nm, n in sizes) / total - target)
+
+    for name, _ in sizes:
+        if not name.endswith(".down"):
+            continue
+        before = err()
+        bits[name] = 3
+        if err() >= before:
+            bits[name] = 2
+            break
+    return bits

@@ -1,0 +1,178 @@
+// Deterministic softmax -> integer CDF (the frequency tables the range coder
+// consumes).  One workgroup of 1024 threads per row; thread t owns the
+// contiguous elements [t*EPT, t*EPT + EPT).  Every floating-point reduction
+// runs in a fixed order that depends only on V, so a row's tables are the same
+// whatever the number of rows in the launch (encode windows vs decode rows).
+//
+// Count rule (src/model/arithmetic_coder_lm.py:49-64, gpu_ac.py:38-42):
+//   f = max(1, floor(double(p) * 1e6 + 0.5))   -- two IEEE double roundings
+#include "common.h"
+#include "kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int CDF_THREADS = 1024;
+constexpr int CDF_WAVES = CDF_THREADS / WAVE;
+
+__device__ __forceinline__ uint32_t scale_count(float p) {
+  double t = __dmul_rn((double)p, 1000000.0);
+  t = __dadd_rn(t, 0.5);
+  double f = floor(t);
+  if (!(f >= 1.0)) return 1u;  // max(1, .); NaN maps to 1 as numpy's int cast + max does
+  if (f >= 4294967295.0) return 0xffffffffu;
+  return (uint32_t)f;
+}
+
+// Fixed-order block reductions over 16 waves.
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < CDF_WAVES; ++i) m = fmaxf(m, red[i]);
+  __syncthreads();
+  return m;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float s = red[0];
+#pragma unroll
+  for (int i = 1; i < CDF_WAVES; ++i) s += red[i];
+  __syncthreads();
+  return s;
+}
+
+// Exclusive block scan of one uint32 per thread (exact integer arithmetic).
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* wred) {
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  uint32_t incl = v;
+#pragma unroll
+  for (int d = 1; d < WAVE; d <<= 1) {
+    uint32_t o = __shfl_up(incl, d, WAVE);
+    if (l >= d) incl += o;
+  }
+  if (l == WAVE - 1) wred[w] = incl;
+  __syncthreads();
+  uint32_t base = 0;
+  for (int i = 0; i < w; ++i) base += wred[i];
+  __syncthreads();
+  return base + incl - v;
+}
+
+template <int EPT, bool FROM_LOGITS>
+__global__ __launch_bounds__(CDF_THREADS) void cdf_kernel(const float* __restrict__ in,
+                                                           int V, int flags,
+                                                           float* __restrict__ probs,
+                                                           uint32_t* __restrict__ cum) {
+  __shared__ float red[CDF_WAVES];
+  __shared__ uint32_t wred[CDF_WAVES];
+  const int64_t row = blockIdx.x;
+  const float* x = in + row * (int64_t)V;
+  const int base = threadIdx.x * EPT;
+  float v[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int j = base + i;
+    v[i] = (j < V) ? x[j] : 0.f;
+  }
+  if (FROM_LOGITS) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i)
+      if (base + i < V) m = fmaxf(m, v[i]);
+    m = block_max(m, red);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      v[i] = (base + i < V) ? expf(v[i] - m) : 0.f;
+      s += v[i];
+    }
+    s = block_sum(s, red);
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) v[i] = v[i] / s;
+    if (flags & ALTXS_CDF_RENORM) {
+      float s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) s2 += v[i];
+      s2 = block_sum(s2, red);
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) v[i] = v[i] / s2;
+    }
+    if (probs) {
+      float* po = probs + row * (int64_t)V;
+#pragma unroll
+      for (int i = 0; i < EPT; ++i)
+        if (base + i < V) po[base + i] = v[i];
+    }
+  }
+  if (!cum) return;
+  uint32_t f[EPT];
+  uint32_t tot = 0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    f[i] = (base + i < V) ? scale_count(v[i]) : 0u;
+    tot += f[i];
+  }
+  uint32_t run = block_excl_scan(tot, wred);
+  uint32_t* co = cum + row * (int64_t)(V + 1);
+  if (threadIdx.x == 0) co[0] = 0u;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    run += f[i];
+    if (base + i < V) co[base + i + 1] = run;
+  }
+}
+
+template <bool FROM_LOGITS>
+hipError_t launch_cdf(const float* in, int64_t rows, int V, int flags, float* probs,
+                      uint32_t* cum, hipStream_t s) {
+  const int ept = (V + CDF_THREADS - 1) / CDF_THREADS;
+  dim3 grid((unsigned)rows), block(CDF_THREADS);
+#define CDF_CASE(E)                                                                   \
+  if (ept <= E) {                                                                     \
+    hipLaunchKernelGGL((cdf_kernel<E, FROM_LOGITS>), grid, block, 0, s, in, V, flags, \
+                       probs, cum);                                                   \
+    return hipGetLastError();                                                         \
+  }
+  CDF_CASE(1) CDF_CASE(2) CDF_CASE(4) CDF_CASE(8) CDF_CASE(16) CDF_CASE(32) CDF_CASE(64)
+#undef CDF_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, bool from_logits,
+                            float* probs, uint32_t* cum, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  return from_logits ? launch_cdf<true>(in, rows, V, flags, probs, cum, s)
+                     : launch_cdf<false>(in, rows, V, flags, probs, cum, s);
+}
+
+extern "C" int32_t altxs_scale_cum(const float* probs, int64_t rows, int64_t V, uint32_t* cum,
+                                   altxs_stream_t stream) {
+  ALTXS_REQUIRE(probs && cum, "altxs_scale_cum: null pointer");
+  ALTXS_REQUIRE(V >= 1 && V <= 65536, "altxs_scale_cum: V=%lld outside [1, 65536]", (long long)V);
+  ALTXS_REQUIRE(rows >= 0 && rows < (1ll << 31), "altxs_scale_cum: bad rows");
+  ALTXS_CHECK_HIP(altxs_launch_cdf(probs, rows, (int)V, 0, false, nullptr, cum,
+                                   (hipStream_t)stream));
+  return ALTXS_OK;
+}
+
+extern "C" int32_t altxs_softmax_cdf(const float* logits, int64_t rows, int64_t V, int32_t flags,
+                                     float* probs, uint32_t* cum, altxs_stream_t stream) {
+  ALTXS_REQUIRE(logits, "altxs_softmax_cdf: null logits");
+  ALTXS_REQUIRE(V >= 1 && V <= 65536, "altxs_softmax_cdf: V=%lld outside [1, 65536]",
+                (long long)V);
+  ALTXS_REQUIRE(rows >= 0 && rows < (1ll << 31), "altxs_softmax_cdf: bad rows");
+  ALTXS_CHECK_HIP(altxs_launch_cdf(logits, rows, (int)V, flags, true, probs, cum,
+                                   (hipStream_t)stream));
+  return ALTXS_OK;
+}

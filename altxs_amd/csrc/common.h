@@ -1,0 +1,68 @@
+// Shared device helpers for the altxs HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/altxs.h"
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+#define WAVE 64
+
+// ---- bf16 <-> fp32 (bf16 stored as raw uint16) -----------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  // round-to-nearest-even via the hardware conversion (v_cvt_pk_bf16_f32)
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, b);
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ---- wave reductions (fixed butterfly order: deterministic) ---------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WAVE));
+  return v;
+}
+
+// ---- device error word ------------------------------------------------------
+// Kernels never fault on bad runtime values (positions, token ids): they skip
+// the access and OR a code into *err, which the host reads when it syncs.
+enum : int32_t {
+  ALTXS_EDEV_POS = 1,    // position >= max_len (KV write/read skipped)
+  ALTXS_EDEV_TOKEN = 2,  // token id outside [0, V) (clamped)
+};
+__device__ __forceinline__ void flag_err(int32_t* err, int32_t code) {
+  if (err) atomicOr(err, code);
+}
+
+// ---- host-side error plumbing ----------------------------------------------
+void altxs_set_error(const char* fmt, ...);
+#define ALTXS_CHECK_HIP(expr)                                                   \
+  do {                                                                          \
+    hipError_t e_ = (expr);                                                     \
+    if (e_ != hipSuccess) {                                                     \
+      altxs_set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_),    \
+                      __FILE__, __LINE__);                                      \
+      return ALTXS_ERR_HIP;                                                     \
+    }                                                                           \
+  } while (0)
+#define ALTXS_REQUIRE(cond, ...)                                                \
+  do {                                                                          \
+    if (!(cond)) {                                                              \
+      altxs_set_error(__VA_ARGS__);                                             \
+      return ALTXS_ERR_ARG;                                                     \
+    }                                                                           \
+  } while (0)

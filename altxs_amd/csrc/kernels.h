@@ -1,0 +1,10 @@
+// Internal launchers shared between translation units of libaltxs_hip.so.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, bool from_logits,
+                            float* probs, uint32_t* cum, hipStream_t s);
+
+struct AltxsAttnArgs;
+hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s);

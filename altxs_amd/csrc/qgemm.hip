@@ -1,0 +1,116 @@
+// Standalone C-ABI for the packed-weight kernels: dense dequantisation (test
+// and interop path), the fused dequant GEMM/GEMV, and its multi-tensor
+// streaming form used to measure HBM throughput over many distinct matrices.
+#include "common.h"
+#include "qgemm.h"
+
+using namespace altxs;
+
+namespace {
+
+// One wave per 16x256 block: lane l expands its 64 codes.
+template <int BITS>
+__global__ __launch_bounds__(64) void dequant_kernel(QT w, float* __restrict__ out) {
+  constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
+  constexpr float center = 0.5f * (float)((1 << BITS) - 1);
+  const int KB = w.K >> 8;
+  const int nb = blockIdx.x / KB, kb = blockIdx.x % KB;
+  const int lane = threadIdx.x;
+  uint32_t p0[2 * P0], p1[P1 > 0 ? 2 * P1 : 1];
+  float scale[4];
+  const size_t bi = (size_t)nb * KB + kb;
+  load_block<BITS>(w.codes + bi * (512 * BITS), w.scales + bi * 64, lane, p0, p1, scale);
+  const int n = nb * 16 + (lane & 15);
+  float* row = out + (size_t)n * w.K + kb * 256 + 8 * (lane >> 4);
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    uint32_t c[8];
+    codes_step<BITS>(p0, p1, s, c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) row[32 * s + i] = ((float)c[i] - center) * scale[s >> 1];
+  }
+}
+
+int check_qt(const AltxsQTensor* w, const char* who) {
+  ALTXS_REQUIRE(w && w->codes && w->scales, "%s: null tensor", who);
+  ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6,
+                "%s: bits=%d not in {2,3,4,6}", who, w->bits);
+  ALTXS_REQUIRE(w->N > 0 && w->N % 16 == 0 && w->N < (1 << 24), "%s: N=%lld must be a positive multiple of 16",
+                who, (long long)w->N);
+  ALTXS_REQUIRE(w->K > 0 && w->K % 256 == 0 && w->K <= 8192,
+                "%s: K=%lld must be a positive multiple of 256 (<= 8192)", who, (long long)w->K);
+  return ALTXS_OK;
+}
+
+QT to_qt(const AltxsQTensor* w) {
+  QT q;
+  q.codes = (const uint8_t*)w->codes;
+  q.scales = (const uint16_t*)w->scales;
+  q.N = (int)w->N;
+  q.K = (int)w->K;
+  return q;
+}
+
+template <int AM>
+hipError_t run_gemm(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss, const void* x,
+                    int xdt, int64_t rows, float* y, hipStream_t s) {
+  QT q = to_qt(w);
+  ProLoad pro{x, xdt, 0};
+  EpiStore epi{y, q.N, rows * q.N};
+  return launch_qgemm_bits<AM>(w->bits, q, (int)rows, (int)count, cs, ss, pro, epi, s);
+}
+
+int32_t gemm_common(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss, const void* x,
+                    int32_t xdt, int64_t rows, float* y, altxs_stream_t stream, const char* who) {
+  int rc = check_qt(w, who);
+  if (rc) return rc;
+  ALTXS_REQUIRE(x && y, "%s: null x/y", who);
+  ALTXS_REQUIRE(rows >= 1 && rows <= (1 << 20), "%s: rows=%lld out of range", who, (long long)rows);
+  ALTXS_REQUIRE(count >= 1 && count <= 65535, "%s: count=%lld out of range", who, (long long)count);
+  ALTXS_REQUIRE(xdt == ALTXS_F32 || xdt == ALTXS_BF16 || xdt == ALTXS_F16, "%s: bad x dtype %d", who,
+                xdt);
+  ALTXS_REQUIRE(lds_bytes((int)w->K, xdt == ALTXS_F32 ? A_F32 : A_BF16) <= 160 * 1024,
+                "%s: K=%lld too large for the LDS A tile", who, (long long)w->K);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (xdt == ALTXS_F32) e = run_gemm<A_F32>(w, count, cs, ss, x, xdt, rows, y, s);
+  else if (xdt == ALTXS_BF16) e = run_gemm<A_BF16>(w, count, cs, ss, x, xdt, rows, y, s);
+  else e = run_gemm<A_F16>(w, count, cs, ss, x, xdt, rows, y, s);
+  ALTXS_CHECK_HIP(e);
+  return ALTXS_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t altxs_dequant(const AltxsQTensor* w, float* out, altxs_stream_t stream) {
+  int rc = check_qt(w, "altxs_dequant");
+  if (rc) return rc;
+  ALTXS_REQUIRE(out, "altxs_dequant: null out");
+  QT q = to_qt(w);
+  dim3 grid((unsigned)((q.N / 16) * (q.K / 256))), block(64);
+  hipStream_t s = (hipStream_t)stream;
+  switch (w->bits) {
+    case 2: hipLaunchKernelGGL(dequant_kernel<2>, grid, block, 0, s, q, out); break;
+    case 3: hipLaunchKernelGGL(dequant_kernel<3>, grid, block, 0, s, q, out); break;
+    case 4: hipLaunchKernelGGL(dequant_kernel<4>, grid, block, 0, s, q, out); break;
+    case 6: hipLaunchKernelGGL(dequant_kernel<6>, grid, block, 0, s, q, out); break;
+  }
+  ALTXS_CHECK_HIP(hipGetLastError());
+  return ALTXS_OK;
+}
+
+extern "C" int32_t altxs_qgemm(const AltxsQTensor* w, const void* x, int32_t x_dtype, int64_t rows,
+                               float* y, altxs_stream_t stream) {
+  return gemm_common(w, 1, 0, 0, x, x_dtype, rows, y, stream, "altxs_qgemm");
+}
+
+extern "C" int32_t altxs_qgemm_stream(const AltxsQTensor* w, int64_t count, int64_t codes_stride,
+                                      int64_t scales_stride, const void* x, int32_t x_dtype,
+                                      int64_t rows, float* y, altxs_stream_t stream) {
+  ALTXS_REQUIRE(w, "altxs_qgemm_stream: null tensor");
+  ALTXS_REQUIRE(codes_stride >= w->N * w->K * w->bits / 8 && scales_stride >= w->N * w->K / 64 * 2 &&
+                    scales_stride % 2 == 0 && codes_stride % 16 == 0,
+                "altxs_qgemm_stream: strides smaller than one tensor or misaligned");
+  return gemm_common(w, count, codes_stride, scales_stride / 2, x, x_dtype, rows, y, stream,
+                     "altxs_qgemm_stream");
+}

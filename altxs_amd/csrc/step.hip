@@ -1,0 +1,740 @@
+// The whole per-symbol step for B independent segments x W window tokens.
+//
+// Per slot (one transformer layer application) five launches:
+//   QKV  : prologue = U-Net skip + resid_mix + RMSNorm*ln_scale (+ sparse-gate
+//          logits), MFMA dequant GEMM, epilogue = per-head QK-RMSNorm, RoPE,
+//          q_gain, K/V written into the cache at pos+t.
+//   ATTN : attn.hip (split over fixed 256-key chunks, fixed-order merge).
+//   O    : out-projection; epilogue = attention residual (or parallel lane term).
+//   UP   : prologue = RMSNorm*ln_scale of the attention output; epilogue =
+//          LeakyReLU(0.5)^2.
+//   DOWN : down-projection; epilogue = MLP residual / parallel-lane update.
+// Then the LM head (final RMSNorm prologue, tanh softcap epilogue), the
+// deterministic softmax -> CDF, and an optional commit (pos += W,
+// prev_raw = last raw embedding).  Every kernel computes each row from that
+// row's inputs only, so a decode row (W = 1) and the same position inside an
+// encode window (W > 1) or a larger batch produce identical bits.
+//
+// Semantics follow src/xsa_ttt/model.py: Block.forward 932-979,
+// CausalSelfAttention.forward 770-871, MLP 874-882, _parallel_block
+// 1293-1355, _apply_decoder_skip 1275-1291, _embed_tokens_window 1559-1579,
+// _project_logits/_apply_asym_softcap 1463-1500, _static_extend_body
+// 1649-1781.
+#include <string.h>
+
+#include "common.h"
+#include "kernels.h"
+#include "qgemm.h"
+
+using namespace altxs;
+
+namespace {
+
+constexpr int HD = 64;
+
+// torch.lerp(start, end, w) (ATen's two-branch formula)
+__device__ __forceinline__ float lerp_t(float start, float end, float w) {
+  return (fabsf(w) < 0.5f) ? start + w * (end - start) : end - (end - start) * (1.f - w);
+}
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+
+// ---- embedding (+ SmearGate) ------------------------------------------------
+
+// Dequantise 8 consecutive weights [8*run, 8*run+8) of row n of a packed tensor.
+template <int BITS>
+__device__ void dequant_run(const QT& w, int n, int run, float (&out)[8]) {
+  constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
+  constexpr float center = 0.5f * (float)((1 << BITS) - 1);
+  const int KB = w.K >> 8;
+  const int k0 = 8 * run, kb = k0 >> 8, kk = k0 & 255;
+  const int s = kk >> 5, lg = (kk & 31) >> 3;
+  const int L = (n & 15) + 16 * lg;
+  const size_t bi = (size_t)(n >> 4) * KB + kb;
+  const uint8_t* blk = w.codes + bi * (512 * BITS);
+  uint32_t p0[2 * P0], p1[P1 > 0 ? 2 * P1 : 1];
+  const uint32_t* a0 = (const uint32_t*)(blk + L * (8 * P0));
+#pragma unroll
+  for (int i = 0; i < 2 * P0; ++i) p0[i] = a0[i];
+  if constexpr (P1 > 0) {
+    const uint32_t* a1 = (const uint32_t*)(blk + 512 * P0 + L * (8 * P1));
+#pragma unroll
+    for (int i = 0; i < 2 * P1; ++i) p1[i] = a1[i];
+  }
+  uint32_t c[8];
+  codes_step<BITS>(p0, p1, s, c);
+  const float sc = __half2float(__ushort_as_half(w.scales[bi * 64 + (n & 15) * 4 + (kk >> 6)]));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = ((float)c[i] - center) * sc;
+}
+
+__device__ void dequant_run_bits(int bits, const QT& w, int n, int run, float (&out)[8]) {
+  switch (bits) {
+    case 2: dequant_run<2>(w, n, run, out); break;
+    case 3: dequant_run<3>(w, n, run, out); break;
+    case 4: dequant_run<4>(w, n, run, out); break;
+    default: dequant_run<6>(w, n, run, out); break;
+  }
+}
+
+struct EmbedP {
+  QT emb;
+  int bits, V, D, W, gw, smear;
+  float eps;
+  const int32_t* tokens;
+  const float* prev_raw;
+  float* cand_raw;
+  const float* smear_w;
+  const float* smear_lambda;
+  float* x0;  // [R, D]
+  int32_t* err;
+};
+
+constexpr int MAX_RUNS = 4;  // D <= 64 lanes * 4 runs * 8 = 2048
+
+__global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
+  const int r = blockIdx.x, lane = threadIdx.x;
+  const int b = r / a.W, t = r % a.W;
+  auto tok_at = [&](int tt) {
+    int tk = a.tokens[(int64_t)b * a.W + tt];
+    if (tk < 0 || tk >= a.V) {
+      if (lane == 0) flag_err(a.err, ALTXS_EDEV_TOKEN);
+      tk = tk < 0 ? 0 : a.V - 1;
+    }
+    return tk;
+  };
+  const int tok = tok_at(t);
+  const int nruns = a.D / 8;
+  float raw[MAX_RUNS][8], prev[MAX_RUNS][8];
+#pragma unroll
+  for (int j = 0; j < MAX_RUNS; ++j) {
+    const int run = lane + 64 * j;
+    if (run < nruns) dequant_run_bits(a.bits, a.emb, tok, run, raw[j]);
+  }
+  float x[MAX_RUNS][8];
+  if (a.smear) {
+    const int ptok = t > 0 ? tok_at(t - 1) : -1;
+#pragma unroll
+    for (int j = 0; j < MAX_RUNS; ++j) {
+      const int run = lane + 64 * j;
+      if (run >= nruns) continue;
+      if (ptok >= 0) {
+        dequant_run_bits(a.bits, a.emb, ptok, run, prev[j]);
+      } else {
+        const float* pr = a.prev_raw + (int64_t)b * a.D + 8 * run;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) prev[j][i] = pr[i];
+      }
+    }
+    // g = lambda * sigmoid(raw[:gw] . w_smear)
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAX_RUNS; ++j) {
+      const int run = lane + 64 * j;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = 8 * run + i;
+        if (run < nruns && k < a.gw) part += raw[j][i] * a.smear_w[k];
+      }
+    }
+    const float gsum = wave_sum(part);
+    const float g = a.smear_lambda[0] * sigmoidf(gsum);
+#pragma unroll
+    for (int j = 0; j < MAX_RUNS; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[j][i] = raw[j][i] + g * prev[j][i];
+  } else {
+#pragma unroll
+    for (int j = 0; j < MAX_RUNS; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[j][i] = raw[j][i];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAX_RUNS; ++j)
+    if (lane + 64 * j < nruns)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += x[j][i] * x[j][i];
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)a.D + a.eps);
+#pragma unroll
+  for (int j = 0; j < MAX_RUNS; ++j) {
+    const int run = lane + 64 * j;
+    if (run >= nruns) continue;
+    float* xo = a.x0 + (int64_t)r * a.D + 8 * run;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xo[i] = x[j][i] * inv;
+    if (t == a.W - 1) {
+      float* co = a.cand_raw + (int64_t)b * a.D + 8 * run;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) co[i] = raw[j][i];
+    }
+  }
+}
+
+// ---- prologues -------------------------------------------------------------
+
+constexpr int MAXC = 4;  // float4 chunks per lane: D <= 64*4*4 = 1024
+
+// Attention-side input of a slot: skip, resid_mix, RMSNorm * ln_scale.
+struct ProQKV {
+  const float* x;      // slot input (x, or lane0 for a parallel slot)
+  const float* x0;     // embedding output
+  const float* skip;   // popped encoder output or NULL
+  const float* skip_w; // [D] row of skip_weights
+  const float* skip_g; // [D] row of skip_gates or NULL
+  const float* mix;    // [2, D]
+  float* base_out;     // x_in (sequential) / lane0 after skip (parallel); block x==0 writes
+  const float* gate_w; // [H, gw] or NULL
+  float* gate_out;     // [R, H]
+  float ln_scale, eps, gate_scale;
+  int D, H, gw, parallel;
+  template <int AM>
+  __device__ void stage(void* As, int m0, int R, int K, int) const {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = D >> 2;
+    const bool writer = blockIdx.x == 0;
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * wave + i, r = m0 + row;
+      if (r >= R) {
+        for (int c = lane; c < nch; c += 64)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a_store<AM>(As, row, 4 * c + e, K, 0.f);
+        continue;
+      }
+      float v[MAXC][4];
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        if (c >= nch) continue;
+        const f32x4 xv = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
+        const f32x4 x0v = *(const f32x4*)(x0 + (int64_t)r * D + 4 * c);
+        float bs[4] = {xv[0], xv[1], xv[2], xv[3]};
+        if (skip) {
+          const f32x4 sv = *(const f32x4*)(skip + (int64_t)r * D + 4 * c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float sc = skip_w[4 * c + e] * sv[e];
+            if (skip_g) bs[e] = lerp_t(sc, bs[e], sigmoidf(skip_g[4 * c + e]));
+            else bs[e] = bs[e] + sc;
+          }
+        }
+        float in[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) in[e] = mix[4 * c + e] * bs[e] + mix[D + 4 * c + e] * x0v[e];
+        if (writer) {
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = parallel ? bs[e] : in[e];
+          *(f32x4*)(base_out + (int64_t)r * D + 4 * c) = o;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[j][e] = in[e];
+          ss += in[e] * in[e];
+        }
+      }
+      ss = wave_sum(ss);
+      const float inv = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+      for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        if (c >= nch) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float n = (v[j][e] * inv) * ln_scale;
+          a_store<AM>(As, row, 4 * c + e, K, n);
+          v[j][e] = n;
+        }
+      }
+      if (writer && gate_w) {
+        for (int h = 0; h < H; ++h) {
+          float part = 0.f;
+#pragma unroll
+          for (int j = 0; j < MAXC; ++j) {
+            const int c = lane + 64 * j;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int k = 4 * c + e;
+              if (c < nch && k < gw) part += v[j][e] * gate_w[h * gw + k];
+            }
+          }
+          const float dot = wave_sum(part);
+          if (lane == 0) gate_out[(int64_t)r * H + h] = sigmoidf(gate_scale * dot);
+        }
+      }
+    }
+  }
+};
+
+// RMSNorm (* scale) of rows of x (MLP input, final norm; final may average lanes).
+struct ProNorm {
+  const float* x;
+  const float* x2;  // second lane (final parallel "mean") or NULL
+  int lane_mode;    // 0: x, 1: 0.5*(x + x2)
+  float scale, eps;
+  int D;
+  template <int AM>
+  __device__ void stage(void* As, int m0, int R, int K, int) const {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = D >> 2;
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * wave + i, r = m0 + row;
+      if (r >= R) {
+        for (int c = lane; c < nch; c += 64)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a_store<AM>(As, row, 4 * c + e, K, 0.f);
+        continue;
+      }
+      float v[MAXC][4];
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        if (c >= nch) continue;
+        const f32x4 xv = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
+        f32x4 yv = xv;
+        if (lane_mode == 1) {
+          const f32x4 x2v = *(const f32x4*)(x2 + (int64_t)r * D + 4 * c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) yv[e] = 0.5f * (xv[e] + x2v[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[j][e] = yv[e];
+          ss += yv[e] * yv[e];
+        }
+      }
+      ss = wave_sum(ss);
+      const float inv = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+      for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        if (c >= nch) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a_store<AM>(As, row, 4 * c + e, K, (v[j][e] * inv) * scale);
+      }
+    }
+  }
+};
+
+// ---- epilogues --------------------------------------------------------------
+
+__device__ __forceinline__ int row_pos(const int32_t* pos, int W, int r) {
+  return pos[r / W] + (r % W);
+}
+
+struct EpiQKV {
+  float* q;          // [R, H, 64]
+  char* kv;          // this slot's cache: [B][2][Hkv][max_len][64]
+  int kv_bf16, H, Hkv, W, max_len, rd;
+  const int32_t* pos;
+  const float* cosb;  // [max_len, rd/2]
+  const float* sinb;
+  const float* q_gain;
+  float eps;
+  int32_t* err;
+  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int wave,
+                             unsigned char* smem, int R, int) const {
+    // Exchange the 16x64 tile (one head) through LDS.
+    __syncthreads();  // every wave is done reading the A tile
+    float* C = (float*)smem;
+    constexpr int CS = HD + 1;
+    const int cl = wave * 16 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) C[(4 * (lane >> 4) + i) * CS + cl] = acc[i];
+    __syncthreads();
+    const int nt = blockIdx.x;  // head tile
+    const int kind = nt < H ? 0 : (nt < H + Hkv ? 1 : 2);
+    const int head = kind == 0 ? nt : (kind == 1 ? nt - H : nt - H - Hkv);
+    const int64_t esz = kv_bf16 ? 2 : 4;
+    const int half = rd >> 1;
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * wave + i, r = m0 + row;
+      if (r >= R) continue;  // wave-uniform
+      float val = C[row * CS + lane];
+      int p = row_pos(pos, W, r);
+      const bool pos_ok = p >= 0 && p < max_len;
+      if (!pos_ok && lane == 0) flag_err(err, ALTXS_EDEV_POS);
+      if (kind < 2) {
+        const float ss = wave_sum(val * val);
+        val = val * rsqrtf(ss * (1.0f / HD) + eps);
+        const int pp = pos_ok ? p : 0;
+        const int partner = lane < half ? lane + half : lane - half;
+        const float pv = __shfl(val, partner & 63, WAVE);
+        if (lane < rd) {
+          const int fi = lane < half ? lane : lane - half;
+          const float cs = cosb[(int64_t)pp * half + fi];
+          const float sn = sinb[(int64_t)pp * half + fi];
+          val = lane < half ? (val * cs + pv * sn) : (pv * -sn + val * cs);
+        }
+      }
+      if (kind == 0) {
+        q[((int64_t)r * H + head) * HD + lane] = val * q_gain[head];
+      } else if (pos_ok) {
+        const int b = r / W;
+        const int64_t off =
+            ((((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len + p) * HD + lane;
+        if (kv_bf16) ((uint16_t*)kv)[off] = f32_to_bf16(val);
+        else ((float*)kv)[off] = val;
+        (void)esz;
+      }
+    }
+  }
+};
+
+struct EpiO {
+  const float* xin;
+  const float* attn_scale;
+  float* xout;
+  int D, parallel;
+  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
+                             int R, int) const {
+    const int col = nb * 16 + (lane & 15);
+    if (col >= D) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = m0 + 4 * (lane >> 4) + i;
+      if (r >= R) continue;
+      const int64_t o = (int64_t)r * D + col;
+      const float a = attn_scale[col] * acc[i];
+      xout[o] = parallel ? a : xin[o] + a;
+    }
+  }
+};
+
+struct EpiUp {
+  void* h;  // [R, F] fp32 or bf16
+  int F, hb16;
+  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
+                             int R, int) const {
+    const int col = nb * 16 + (lane & 15);
+    if (col >= F) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = m0 + 4 * (lane >> 4) + i;
+      if (r >= R) continue;
+      const float v = acc[i];
+      const float lr = v > 0.f ? v : 0.5f * v;
+      const float o = lr * lr;
+      const int64_t idx = (int64_t)r * F + col;
+      if (hb16) ((uint16_t*)h)[idx] = f32_to_bf16(o);
+      else ((float*)h)[idx] = o;
+    }
+  }
+};
+
+struct EpiDown {
+  const float* xout;   // seq: x_out; par: attn term a
+  const float* mlp_scale;
+  float* out0;         // seq: slot output; par: lane0'
+  float* out1;         // par: lane1'
+  const float* lane0;  // par: lane0 after skip
+  const float* lane1;  // par: lane1 input
+  const float* pr;     // par: [2]
+  const float* pp;     // par: [2, 2]
+  int D, parallel;
+  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
+                             int R, int) const {
+    const int col = nb * 16 + (lane & 15);
+    if (col >= D) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = m0 + 4 * (lane >> 4) + i;
+      if (r >= R) continue;
+      const int64_t o = (int64_t)r * D + col;
+      const float m = mlp_scale[col] * acc[i];
+      if (!parallel) {
+        out0[o] = xout[o] + m;
+      } else {
+        const float a = xout[o];
+        out0[o] = pr[0] * lane0[o] + pp[0] * a + pp[2] * m;
+        out1[o] = pr[1] * lane1[o] + pp[1] * a + pp[3] * m;
+      }
+    }
+  }
+};
+
+struct EpiLogits {
+  float* logits;
+  int V, asym;
+  float cap;
+  const float* cap_pn;
+  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
+                             int R, int) const {
+    const int col = nb * 16 + (lane & 15);
+    if (col >= V) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = m0 + 4 * (lane >> 4) + i;
+      if (r >= R) continue;
+      const float l = acc[i];
+      float o;
+      if (asym) {
+        const float c = l >= 0.f ? cap_pn[0] : cap_pn[1];
+        o = c * tanhf(l / c);
+      } else {
+        o = cap * tanhf(l / cap);
+      }
+      logits[(int64_t)r * V + col] = o;
+    }
+  }
+};
+
+__global__ void commit_kernel(int32_t* pos, float* prev_raw, const float* cand_raw, int B, int D,
+                              int W) {
+  const int b = blockIdx.x;
+  for (int k = threadIdx.x; k < D; k += blockDim.x)
+    prev_raw[(int64_t)b * D + k] = cand_raw[(int64_t)b * D + k];
+  if (threadIdx.x == 0) pos[b] += W;
+}
+
+// ---- host side --------------------------------------------------------------
+
+struct WS {
+  float *X0, *X1, *XIN, *XOUT, *Q, *GATE;
+  void *Y, *HB;
+};
+
+int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+int64_t carve(const AltxsStepDesc* d, WS* w, char* base) {
+  const int64_t R = (int64_t)d->B * d->W, Rp = align_up(R, 16);
+  const int64_t D = d->D, n = d->n_slots;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align_up(bytes, 256);
+    return p;
+  };
+  char* x0 = take((n + 1) * Rp * D * 4);
+  char* x1 = take((n + 1) * Rp * D * 4);
+  char* xin = take(Rp * D * 4);
+  char* xout = take(Rp * D * 4);
+  char* q = take(Rp * d->H * HD * 4);
+  char* gate = take(Rp * d->H * 4);
+  char* y = take(Rp * D * 4);
+  char* hb = take(Rp * (int64_t)d->F * 4);
+  if (w) {
+    w->X0 = (float*)x0; w->X1 = (float*)x1; w->XIN = (float*)xin; w->XOUT = (float*)xout;
+    w->Q = (float*)q; w->GATE = (float*)gate; w->Y = y; w->HB = hb;
+  }
+  return off;
+}
+
+QT qt_of(const AltxsQTensor& t) {
+  QT q;
+  q.codes = (const uint8_t*)t.codes;
+  q.scales = (const uint16_t*)t.scales;
+  q.N = (int)t.N;
+  q.K = (int)t.K;
+  return q;
+}
+
+int check_tensor(const AltxsQTensor& t, int64_t N, int64_t K, const char* what, int li) {
+  ALTXS_REQUIRE(t.codes && t.scales, "altxs_step: layer %d %s: null tensor", li, what);
+  ALTXS_REQUIRE(t.N == N && t.K == K, "altxs_step: layer %d %s: shape [%lld,%lld] != [%lld,%lld]",
+                li, what, (long long)t.N, (long long)t.K, (long long)N, (long long)K);
+  ALTXS_REQUIRE(t.bits == 2 || t.bits == 3 || t.bits == 4 || t.bits == 6,
+                "altxs_step: layer %d %s: bits=%d", li, what, t.bits);
+  ALTXS_REQUIRE(((uintptr_t)t.codes & 15) == 0 && ((uintptr_t)t.scales & 7) == 0,
+                "altxs_step: layer %d %s: misaligned", li, what);
+  return ALTXS_OK;
+}
+
+int validate(const AltxsStepDesc* d) {
+  ALTXS_REQUIRE(d, "altxs_step: null descriptor");
+  ALTXS_REQUIRE(d->abi_version == ALTXS_ABI_VERSION, "altxs_step: abi_version %d != %d",
+                d->abi_version, ALTXS_ABI_VERSION);
+  ALTXS_REQUIRE(d->head_dim == HD, "altxs_step: head_dim=%d (only 64 is built)", d->head_dim);
+  ALTXS_REQUIRE(d->D == d->H * HD, "altxs_step: D != H*head_dim");
+  ALTXS_REQUIRE(d->D % 256 == 0 && d->D <= 1024, "altxs_step: D=%d must be a multiple of 256, <= 1024",
+                d->D);
+  ALTXS_REQUIRE(d->F % 256 == 0 && d->F <= 8192, "altxs_step: F=%d must be a multiple of 256", d->F);
+  ALTXS_REQUIRE(d->V >= 16 && d->V % 16 == 0 && d->V <= 65536, "altxs_step: V=%d must be a multiple of 16 in [16, 65536]",
+                d->V);
+  ALTXS_REQUIRE(d->Hkv >= 1 && d->H % d->Hkv == 0, "altxs_step: H %% Hkv != 0");
+  const int group = d->H / d->Hkv;
+  ALTXS_REQUIRE(group == 1 || group == 2 || group == 4, "altxs_step: H/Hkv=%d not in {1,2,4}", group);
+  ALTXS_REQUIRE(d->B >= 1 && d->W >= 1 && (int64_t)d->B * d->W <= (1 << 20), "altxs_step: bad B/W");
+  ALTXS_REQUIRE(d->n_layers >= 1 && d->n_layers <= ALTXS_MAX_LAYERS, "altxs_step: n_layers");
+  ALTXS_REQUIRE(d->n_slots >= 1 && d->n_slots <= ALTXS_MAX_SLOTS, "altxs_step: n_slots");
+  ALTXS_REQUIRE(d->max_len >= 256 && d->max_len % 256 == 0, "altxs_step: max_len=%d must be a multiple of 256",
+                d->max_len);
+  ALTXS_REQUIRE(d->rope_dims >= 2 && d->rope_dims <= HD && d->rope_dims % 2 == 0,
+                "altxs_step: rope_dims=%d", d->rope_dims);
+  ALTXS_REQUIRE(d->gate_window >= 0 && d->gate_window <= d->D, "altxs_step: gate_window");
+  ALTXS_REQUIRE(d->lora_rank == 0, "altxs_step: LoRA is not built in this version");
+  ALTXS_REQUIRE(d->tokens && d->pos && d->prev_raw && d->cand_raw && d->kv && d->ws && d->logits &&
+                    d->rope_cos && d->rope_sin && d->err,
+                "altxs_step: null state/output pointer");
+  ALTXS_REQUIRE(d->ws_bytes >= carve(d, nullptr, nullptr), "altxs_step: workspace too small");
+  if (d->flags & ALTXS_F_SMEAR)
+    ALTXS_REQUIRE(d->smear_w && d->smear_lambda, "altxs_step: smear params missing");
+  if (d->flags & ALTXS_F_ASYM_SOFTCAP) ALTXS_REQUIRE(d->softcap_pn, "altxs_step: softcap_pn missing");
+  const int kvd = d->Hkv * HD;
+  for (int l = 0; l < d->n_layers; ++l) {
+    const AltxsLayer& L = d->layers[l];
+    int rc;
+    if ((rc = check_tensor(L.qkv, d->D + 2 * kvd, d->D, "qkv", l))) return rc;
+    if ((rc = check_tensor(L.o, d->D, d->D, "o", l))) return rc;
+    if ((rc = check_tensor(L.up, d->F, d->D, "up", l))) return rc;
+    if ((rc = check_tensor(L.down, d->D, d->F, "down", l))) return rc;
+    ALTXS_REQUIRE(L.resid_mix && L.attn_scale && L.mlp_scale && L.q_gain,
+                  "altxs_step: layer %d small params missing", l);
+    if (d->flags & ALTXS_F_SPARSE_GATE)
+      ALTXS_REQUIRE(L.attn_gate_w, "altxs_step: layer %d attn_gate_w missing", l);
+  }
+  int rc;
+  if ((rc = check_tensor(d->emb, d->V, d->D, "emb", -1))) return rc;
+  for (int s = 0; s < d->n_slots; ++s) {
+    const AltxsSlot& S = d->slots[s];
+    ALTXS_REQUIRE(S.layer >= 0 && S.layer < d->n_layers, "altxs_step: slot %d layer", s);
+    ALTXS_REQUIRE(S.kind == ALTXS_SLOT_SEQ || S.kind == ALTXS_SLOT_PAR, "altxs_step: slot %d kind", s);
+    ALTXS_REQUIRE(S.skip_src < s, "altxs_step: slot %d pops a later slot", s);
+    if (S.skip_src >= 0) ALTXS_REQUIRE(S.skip_idx >= 0 && d->skip_weights, "altxs_step: slot %d skip", s);
+    if (S.kind == ALTXS_SLOT_PAR)
+      ALTXS_REQUIRE(d->layers[S.layer].par_resid && d->layers[S.layer].par_post,
+                    "altxs_step: slot %d parallel lambdas missing", s);
+  }
+  return ALTXS_OK;
+}
+
+template <int AM>
+hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
+  const int R = d->B * d->W;
+  const int64_t Rp = align_up(R, 16);
+  const int64_t D = d->D;
+  const int hb16 = AM == A_BF16 ? 1 : 0;
+  const int xdt = AM == A_BF16 ? ALTXS_BF16 : ALTXS_F32;
+  const int64_t esz = d->kv_bf16 ? 2 : 4;
+  const int64_t slot_kv = (int64_t)d->B * 2 * d->Hkv * d->max_len * HD;
+  hipError_t e;
+
+  {  // embedding
+    EmbedP p;
+    p.emb = qt_of(d->emb); p.bits = d->emb.bits; p.V = d->V; p.D = d->D; p.W = d->W;
+    p.gw = d->gate_window; p.smear = (d->flags & ALTXS_F_SMEAR) ? 1 : 0; p.eps = d->norm_eps;
+    p.tokens = d->tokens; p.prev_raw = d->prev_raw; p.cand_raw = d->cand_raw;
+    p.smear_w = d->smear_w; p.smear_lambda = d->smear_lambda; p.x0 = w.X0; p.err = d->err;
+    hipLaunchKernelGGL(embed_kernel, dim3(R), dim3(64), 0, st, p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  const float* x0 = w.X0;
+  for (int s = 0; s < d->n_slots; ++s) {
+    const AltxsSlot& S = d->slots[s];
+    const AltxsLayer& L = d->layers[S.layer];
+    const bool par = S.kind == ALTXS_SLOT_PAR;
+    float* xin_slot = w.X0 + s * Rp * D;           // x or lane0 entering the slot
+    const float* lane1_in = par ? (S.first_parallel ? xin_slot : w.X1 + s * Rp * D) : nullptr;
+    char* kv = (char*)d->kv + s * slot_kv * esz;
+    // QKV
+    {
+      ProQKV pro;
+      pro.x = xin_slot; pro.x0 = x0;
+      pro.skip = S.skip_src >= 0 ? w.X0 + (S.skip_src + 1) * Rp * D : nullptr;
+      pro.skip_w = S.skip_src >= 0 ? d->skip_weights + (int64_t)S.skip_idx * D : nullptr;
+      pro.skip_g = (S.skip_src >= 0 && (d->flags & ALTXS_F_SKIP_GATES) && d->skip_gates)
+                       ? d->skip_gates + (int64_t)S.skip_idx * D : nullptr;
+      pro.mix = L.resid_mix; pro.base_out = w.XIN;
+      pro.gate_w = (d->flags & ALTXS_F_SPARSE_GATE) ? L.attn_gate_w : nullptr;
+      pro.gate_out = w.GATE; pro.ln_scale = L.ln_scale; pro.eps = d->norm_eps;
+      pro.gate_scale = d->gate_scale; pro.D = d->D; pro.H = d->H; pro.gw = d->gate_window;
+      pro.parallel = par ? 1 : 0;
+      EpiQKV epi;
+      epi.q = w.Q; epi.kv = kv; epi.kv_bf16 = d->kv_bf16; epi.H = d->H; epi.Hkv = d->Hkv;
+      epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = d->pos;
+      epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
+      epi.err = d->err;
+      if ((e = launch_qgemm_bits<AM>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+        return e;
+    }
+    // attention
+    {
+      AltxsAttnArgs a;
+      memset(&a, 0, sizeof(a));
+      a.B = d->B; a.W = d->W; a.H = d->H; a.Hkv = d->Hkv; a.head_dim = HD; a.max_len = d->max_len;
+      a.kv_bf16 = d->kv_bf16; a.y_bf16 = hb16; a.q = w.Q;
+      a.k = kv; a.v = kv + (int64_t)d->Hkv * d->max_len * HD * esz;
+      a.kv_seg_stride = 2ll * d->Hkv * d->max_len * HD; a.pos = d->pos;
+      a.gate = (d->flags & ALTXS_F_SPARSE_GATE) ? w.GATE : nullptr;
+      a.use_xsa = L.use_xsa; a.y = w.Y; a.err = d->err;
+      hipEvent_t* ev = (hipEvent_t*)d->attn_events;
+      if (ev && (e = hipEventRecord(ev[2 * s], st)) != hipSuccess) return e;
+      if ((e = altxs_launch_attn(a, st)) != hipSuccess) return e;
+      if (ev && (e = hipEventRecord(ev[2 * s + 1], st)) != hipSuccess) return e;
+    }
+    // out-projection + attention residual
+    {
+      ProLoad pro{w.Y, xdt, 0};
+      EpiO epi{w.XIN, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
+      if ((e = launch_qgemm_bits<AM>(L.o.bits, qt_of(L.o), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+        return e;
+    }
+    // MLP up + LeakyReLU(0.5)^2
+    {
+      ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
+      EpiUp epi{w.HB, d->F, hb16};
+      if ((e = launch_qgemm_bits<AM>(L.up.bits, qt_of(L.up), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+        return e;
+    }
+    // MLP down + residual / lanes
+    {
+      ProLoad pro{w.HB, xdt, 0};
+      EpiDown epi;
+      epi.xout = w.XOUT; epi.mlp_scale = L.mlp_scale;
+      epi.out0 = w.X0 + (s + 1) * Rp * D; epi.out1 = w.X1 + (s + 1) * Rp * D;
+      epi.lane0 = w.XIN; epi.lane1 = lane1_in; epi.pr = L.par_resid; epi.pp = L.par_post;
+      epi.D = d->D; epi.parallel = par ? 1 : 0;
+      if ((e = launch_qgemm_bits<AM>(L.down.bits, qt_of(L.down), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+        return e;
+    }
+  }
+  // final norm + LM head + softcap
+  {
+    const int n = d->n_slots;
+    bool any_par = false;
+    for (int s = 0; s < n; ++s) any_par |= d->slots[s].kind == ALTXS_SLOT_PAR;
+    const float* xf = w.X0 + n * Rp * D;
+    const float* x2 = nullptr;
+    int mode = 0;
+    if (any_par) {
+      if (d->flags & ALTXS_F_FINAL_MLP) xf = w.X1 + n * Rp * D;
+      else if (!(d->flags & ALTXS_F_FINAL_ATTN)) { x2 = w.X1 + n * Rp * D; mode = 1; }
+    }
+    ProNorm pro{xf, x2, mode, 1.0f, d->norm_eps, d->D};
+    EpiLogits epi{d->logits, d->V, (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap,
+                  d->softcap_pn};
+    if ((e = launch_qgemm_bits<AM>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+      return e;
+  }
+  if (d->probs || d->cum) {
+    const int fl = (d->flags & ALTXS_F_RENORM) ? ALTXS_CDF_RENORM : 0;
+    if ((e = altxs_launch_cdf(d->logits, R, d->V, fl, true, d->probs, d->cum, st)) != hipSuccess)
+      return e;
+  }
+  if (d->flags & ALTXS_F_COMMIT) {
+    hipLaunchKernelGGL(commit_kernel, dim3(d->B), dim3(256), 0, st, d->pos, d->prev_raw,
+                       (const float*)d->cand_raw, d->B, d->D, d->W);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int64_t altxs_step_workspace_bytes(const AltxsStepDesc* d) {
+  if (!d) return -1;
+  return carve(d, nullptr, nullptr);
+}
+
+extern "C" int32_t altxs_step(const AltxsStepDesc* d, altxs_stream_t stream) {
+  int rc = validate(d);
+  if (rc) return rc;
+  WS w;
+  carve(d, &w, (char*)d->ws);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = d->act_bf16 ? run_step<A_BF16>(d, w, st) : run_step<A_F32>(d, w, st);
+  ALTXS_CHECK_HIP(e);
+  return ALTXS_OK;
+}

@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""Scored symbols/sec of the altxs per-symbol step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload ("cfg3"): a ~40M-weight GPT (10 layers, d=512,
+8 heads MHA of 64, FFN 2048, V=16384, mixed 2/3/4/6-bit group-64 weights at
+~3.16 bpw) scoring one symbol for each of 64 independent segments whose KV
+caches hold 2047 previous tokens, so every attention row reads 2048 keys.  A
+step = embedding -> 10 slots -> LM head -> softmax -> integer CDFs for all 64
+segments; ``value`` = 64 / step time.  The KV cache is filled with N(0, 1)
+bf16 values (the scale of QK-RMS-normalised keys) and the step runs at a
+fixed position, overwriting the same cache row, so each step moves the same
+bytes.  Weights are seeded N(0, 0.02^2) then quantised; tokens are Zipf(1.1).
+
+The line also carries:
+* ``roofline``: the decode-attention kernel (the dominant one), algorithmic
+  bytes per launch / its mean launch duration, timed with HIP events recorded
+  on the step's stream around every attention launch of the timed steps;
+* ``step_roofline``: algorithmic bytes of the whole step / step time;
+* ``cpu_baseline``: the CPU oracle (op-for-op fp32 PyTorch restatement of the
+  reference eager step, B=1 per segment as the reference runs) timed on this
+  host on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+METRIC = "scored symbols/sec @32M mixed-3.15bpw, 64 segs ctx2048; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic_<kernel>.txt)."""
+    path = os.path.join(HERE, "profiles", f"traffic_{kernel}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path, encoding="utf8"):
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split("=")[1].split()[0])
+    return None
+
+
+def cpu_baseline(sm, ctx: int, seconds: float, seed: int = 0) -> dict:
+    """Time the CPU oracle on single-segment decode steps at context ``ctx``."""
+    import numpy as np
+    import torch
+
+    from altxs_amd import synth
+    from oracle.model_ref import OracleModel
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    om = OracleModel(sm.cfg, sm.state_dict(), act="fp32", max_len=ctx)
+    st = om.new_state(ctx)
+    g = torch.Generator().manual_seed(seed)
+    for s in range(om.n_slots):
+        st.k[s].normal_(generator=g)
+        st.v[s].normal_(generator=g)
+    toks = synth.zipf_tokens(sm.cfg.vocab_size, (4096,), seed=seed + 1)
+    om.step(st, [int(toks[0])])  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        st.pos = ctx - 1
+        om.step(st, [int(toks[n % len(toks)])])
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 8) or n >= 100000:
+            break
+    return {"value": n / el, "unit": "sym/s", "cores": cores, "kind": "port",
+            "sample": f"{n} single-segment decode steps at ctx {ctx} (fp32 oracle, B=1, "
+                      f"{el:.1f} s, torch threads={cores})"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--profile", default="cfg3")
+    ap.add_argument("--segments", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--act", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--kv", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU only (independent segments shard across GPUs "
+              "with no communication; see DESIGN.md); --gpus must be 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from altxs_amd import hiprt, synth
+    from altxs_amd.config import make_config
+    from altxs_amd.model import StepModel
+
+    B, ctx = a.segments, a.ctx
+    max_len = (ctx + 255) // 256 * 256
+    cfg = make_config(a.profile)
+    t0 = time.time()
+    sm = synth.make_model(cfg)
+    log(f"model {a.profile}: {sm.bits_summary()['bpw']:.4f} bpw, built in {time.time() - t0:.1f}s")
+    model = StepModel(sm, act=a.act, kv=a.kv)
+    st = model.make_static_state(max_len, win=1, batch=B, want_probs=False, want_cdf=True)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    st.kv.normal_(generator=g)
+    st.pos.fill_(ctx - 1)
+    st.token.copy_(torch.from_numpy(synth.zipf_tokens(cfg.vocab_size, (B, 1)).astype(np.int32)))
+    torch.cuda.synchronize()
+
+    for _ in range(a.warmup):
+        model.step(st)
+    torch.cuda.synchronize()
+    st.check_errors()
+    log(f"warmup done ({a.warmup} steps)")
+
+    graph = None
+    if not a.no_graph:
+        try:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                model.step(st)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+        except Exception as exc:  # noqa: BLE001
+            log(f"graph capture failed ({exc!r}); timing eager launches")
+            graph = None
+
+    # ---- timed region: exactly K steps -------------------------------------
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(a.steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            model.step(st)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / a.steps
+    st.check_errors()
+    log(f"timed {a.steps} steps ({'graph' if graph is not None else 'eager'}): {ms:.3f} ms/step")
+
+    # ---- dominant kernel: HIP events around every attention launch ----------
+    n_slots = model.n_slots
+    ev = hiprt.EventArray(2 * n_slots * a.steps)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s0.record()
+    for k in range(a.steps):
+        model.step(st, attn_events=ev.ptr + k * 2 * n_slots * 8)
+    s1.record()
+    torch.cuda.synchronize()
+    eager_ms = s0.elapsed_time(s1) / a.steps
+    durs = [ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(n_slots * a.steps)]
+    ev.close()
+    attn_ms = float(np.mean(durs))
+    kvb = 2 if a.kv == "bf16" else 4
+    ab = synth.algorithmic_step_bytes(sm, B, ctx, kv_bytes=kvb)
+    ybytes = 2 if a.act == "bf16" else 4
+    attn_bytes = (ab["kv_read"] // ab["n_slots"] + B * cfg.num_heads * cfg.head_dim * (4 + ybytes)
+                  + B * cfg.num_heads * 4)
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    step_gbs = ab["total"] / (ms * 1e-3) / 1e9
+    log(f"attention: {attn_ms * 1e3:.1f} us/launch, {achieved:.0f} GB/s; eager step {eager_ms:.3f} ms; "
+        f"step {step_gbs:.0f} GB/s of algorithmic traffic")
+
+    cpu = None
+    if not a.no_cpu:
+        log(f"cpu baseline (~{a.cpu_seconds:.0f}s)")
+        cpu = cpu_baseline(sm, ctx, a.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']:.1f} sym/s on {cpu['cores']} cores")
+
+    value = B / (ms * 1e-3)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "sym/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": a.kv if a.act == a.kv else f"{a.act}-act/{a.kv}-kv",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{a.profile} decode step: {B} segments x 1 symbol, ctx {ctx}, "
+                         f"{cfg.num_layers} layers d={cfg.model_dim} H={cfg.num_heads} "
+                         f"FFN={cfg.hidden_dim} V={cfg.vocab_size}, "
+                         f"{sm.bits_summary()['bpw']:.3f} bpw group-64 weights, "
+                         f"{a.act} activations, {a.kv} KV"),
+            "segments": B, "ctx": ctx, "timing": "hip-graph" if graph is not None else "eager",
+            "eager_ms_per_step": round(eager_ms, 4),
+        },
+        "roofline": {
+            "kernel": "attn_kernel (decode attention)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic("attn"),
+            "bytes_per_launch": int(attn_bytes),
+            "us_per_launch": round(attn_ms * 1e3, 2),
+        },
+        "step_roofline": {
+            "algorithmic_bytes": int(ab["total"]),
+            "achieved": round(step_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,241 @@
+/*
+ * altxs.h -- C-ABI of libaltxs_hip.so, the MI355X (gfx950) implementation of
+ * the altxs per-symbol model step.
+ *
+ * All pointers are device pointers unless stated otherwise; sizes are element
+ * counts.  Every entry point enqueues work on `stream` (a hipStream_t passed as
+ * void*; NULL = the legacy default stream), never synchronises, never
+ * allocates, and returns ALTXS_OK (0) or a negative ALTXS_ERR_* code.  The
+ * message for the last failure on the calling thread is altxs_last_error().
+ * Runtime values that live in device memory (positions, token ids) cannot be
+ * checked on the host; kernels skip out-of-range accesses and OR a code into
+ * the caller's device error word instead of faulting.
+ *
+ * Reference citations are path:line into altvectra/altxs.
+ */
+#ifndef ALTXS_H
+#define ALTXS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ALTXS_ABI_VERSION 1
+
+enum {
+  ALTXS_OK = 0,
+  ALTXS_ERR_ARG = -1,         /* bad shape / pointer / unsupported combination */
+  ALTXS_ERR_HIP = -2,         /* a HIP runtime call failed */
+  ALTXS_ERR_UNSUPPORTED = -3, /* feature not built */
+};
+
+/* dtype codes for activation inputs */
+enum { ALTXS_F32 = 0, ALTXS_BF16 = 1, ALTXS_F16 = 2 };
+
+typedef void *altxs_stream_t;
+
+/* ABI version of the loaded library (== ALTXS_ABI_VERSION). */
+int32_t altxs_abi_version(void);
+
+/* Message for the last error returned on this thread ("" if none). */
+const char *altxs_last_error(void);
+
+/*
+ * Packed mixed-bit weight tensor W[N, K]: symmetric group-64 quantisation
+ * along K, w[n,k] = (code[n,k] - (2^bits - 1)/2) * scale[n, k/64], fp16 scales,
+ * bits in {2,3,4,6} per tensor.  The math is the reference's "symmetric"
+ * codebook mode (src/hyperflow_distillation/mixed_bit_delta.py:147-152,
+ * 172-229) with the channel width set to a 64-wide group and b = 6 added.
+ * Storage is the MFMA-tiled layout produced by altxs_amd.codec.pack_tiled:
+ * 16-row x 256-column blocks; in each block every lane of a wave owns the
+ * codes its v_mfma_f32_16x16x32 B operand needs, split into 4/2/1-bit planes
+ * so each lane reads whole 16/8-byte words.  N % 16 == 0, K % 256 == 0.
+ */
+typedef struct AltxsQTensor {
+  const void *codes;  /* uint8 planes, N*K*bits/8 bytes */
+  const void *scales; /* fp16, N*K/64 entries (tiled) */
+  int64_t N, K;
+  int32_t bits;
+  int32_t reserved;
+} AltxsQTensor;
+
+/*
+ * probs[rows, V] (fp32) -> cum[rows, V+1] (uint32): f_i = max(1,
+ * floor(double(p_i) * 1e6 + 0.5)) with two IEEE double roundings and no FMA,
+ * cum_0 = 0, cum_{i+1} = cum_i + f_i.  Bit-exact with _scale_cum_np
+ * (src/model/arithmetic_coder_lm.py:49-64) and the GPU coder's scale_p
+ * (src/xsa_ttt/gpu_ac.py:38-42).  Requires V <= 65536.
+ */
+int32_t altxs_scale_cum(const float *probs, int64_t rows, int64_t V, uint32_t *cum,
+                        altxs_stream_t stream);
+
+#define ALTXS_CDF_RENORM 1 /* p /= sum(p) after the softmax (compress.py:78-83) */
+
+/*
+ * Deterministic softmax + CDF: probs = softmax(logits) in fp32 with a fixed
+ * reduction order (independent of `rows`), then cum as altxs_scale_cum.
+ * Replaces torch.softmax(state.logits, -1, out=probs_dev)
+ * (src/xsa_ttt/incremental.py:603-605, 627-633) followed by _scale_cum_np.
+ * probs or cum may be NULL.  Requires V <= 65536.
+ */
+int32_t altxs_softmax_cdf(const float *logits, int64_t rows, int64_t V, int32_t flags,
+                          float *probs, uint32_t *cum, altxs_stream_t stream);
+
+/* Dense fp32 copy of a packed tensor: out[N, K].  Replaces dequantize_channels
+ * (mixed_bit_delta.py:172-229) for the group-64 format. */
+int32_t altxs_dequant(const AltxsQTensor *w, float *out, altxs_stream_t stream);
+
+/*
+ * y[rows, N] = x[rows, K] . W^T with the dequantisation fused into an MFMA
+ * GEMM (fp32 accumulate).  x_dtype: ALTXS_F16 / ALTXS_BF16 (one MFMA pass) or
+ * ALTXS_F32 (three-way bf16 split of x, fp32-faithful).  Row results do not
+ * depend on `rows` (batch-invariant).  Replaces gemv_rows(x, w, out)
+ * (src/xsa_ttt/ac_gemv.py:391-420) and F.linear in _projection_linear
+ * (src/xsa_ttt/model.py:93-111).
+ */
+int32_t altxs_qgemm(const AltxsQTensor *w, const void *x, int32_t x_dtype, int64_t rows,
+                    float *y, altxs_stream_t stream);
+
+/*
+ * The same GEMM over `count` tensors of one shape and bit width laid out at a
+ * fixed byte stride (codes_stride, scales_stride bytes) from w->codes /
+ * w->scales; y is [count, rows, N].  One launch streams all of them; it is the
+ * HBM microbenchmark form of altxs_qgemm (no reference counterpart).
+ */
+int32_t altxs_qgemm_stream(const AltxsQTensor *w, int64_t count, int64_t codes_stride,
+                           int64_t scales_stride, const void *x, int32_t x_dtype,
+                           int64_t rows, float *y, altxs_stream_t stream);
+
+/*
+ * Decode attention over a KV cache.  For row r = b*W + t the query sits at
+ * position p = pos[b] + t and attends to keys [0, p] of segment b.  Keys are
+ * scanned in fixed 256-key chunks and merged left to right, so a row's result
+ * does not depend on B or W.  Replaces run_split_attn (split_attn.py:341-425)
+ * and the eager _static_window_attention (model.py:550-585).
+ */
+typedef struct AltxsAttnArgs {
+  int32_t B, W, H, Hkv, head_dim, max_len;
+  int32_t kv_bf16;  /* KV element type: 0 fp32, 1 bf16 */
+  int32_t y_bf16;   /* output element type: 0 fp32, 1 bf16 */
+  const float *q;   /* [B*W, H, head_dim] fp32 */
+  const void *k;    /* [B, Hkv, max_len, head_dim], seg stride kv_seg_stride elems */
+  const void *v;
+  int64_t kv_seg_stride; /* elements between segments (both K and V) */
+  const int32_t *pos;    /* [B] */
+  const float *gate;     /* [B*W, H] multiplier (sparse attention gate) or NULL */
+  int32_t use_xsa;       /* subtract the current value direction (model.py:760-768) */
+  int32_t reserved;
+  void *y;               /* [B*W, H*head_dim] */
+  int32_t *err;          /* device error word or NULL */
+} AltxsAttnArgs;
+
+int32_t altxs_decode_attn(const AltxsAttnArgs *a, altxs_stream_t stream);
+
+/* ---- the whole per-symbol step ------------------------------------------ */
+
+#define ALTXS_MAX_LAYERS 32
+#define ALTXS_MAX_SLOTS 64
+
+enum {
+  ALTXS_F_SMEAR = 1 << 0,       /* SmearGate on the embedding (model.py:1559-1579) */
+  ALTXS_F_SPARSE_GATE = 1 << 1, /* sparse attention gate (model.py:854-862) */
+  ALTXS_F_SKIP_GATES = 1 << 2,  /* gated U-Net skips (model.py:1275-1291) */
+  ALTXS_F_ASYM_SOFTCAP = 1 << 3,/* asymmetric tanh softcap (model.py:1478-1493) */
+  ALTXS_F_COMMIT = 1 << 4,      /* after the step: pos += W, prev_raw = last raw */
+  ALTXS_F_RENORM = 1 << 5,      /* renormalise probs before the CDF */
+  ALTXS_F_FINAL_ATTN = 1 << 6,  /* parallel_final_lane = "attn" (default mean) */
+  ALTXS_F_FINAL_MLP = 1 << 7,   /* parallel_final_lane = "mlp" */
+};
+
+enum { ALTXS_SLOT_SEQ = 0, ALTXS_SLOT_PAR = 1 };
+
+typedef struct AltxsLayer {
+  AltxsQTensor qkv;          /* [(H + 2*Hkv)*head_dim, D]: q rows, k rows, v rows */
+  AltxsQTensor o;            /* [D, D] */
+  AltxsQTensor up;           /* [F, D] */
+  AltxsQTensor down;         /* [D, F] */
+  const float *resid_mix;    /* [2, D] */
+  const float *attn_scale;   /* [D] */
+  const float *mlp_scale;    /* [D] */
+  const float *q_gain;       /* [H] */
+  const float *attn_gate_w;  /* [H, gate_window] or NULL */
+  const float *par_resid;    /* [2] parallel_resid_lambdas[layer] or NULL */
+  const float *par_post;     /* [2, 2] parallel_post_lambdas[layer] or NULL */
+  const uint16_t *lora_q_a;  /* LoRA (fp16) A [rank, D], B [H*hd, rank]; NULL = off */
+  const uint16_t *lora_q_b;
+  const uint16_t *lora_v_a;  /* A [rank, D], B [Hkv*hd, rank] */
+  const uint16_t *lora_v_b;
+  float lora_scale;
+  float ln_scale;            /* 1/sqrt(layer+1) with ln_scale, else 1 */
+  int32_t use_xsa;
+  int32_t reserved;
+} AltxsLayer;
+
+typedef struct AltxsSlot {
+  int32_t layer;
+  int32_t kind;            /* ALTXS_SLOT_SEQ / ALTXS_SLOT_PAR */
+  int32_t skip_idx;        /* decoder skip weight row, -1 = none */
+  int32_t skip_src;        /* slot whose output is popped, -1 = none */
+  int32_t first_parallel;  /* first parallel slot: both lanes start from x */
+  int32_t reserved;
+} AltxsSlot;
+
+typedef struct AltxsStepDesc {
+  int32_t abi_version;
+  int32_t B, W, D, H, Hkv, head_dim, F, V;
+  int32_t n_layers, n_slots, max_len, gate_window, rope_dims, lora_rank;
+  int32_t act_bf16; /* 0: fp32 activations (3-way split MFMA), 1: bf16 */
+  int32_t kv_bf16;  /* 0: fp32 KV cache, 1: bf16 */
+  int32_t flags;    /* ALTXS_F_* */
+  float norm_eps, gate_scale, logit_softcap;
+  AltxsLayer layers[ALTXS_MAX_LAYERS];
+  AltxsSlot slots[ALTXS_MAX_SLOTS];
+  AltxsQTensor emb;          /* tied embedding / LM head [V, D] */
+  const float *skip_weights; /* [n_skip, D] */
+  const float *skip_gates;   /* [n_skip, D] or NULL */
+  const float *smear_w;      /* [gate_window] */
+  const float *smear_lambda; /* [1] */
+  const float *softcap_pn;   /* [2] = (softcap_pos, softcap_neg) */
+  const float *rope_cos;     /* [max_len, rope_dims/2] fp32 */
+  const float *rope_sin;
+  /* caller-owned state */
+  const int32_t *tokens; /* [B, W] */
+  int32_t *pos;          /* [B] window start position of each segment */
+  float *prev_raw;       /* [B, D] raw embedding of each segment's previous token */
+  float *cand_raw;       /* [B, D] raw embedding of the window's last token */
+  void *kv;              /* [n_slots, B, 2, Hkv, max_len, head_dim] */
+  void *ws;              /* workspace, altxs_step_workspace_bytes() bytes */
+  int64_t ws_bytes;
+  float *logits;         /* [B*W, V] */
+  float *probs;          /* [B*W, V] or NULL */
+  uint32_t *cum;         /* [B*W, V+1] or NULL */
+  int32_t *err;          /* [1] device error word */
+  /* Optional timing hook: NULL, or 2*n_slots hipEvent_t handles; events 2s and
+   * 2s+1 are recorded on `stream` right before and after slot s's attention
+   * launch (the dominant kernel), so a caller can time it on its own stream. */
+  void **attn_events;
+} AltxsStepDesc;
+
+/* Workspace bytes altxs_step needs for this descriptor (host-only). */
+int64_t altxs_step_workspace_bytes(const AltxsStepDesc *d);
+
+/*
+ * One W-token step for B independent segments: embedding (+smear), every slot
+ * (QKV + QK-RMS + RoPE + KV write, attention, out-projection + residual,
+ * RMSNorm/MLP), final norm, LM head + softcap, softmax and integer CDFs.
+ * K/V rows are written at pos[b] + t.  W = 1 is the decode row; W > 1 is the
+ * teacher-forced encode window; per-row results are identical for the same
+ * prefix.  Replaces try_persistent_extend(model, state)
+ * (src/xsa_ttt/persistent_step.py:1081), try_mega_encode(model, state)
+ * (src/xsa_ttt/mega_encode.py:1693) and GPT.static_extend
+ * (src/xsa_ttt/model.py:1617-1781), plus the softmax that follows
+ * (incremental.py:603-633).
+ */
+int32_t altxs_step(const AltxsStepDesc *d, altxs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ALTXS_H */

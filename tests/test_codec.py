@@ -1,0 +1,115 @@
+"""Mixed-bit codec: reference per-channel arithmetic KATs and the group-64 tiled format."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from altxs_amd import codec
+from oracle import codec_ref
+
+REF_WEIGHTS = "/root/reference/weights/mixed_da_bpw3.15_upb1.8"
+
+
+def test_unpack_codes_known_answers():
+    # 2-bit: 0b11_10_01_00 -> [0, 1, 2, 3] (LSB first)
+    assert list(codec_ref.unpack_codes(np.array([0b11100100], np.uint8), 2, 4)) == [0, 1, 2, 3]
+    # 4-bit: 0x21 -> [1, 2]
+    assert list(codec_ref.unpack_codes(np.array([0x21], np.uint8), 4, 2)) == [1, 2]
+    # 3-bit: codes 0..7 in one little-endian 24-bit word
+    word = sum(c << (3 * c) for c in range(8))
+    b = np.array([word & 255, (word >> 8) & 255, (word >> 16) & 255], np.uint8)
+    assert list(codec_ref.unpack_codes(b, 3, 8)) == list(range(8))
+    with pytest.raises(ValueError):
+        codec_ref.unpack_codes(b, 6, 8)
+
+
+def test_symmetric_levels_closed_form():
+    lv = codec_ref.symmetric_levels(np.array([0.5], np.float16), 3)
+    assert np.allclose(lv[0], (np.arange(8) - 3.5) * 0.5)
+
+
+def test_fp4_table():
+    t = codec_ref.fp4_e2m1()
+    assert list(t[:8]) == [0, 0.5, 1, 1.5, 2, 3, 4, 6]
+    assert np.array_equal(t[8:], -t[:8])
+
+
+@pytest.mark.parametrize("bits", codec.BITS)
+def test_quantize_roundtrip_error(bits):
+    rng = np.random.default_rng(bits)
+    w = rng.standard_normal((32, 512)).astype(np.float32) * 0.02
+    codes, scales = codec.quantize_group64(w, bits)
+    deq = codec_ref.dequant_group64(codes, scales, bits)
+    s = np.repeat(scales.astype(np.float32), 64, axis=1)
+    assert np.all(np.abs(deq - w) <= 0.5 * s * (1 + 1e-3) + 1e-7)
+    assert codes.max() <= 2 ** bits - 1
+    assert np.array_equal(deq, codec.dequantize_group64(codes, scales, bits))
+
+
+@pytest.mark.parametrize("bits", codec.BITS)
+@pytest.mark.parametrize("shape", [(16, 256), (48, 512), (32, 2048)])
+def test_tiled_layout_roundtrip(bits, shape):
+    rng = np.random.default_rng(1)
+    n, k = shape
+    codes = rng.integers(0, 2 ** bits, size=(n, k)).astype(np.uint8)
+    scales = rng.standard_normal((n, k // 64)).astype(np.float16)
+    tiled, tsc = codec.pack_tiled(codes, scales, bits)
+    assert tiled.size == n * k * bits // 8
+    c2, s2 = codec.unpack_tiled(tiled, tsc, n, k, bits)
+    assert np.array_equal(c2, codes) and np.array_equal(s2.view(np.uint16), scales.view(np.uint16))
+    # independent element-by-element reader of the layout description
+    c3, s3 = codec_ref.unpack_tiled(tiled, tsc, n, k, bits)
+    assert np.array_equal(c3, codes) and np.array_equal(s3.view(np.uint16), scales.view(np.uint16))
+
+
+def test_tiled_lane_ownership():
+    """Lane l of block (0,0) owns row l%16, columns 32s + 8(l//16) + i (s, i < 8)."""
+    n, k, bits = 16, 256, 4
+    codes = np.zeros((n, k), np.uint8)
+    codes[5, 32 * 3 + 8 * 2 + 7] = 9  # lane 5 + 16*2 = 37, k-step 3, i = 7
+    tiled, _ = codec.pack_tiled(codes, np.ones((n, k // 64), np.float16), bits)
+    lane_bytes = tiled.reshape(64, 32)
+    nz = np.nonzero(lane_bytes)
+    assert list(nz[0]) == [37]
+    word = lane_bytes[37].view("<u4")
+    assert word[3] == 9 << 28  # k-step 3 -> word 3, code i=7 -> bits 28..31
+
+
+def test_allocate_bits_hits_budget():
+    from altxs_amd.config import make_config
+    from altxs_amd.synth import tensor_list
+
+    cfg = make_config("cfg3")
+    sizes = [(nm, n * k) for nm, n, k in tensor_list(cfg)]
+    bits = codec.allocate_bits(sizes, 3.15)
+    mean = sum(bits[nm] * n for nm, n in sizes) / sum(n for _, n in sizes)
+    assert abs(mean - 3.15) < 0.01
+    assert set(bits.values()) == {2, 3, 4, 6}
+
+
+@pytest.mark.skipif(not os.path.exists(REF_WEIGHTS + ".json"), reason="reference asset absent")
+def test_shipped_asset_sizes_match_closed_forms():
+    """The shipped codec's packed tensors have the byte sizes the layout implies."""
+    from safetensors.numpy import load_file
+
+    meta = json.load(open(REF_WEIGHTS + ".json", encoding="utf8"))
+    st = load_file(REF_WEIGHTS + ".safetensors")
+    for name, layout in meta["layouts"].items():
+        bits = st[f"bits/{name}"]
+        width = int(layout["channel_width"])
+        for b in (2, 3, 4):
+            nch = int((bits == b).sum())
+            key = f"packed/{name}/b{b}"
+            if key in st:
+                assert st[key].size == nch * width * b // 8, key
+        # decode the whole bank with the oracle (lloyd codebooks) -> finite values
+        cbs = {b: st.get(f"codebook/{name}/b{b}", np.empty((0, 1 << b), np.float16)) for b in (2, 3, 4)}
+        pk = {b: st.get(f"packed/{name}/b{b}", np.zeros(0, np.uint8)) for b in (2, 3, 4)}
+        ch = codec_ref.dequantize_channels(bits, cbs, pk, channel_width=width,
+                                           mode=meta.get("codebook_mode", "lloyd"))
+        assert ch.shape == (bits.size, width) and np.isfinite(ch).all()
+        assert np.all(ch[bits == 0] == 0)

@@ -1,0 +1,228 @@
+"""GPU parity of the standalone kernels (through the C-ABI) against the CPU oracle."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _log(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+# ---------------------------------------------------------------- CDF ----------
+
+def _adversarial_rows(V: int, rng) -> np.ndarray:
+    rows = []
+    rows.append(np.full(V, 1.0 / V, np.float32))
+    r = np.zeros(V, np.float32)
+    r[V // 3] = 1.0
+    rows.append(r)
+    # values straddling the (k - 1/2) * 1e-6 rounding boundaries
+    ks = rng.integers(1, 5000, V)
+    r = ((ks - 0.5) * 1e-6).astype(np.float32)
+    r = np.nextafter(r, np.where(rng.random(V) < 0.5, 0, 1).astype(np.float32))
+    rows.append(r)
+    rows.append(np.full(V, 1e-40, np.float32))  # denormals
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("V", [256, 4096, 16384, 65536])
+def test_scale_cum_bit_exact(V):
+    from altxs_amd import ops
+    from oracle import coder
+
+    _log(f"scale_cum V={V}")
+    rng = np.random.default_rng(V)
+    lg = rng.standard_normal((37, V)).astype(np.float32) * 3
+    p = np.exp(lg - lg.max(1, keepdims=True))
+    p = (p / p.sum(1, keepdims=True)).astype(np.float32)
+    p = np.concatenate([p, _adversarial_rows(V, rng)])
+    got = ops.scale_cum(torch.from_numpy(p).to(DEV)).cpu().numpy().astype(np.int64)
+    torch.cuda.synchronize()
+    assert np.array_equal(got, coder.scale_cum(p))
+
+
+@pytest.mark.parametrize("V", [256, 4096, 16384])
+def test_softmax_cdf_matches_torch_and_is_batch_invariant(V):
+    from altxs_amd import ops
+    from oracle import coder
+
+    _log(f"softmax_cdf V={V}")
+    rng = np.random.default_rng(1)
+    lg = torch.from_numpy(rng.standard_normal((64, V)).astype(np.float32) * 4).to(DEV)
+    probs, cum = ops.softmax_cdf(lg)
+    ref = torch.softmax(lg.double().cpu(), -1)
+    assert (probs.double().cpu() - ref).abs().max() < 1e-6 * max(1.0, float(ref.max()))
+    # the CDF is exactly the count rule on the kernel's own probabilities
+    assert np.array_equal(cum.cpu().numpy().astype(np.int64), coder.scale_cum(probs.cpu().numpy()))
+    # a row alone gives the same bits as inside a batch, and reruns agree
+    for r in (0, 17, 63):
+        p1, c1 = ops.softmax_cdf(lg[r:r + 1].contiguous())
+        assert torch.equal(p1[0], probs[r]) and torch.equal(c1[0], cum[r])
+    p2, c2 = ops.softmax_cdf(lg)
+    assert torch.equal(p2, probs) and torch.equal(c2, cum)
+    # renormalised mode sums to one
+    pr, _ = ops.softmax_cdf(lg, renorm=True, want_cdf=False)
+    assert (pr.double().sum(-1) - 1).abs().max() < 1e-5
+
+
+# --------------------------------------------------------------- GEMM ----------
+
+def _packed(bits, n, k, seed, std=0.02):
+    from altxs_amd.codec import PackedTensor
+
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((n, k)).astype(np.float32) * std
+    return PackedTensor.from_dense("w", w, bits)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6])
+@pytest.mark.parametrize("shape", [(512, 2048), (2048, 512)])
+def test_dequant_bit_exact(bits, shape):
+    from altxs_amd import ops
+    from oracle import codec_ref
+
+    _log(f"dequant bits={bits} shape={shape}")
+    p = _packed(bits, *shape, seed=bits)
+    w = ops.DeviceQTensor(p)
+    got = ops.dequant(w).cpu().numpy()
+    want = codec_ref.dequant_group64(p.codes, p.scales, bits)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6])
+@pytest.mark.parametrize("shape", [(512, 2048), (2048, 512)])
+@pytest.mark.parametrize("B", [1, 64])
+@pytest.mark.parametrize("xdt", ["f16", "bf16", "f32"])
+def test_qgemm_against_fp32_matmul(bits, shape, B, xdt):
+    from altxs_amd import ops
+    from oracle import codec_ref
+
+    _log(f"qgemm bits={bits} shape={shape} B={B} x={xdt}")
+    n, k = shape
+    p = _packed(bits, n, k, seed=10 + bits)
+    w = ops.DeviceQTensor(p)
+    rng = np.random.default_rng(B)
+    x32 = torch.from_numpy(rng.standard_normal((B, k)).astype(np.float32))
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[xdt]
+    x = x32.to(dt)
+    y = ops.qgemm(w, x.to(DEV).contiguous()).cpu().double()
+    wd = torch.from_numpy(codec_ref.dequant_group64(p.codes, p.scales, bits)).double()
+    ref = x.double() @ wd.T
+    err = (y - ref).abs().max().item()
+    assert err < 1e-3, err  # fp32 accumulation of exact products
+    assert err < 1e-5 * max(1.0, ref.abs().max().item()) * math.sqrt(k)
+
+
+def test_qgemm_batch_invariant():
+    from altxs_amd import ops
+
+    _log("qgemm batch invariance")
+    p = _packed(3, 2048, 512, seed=3)
+    w = ops.DeviceQTensor(p)
+    x = torch.randn(64, 512, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(DEV)
+    y64 = ops.qgemm(w, x)
+    for r in (0, 5, 31, 63):
+        y1 = ops.qgemm(w, x[r:r + 1].contiguous())
+        assert torch.equal(y1[0], y64[r])
+    y17 = ops.qgemm(w, x[:17].contiguous())
+    assert torch.equal(y17, y64[:17])
+
+
+def test_qgemm_stream_matches_single():
+    from altxs_amd import ops
+
+    _log("qgemm_stream")
+    count, n, k, bits = 5, 512, 2048, 3
+    ps = [_packed(bits, n, k, seed=100 + i) for i in range(count)]
+    cs, ss = ps[0].tiled.size, ps[0].tiled_scales.size * 2
+    codes = torch.from_numpy(np.concatenate([p.tiled for p in ps])).to(DEV)
+    scales = torch.from_numpy(np.concatenate([p.tiled_scales for p in ps]).view(np.int16)).to(DEV)
+    x = torch.randn(3, k).to(torch.float16).to(DEV)
+    out = torch.empty(count, 3, n, device=DEV)
+    ops.qgemm_stream(codes, scales, count, n, k, bits, cs, ss, x, out)
+    for i, p in enumerate(ps):
+        assert torch.equal(out[i], ops.qgemm(ops.DeviceQTensor(p), x))
+
+
+# ---------------------------------------------------------- attention ----------
+
+def _attn_ref(q, k, v, pos, W, gate, use_xsa):
+    """fp64 reference on the (already rounded) cache values. q [R,H,64]; k/v [B,Hkv,L,64]."""
+    R, H, hd = q.shape
+    B, Hkv = k.shape[0], k.shape[1]
+    g = H // Hkv
+    out = torch.zeros(R, H, hd, dtype=torch.float64)
+    for r in range(R):
+        b, t = divmod(r, W)
+        p = int(pos[b]) + t
+        for h in range(H):
+            kk = k[b, h // g, : p + 1].double()
+            vv = v[b, h // g, : p + 1].double()
+            s = (kk @ q[r, h].double()) / 8.0
+            y = torch.softmax(s, 0) @ vv
+            if use_xsa:
+                vc = v[b, h // g, p].double()
+                vn = vc / max(vc.norm().item(), 1e-12)
+                y = y - (y @ vn) * vn
+            if gate is not None:
+                y = y * float(gate[r, h])
+            out[r, h] = y
+    return out.reshape(R, H * hd)
+
+
+@pytest.mark.parametrize("kv", ["fp32", "bf16"])
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (4, 2), (8, 2)])
+def test_decode_attention_against_reference(kv, H, Hkv):
+    from altxs_amd import ops
+
+    _log(f"attn kv={kv} H={H} Hkv={Hkv}")
+    B, W, L = 3, 2, 768
+    gen = torch.Generator().manual_seed(H * 10 + Hkv)
+    pos = torch.tensor([0, 300, 700], dtype=torch.int32)  # ragged; 700+1 < 768
+    dt = torch.bfloat16 if kv == "bf16" else torch.float32
+    k = torch.randn(B, Hkv, L, 64, generator=gen).to(dt)
+    v = torch.randn(B, Hkv, L, 64, generator=gen).to(dt)
+    q = torch.randn(B * W, H, 64, generator=gen) * 3
+    gate = torch.rand(B * W, H, generator=gen)
+    y = ops.decode_attn(q.to(DEV), k.to(DEV), v.to(DEV), pos.to(DEV), W=W, gate=gate.to(DEV),
+                        use_xsa=True)
+    ref = _attn_ref(q, k.float(), v.float(), pos, W, gate, True)
+    assert (y.cpu().double() - ref).abs().max() < 2e-5
+
+
+def test_decode_attention_window_equals_rows():
+    """Row at position p computes the same bits as W=1 and inside a W=4 window."""
+    from altxs_amd import ops
+
+    _log("attn W=4 vs W=1 bit equality")
+    B, L, H = 2, 1024, 8
+    gen = torch.Generator().manual_seed(7)
+    k = torch.randn(B, H, L, 64, generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn(B, H, L, 64, generator=gen).to(torch.bfloat16).to(DEV)
+    q = (torch.randn(B * 4, H, 64, generator=gen) * 3).to(DEV)
+    pos = torch.tensor([253, 510], dtype=torch.int32, device=DEV)  # windows cross chunk edges
+    y4 = ops.decode_attn(q, k, v, pos, W=4, use_xsa=True)
+    for t in range(4):
+        q1 = q.view(B, 4, H, 64)[:, t].contiguous()
+        y1 = ops.decode_attn(q1, k, v, pos + t, W=1, use_xsa=True)
+        assert torch.equal(y1, y4.view(B, 4, -1)[:, t])
+
+
+def test_attention_position_error_flag():
+    from altxs_amd import ops
+
+    _log("attn pos out of range -> error flag, no fault")
+    k = torch.zeros(1, 1, 256, 64, device=DEV)
+    q = torch.zeros(1, 1, 64, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.decode_attn(q, k, k.clone(), torch.tensor([999], dtype=torch.int32, device=DEV), err=err)
+    assert int(err.item()) & 1

@@ -1,0 +1,71 @@
+"""The C-ABI library loads, exports every declared symbol and matches the header layout.
+
+No compute calls: these run without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from altxs_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "altxs.h")
+
+
+def _declared() -> list[str]:
+    text = open(HEADER, encoding="utf8").read()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|int64_t|const char \*)\s*(altxs_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} missing: run `python -m altxs_amd.build`")
+    L = _lib.load()
+    declared = _declared()
+    assert set(declared) == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(L, name), name
+    assert L.altxs_abi_version() == _lib.ABI_VERSION
+    assert L.altxs_last_error() == b""
+
+
+def test_bad_arguments_return_errors_without_gpu():
+    L = _lib.load()
+    rc = L.altxs_scale_cum(None, 1, 256, None, None)
+    assert rc == -1 and b"null" in L.altxs_last_error()
+    d = _lib.StepDesc()
+    d.abi_version = 999
+    assert L.altxs_step(ctypes.byref(d), None) == -1
+    assert b"abi_version" in L.altxs_last_error()
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """sizeof/offsetof from the C compiler equal the ctypes mirror."""
+    src = tmp_path / "layout.c"
+    src.write_text(f"""
+#include <stdio.h>
+#include <stddef.h>
+#include "{HEADER}"
+int main(void) {{
+  printf("%zu %zu %zu %zu %zu\\n", sizeof(AltxsQTensor), sizeof(AltxsAttnArgs), sizeof(AltxsLayer),
+         sizeof(AltxsSlot), sizeof(AltxsStepDesc));
+  printf("%zu %zu %zu %zu\\n", offsetof(AltxsStepDesc, layers), offsetof(AltxsStepDesc, emb),
+         offsetof(AltxsStepDesc, tokens), offsetof(AltxsStepDesc, err));
+  return 0;
+}}
+""")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    c_sizes = [int(x) for x in out]
+    py = [ctypes.sizeof(_lib.QTensor), ctypes.sizeof(_lib.AttnArgs), ctypes.sizeof(_lib.Layer),
+          ctypes.sizeof(_lib.Slot), ctypes.sizeof(_lib.StepDesc),
+          _lib.StepDesc.layers.offset, _lib.StepDesc.emb.offset, _lib.StepDesc.tokens.offset,
+          _lib.StepDesc.err.offset]
+    assert c_sizes == py
