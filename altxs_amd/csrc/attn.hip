@@ -19,9 +19,31 @@
 #include "common.h"
 #include "kernels.h"
 
+// Build-time knobs (the defaults are the measured best on MI355X).
+#ifndef ALTXS_ATT_WAVES
+#define ALTXS_ATT_WAVES 8      // waves per workgroup (chunk c goes to wave c % waves)
+#endif
+#ifndef ALTXS_ATT_PREFETCH
+#define ALTXS_ATT_PREFETCH 1   // load the next K/V tile while computing the current one
+#endif
+#ifndef ALTXS_ATT_NT
+#define ALTXS_ATT_NT 1         // non-temporal (streaming) K/V loads
+#endif
+#ifndef ALTXS_ATT_MINW
+#define ALTXS_ATT_MINW 1       // min waves per SIMD the register allocation must allow
+#endif
+
 namespace {
 
-constexpr int ATT_WAVES = 8;
+__device__ __forceinline__ u32x4 kv_load(const u32x4* p) {
+#if ALTXS_ATT_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
+constexpr int ATT_WAVES = ALTXS_ATT_WAVES;
 constexpr int ATT_THREADS = ATT_WAVES * WAVE;
 constexpr int CHUNK = 256;
 constexpr int TILE = 64;
@@ -80,7 +102,7 @@ struct AttnP {
 };
 
 template <int KVBF16, int GROUP, int YBF16>
-__global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnP a) {
+__global__ __launch_bounds__(ATT_THREADS, ALTXS_ATT_MINW) void attn_kernel(AttnP a) {
   using L = KVL<KVBF16>;
   constexpr int EPL = L::EPL, LPK = L::LPK, KPI = L::KPI, NI = L::NI;
   constexpr int ESZ = KVBF16 ? 2 : 4;
@@ -119,55 +141,89 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnP a) {
     for (int e = 0; e < EPL; ++e) acc[j][e] = 0.f;
   }
 
-  for (int c = wave; c < nchunks; c += ATT_WAVES) {
-    for (int tile = 0; tile < CHUNK / TILE; ++tile) {
-      const int k0 = c * CHUNK + tile * TILE;
-      if (k0 >= nkeys) break;
-      // Rows [k0, k0+64) are inside the cache: max_len is a multiple of 256.
-      u32x4 kr[NI], vr[NI];
+  // The wave's tiles, in order: chunks c = wave, wave + ATT_WAVES, ...; within
+  // a chunk, 64-key tiles while k0 < nkeys.  Rows [k0, k0+64) are inside the
+  // cache because max_len is a multiple of 256.
+  auto load_tile = [&](u32x4 (&kr)[NI], u32x4 (&vr)[NI], int k0) {
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int64_t off = ((int64_t)(k0 + KPI * i + ksub) * HD + dslice) * ESZ;
-        kr[i] = __builtin_nontemporal_load((const u32x4*)(kb + off));
-      }
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int64_t off = ((int64_t)(k0 + KPI * i + ksub) * HD + dslice) * ESZ;
-        vr[i] = __builtin_nontemporal_load((const u32x4*)(vb + off));
-      }
-      const int my_key = k0 + KPI * (lane % LPK) + ksub;
-#pragma unroll
-      for (int j = 0; j < GROUP; ++j) {
-        float s[NI];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          float kx[EPL];
-          unpack16<KVBF16>(kr[i], kx);
-          float d = 0.f;
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) d += qv[j][e] * kx[e];
-          s[i] = d;
-        }
-        float sc = transpose_reduce<NI, LPK>(s, lane);
-        if (my_key >= nkeys) sc = -INFINITY;
-        const float m_new = fmaxf(m_run[j], wave_max(sc));
-        const float alpha = __expf(m_run[j] - m_new);
-        const float pl = __expf(sc - m_new);
-        l_run[j] = l_run[j] * alpha + pl;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[j][e] *= alpha;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const float pk = __shfl(pl, (lane & ~(LPK - 1)) | i, WAVE);
-          float vx[EPL];
-          unpack16<KVBF16>(vr[i], vx);
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) acc[j][e] += pk * vx[e];
-        }
-        m_run[j] = m_new;
-      }
+    for (int i = 0; i < NI; ++i) {
+      const int64_t off = ((int64_t)(k0 + KPI * i + ksub) * HD + dslice) * ESZ;
+      kr[i] = kv_load((const u32x4*)(kb + off));
     }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int64_t off = ((int64_t)(k0 + KPI * i + ksub) * HD + dslice) * ESZ;
+      vr[i] = kv_load((const u32x4*)(vb + off));
+    }
+  };
+  auto process_tile = [&](const u32x4 (&kr)[NI], const u32x4 (&vr)[NI], int k0) {
+    const int my_key = k0 + KPI * (lane % LPK) + ksub;
+#pragma unroll
+    for (int j = 0; j < GROUP; ++j) {
+      float s[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float kx[EPL];
+        unpack16<KVBF16>(kr[i], kx);
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) d += qv[j][e] * kx[e];
+        s[i] = d;
+      }
+      float sc = transpose_reduce<NI, LPK>(s, lane);
+      if (my_key >= nkeys) sc = -INFINITY;
+      const float m_new = fmaxf(m_run[j], wave_max(sc));
+      const float alpha = __expf(m_run[j] - m_new);
+      const float pl = __expf(sc - m_new);
+      l_run[j] = l_run[j] * alpha + pl;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[j][e] *= alpha;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float pk = __shfl(pl, (lane & ~(LPK - 1)) | i, WAVE);
+        float vx[EPL];
+        unpack16<KVBF16>(vr[i], vx);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[j][e] += pk * vx[e];
+      }
+      m_run[j] = m_new;
+    }
+  };
+  // next tile after (c, tt) in this wave's order; false when none is left
+  auto advance = [&](int& c, int& tt) {
+    ++tt;
+    if (tt == CHUNK / TILE || c * CHUNK + tt * TILE >= nkeys) {
+      c += ATT_WAVES;
+      tt = 0;
+    }
+    return c < nchunks;
+  };
+  int c = wave, tt = 0;
+  bool have = c < nchunks;
+  u32x4 k0r[NI], v0r[NI];
+  if (have) load_tile(k0r, v0r, c * CHUNK);
+#if ALTXS_ATT_PREFETCH
+  u32x4 k1r[NI], v1r[NI];
+  while (have) {  // two tiles per trip: ping-pong register buffers
+    int c1 = c, t1 = tt;
+    const bool have1 = advance(c1, t1);
+    if (have1) load_tile(k1r, v1r, c1 * CHUNK + t1 * TILE);
+    process_tile(k0r, v0r, c * CHUNK + tt * TILE);
+    if (!have1) break;
+    c = c1; tt = t1;
+    int c2 = c, t2 = tt;
+    have = advance(c2, t2);
+    if (have) load_tile(k0r, v0r, c2 * CHUNK + t2 * TILE);
+    process_tile(k1r, v1r, c * CHUNK + tt * TILE);
+    c = c2; tt = t2;
   }
+#else
+  while (have) {
+    process_tile(k0r, v0r, c * CHUNK + tt * TILE);
+    have = advance(c, tt);
+    if (have) load_tile(k0r, v0r, c * CHUNK + tt * TILE);
+  }
+#endif
   // Combine the lanes that share a dim slice (fixed butterfly), then publish.
 #pragma unroll
   for (int j = 0; j < GROUP; ++j) {

@@ -11,21 +11,19 @@ namespace {
 // One wave per 16x256 block: lane l expands its 64 codes.
 template <int BITS>
 __global__ __launch_bounds__(64) void dequant_kernel(QT w, float* __restrict__ out) {
-  constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
   constexpr float center = 0.5f * (float)((1 << BITS) - 1);
   const int KB = w.K >> 8;
   const int nb = blockIdx.x / KB, kb = blockIdx.x % KB;
   const int lane = threadIdx.x;
-  uint32_t p0[2 * P0], p1[P1 > 0 ? 2 * P1 : 1];
-  float scale[4];
-  const size_t bi = (size_t)nb * KB + kb;
-  load_block<BITS>(w.codes + bi * (512 * BITS), w.scales + bi * 64, lane, p0, p1, scale);
+  Blk<BITS, A_BF16, false> b;
+  load_blk(b, w, nb, kb, lane, ADirect{nullptr, 0}, 0, 0, 0);
+  const float scale[4] = {half_lo(b.sc[0]), half_hi(b.sc[0]), half_lo(b.sc[1]), half_hi(b.sc[1])};
   const int n = nb * 16 + (lane & 15);
   float* row = out + (size_t)n * w.K + kb * 256 + 8 * (lane >> 4);
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
     uint32_t c[8];
-    codes_step<BITS>(p0, p1, s, c);
+    codes_step<BITS>(b.p0, b.p1, s, c);
 #pragma unroll
     for (int i = 0; i < 8; ++i) row[32 * s + i] = ((float)c[i] - center) * scale[s >> 1];
   }
@@ -35,10 +33,12 @@ int check_qt(const AltxsQTensor* w, const char* who) {
   ALTXS_REQUIRE(w && w->codes && w->scales, "%s: null tensor", who);
   ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6,
                 "%s: bits=%d not in {2,3,4,6}", who, w->bits);
-  ALTXS_REQUIRE(w->N > 0 && w->N % 16 == 0 && w->N < (1 << 24), "%s: N=%lld must be a positive multiple of 16",
-                who, (long long)w->N);
+  ALTXS_REQUIRE(w->N > 0 && w->N % 16 == 0 && w->N < (1 << 24),
+                "%s: N=%lld must be a positive multiple of 16", who, (long long)w->N);
   ALTXS_REQUIRE(w->K > 0 && w->K % 256 == 0 && w->K <= 8192,
                 "%s: K=%lld must be a positive multiple of 256 (<= 8192)", who, (long long)w->K);
+  ALTXS_REQUIRE(((uintptr_t)w->codes & 15) == 0 && ((uintptr_t)w->scales & 7) == 0,
+                "%s: codes must be 16-byte and scales 8-byte aligned", who);
   return ALTXS_OK;
 }
 
@@ -53,11 +53,11 @@ QT to_qt(const AltxsQTensor* w) {
 
 template <int AM>
 hipError_t run_gemm(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss, const void* x,
-                    int xdt, int64_t rows, float* y, hipStream_t s) {
+                    int64_t rows, float* y, hipStream_t s) {
   QT q = to_qt(w);
-  ProLoad pro{x, xdt, 0};
   EpiStore epi{y, q.N, rows * q.N};
-  return launch_qgemm_bits<AM>(w->bits, q, (int)rows, (int)count, cs, ss, pro, epi, s);
+  return launch_qgemm_rt<AM, 2, 4>(w->bits, q, (int)rows, (int)count, cs, ss,
+                                   ADirect{x, 0}, ProNone{}, epi, s);
 }
 
 int32_t gemm_common(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss, const void* x,
@@ -65,17 +65,16 @@ int32_t gemm_common(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss
   int rc = check_qt(w, who);
   if (rc) return rc;
   ALTXS_REQUIRE(x && y, "%s: null x/y", who);
+  ALTXS_REQUIRE(((uintptr_t)x & 15) == 0, "%s: x must be 16-byte aligned", who);
   ALTXS_REQUIRE(rows >= 1 && rows <= (1 << 20), "%s: rows=%lld out of range", who, (long long)rows);
   ALTXS_REQUIRE(count >= 1 && count <= 65535, "%s: count=%lld out of range", who, (long long)count);
-  ALTXS_REQUIRE(xdt == ALTXS_F32 || xdt == ALTXS_BF16 || xdt == ALTXS_F16, "%s: bad x dtype %d", who,
-                xdt);
-  ALTXS_REQUIRE(lds_bytes((int)w->K, xdt == ALTXS_F32 ? A_F32 : A_BF16) <= 160 * 1024,
-                "%s: K=%lld too large for the LDS A tile", who, (long long)w->K);
+  ALTXS_REQUIRE(xdt == ALTXS_F32 || xdt == ALTXS_BF16 || xdt == ALTXS_F16, "%s: bad x dtype %d",
+                who, xdt);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
-  if (xdt == ALTXS_F32) e = run_gemm<A_F32>(w, count, cs, ss, x, xdt, rows, y, s);
-  else if (xdt == ALTXS_BF16) e = run_gemm<A_BF16>(w, count, cs, ss, x, xdt, rows, y, s);
-  else e = run_gemm<A_F16>(w, count, cs, ss, x, xdt, rows, y, s);
+  if (xdt == ALTXS_F32) e = run_gemm<A_F32>(w, count, cs, ss, x, rows, y, s);
+  else if (xdt == ALTXS_BF16) e = run_gemm<A_BF16>(w, count, cs, ss, x, rows, y, s);
+  else e = run_gemm<A_F16>(w, count, cs, ss, x, rows, y, s);
   ALTXS_CHECK_HIP(e);
   return ALTXS_OK;
 }
@@ -109,7 +108,7 @@ extern "C" int32_t altxs_qgemm_stream(const AltxsQTensor* w, int64_t count, int6
                                       int64_t rows, float* y, altxs_stream_t stream) {
   ALTXS_REQUIRE(w, "altxs_qgemm_stream: null tensor");
   ALTXS_REQUIRE(codes_stride >= w->N * w->K * w->bits / 8 && scales_stride >= w->N * w->K / 64 * 2 &&
-                    scales_stride % 2 == 0 && codes_stride % 16 == 0,
+                    scales_stride % 8 == 0 && codes_stride % 16 == 0,
                 "altxs_qgemm_stream: strides smaller than one tensor or misaligned");
   return gemm_common(w, count, codes_stride, scales_stride / 2, x, x_dtype, rows, y, stream,
                      "altxs_qgemm_stream");

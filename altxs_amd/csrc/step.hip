@@ -172,96 +172,125 @@ __global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
 }
 
 // ---- prologues -------------------------------------------------------------
+//
+// 256 threads stage the 16-row A tile: 16 lanes per row, each lane owning the
+// float4 chunks c = lane + 16*j of the row (D <= 512 -> j < 8).  All loads of
+// a row are issued before any arithmetic; the row's RMS is a 16-lane butterfly.
 
-constexpr int MAXC = 4;  // float4 chunks per lane: D <= 64*4*4 = 1024
+constexpr int PTPR = 16;                  // prologue threads per row
+constexpr int PMAXJ = 512 / 4 / PTPR;     // float4 chunks per lane (D <= 512)
+
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
+  return v;
+}
 
 // Attention-side input of a slot: skip, resid_mix, RMSNorm * ln_scale.
 struct ProQKV {
+  static constexpr bool kStage = true;
   const float* x;      // slot input (x, or lane0 for a parallel slot)
   const float* x0;     // embedding output
   const float* skip;   // popped encoder output or NULL
   const float* skip_w; // [D] row of skip_weights
   const float* skip_g; // [D] row of skip_gates or NULL
   const float* mix;    // [2, D]
-  float* base_out;     // x_in (sequential) / lane0 after skip (parallel); block x==0 writes
+  float* base_out;     // x_in (sequential) / lane0 after skip (parallel); tile x==0 writes
   const float* gate_w; // [H, gw] or NULL
-  float* gate_out;     // [R, H]
+  float* gate_out;     // [R, H]; tile x==h (< H) writes head h
   float ln_scale, eps, gate_scale;
   int D, H, gw, parallel;
-  template <int AM>
+  template <int AM, int NT>
   __device__ void stage(void* As, int m0, int R, int K, int) const {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int RPP = NT / PTPR < 16 ? NT / PTPR : 16;  // rows per pass
+    const int t = threadIdx.x;
+    if (t >= RPP * PTPR) return;
+    const int li = t % PTPR;
     const int nch = D >> 2;
     const bool writer = blockIdx.x == 0;
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * wave + i, r = m0 + row;
-      if (r >= R) {
-        for (int c = lane; c < nch; c += 64)
+    const bool gater = gate_w && (int)blockIdx.x < H;
+    // this lane's gate weights (the gate reads only the first gw <= 16 features)
+    float gwl[4] = {0.f, 0.f, 0.f, 0.f};
+    if (gater) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) a_store<AM>(As, row, 4 * c + e, K, 0.f);
+      for (int e = 0; e < 4; ++e)
+        if (4 * li + e < gw) gwl[e] = gate_w[blockIdx.x * gw + 4 * li + e];
+    }
+    for (int row = t / PTPR; row < 16; row += RPP) {
+      const int r = m0 + row;
+      float in[PMAXJ][4];
+      if (r >= R) {
+#pragma unroll
+        for (int j = 0; j < PMAXJ; ++j) {
+          const int c = li + PTPR * j;
+          if (c < nch) {
+            const float z[4] = {0.f, 0.f, 0.f, 0.f};
+            a_store4<AM>(As, row, 4 * c, K, z);
+          }
+        }
         continue;
       }
-      float v[MAXC][4];
+      // every load of the row is issued here, before any use
+      f32x4 xv[PMAXJ], x0v[PMAXJ], sv[PMAXJ], m0v[PMAXJ], m1v[PMAXJ], swv[PMAXJ], sgv[PMAXJ];
+#pragma unroll
+      for (int j = 0; j < PMAXJ; ++j) {
+        const int c = li + PTPR * j;
+        if (c < nch) {
+          xv[j] = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
+          x0v[j] = *(const f32x4*)(x0 + (int64_t)r * D + 4 * c);
+          m0v[j] = *(const f32x4*)(mix + 4 * c);
+          m1v[j] = *(const f32x4*)(mix + D + 4 * c);
+          if (skip) {
+            sv[j] = *(const f32x4*)(skip + (int64_t)r * D + 4 * c);
+            swv[j] = *(const f32x4*)(skip_w + 4 * c);
+            if (skip_g) sgv[j] = *(const f32x4*)(skip_g + 4 * c);
+          }
+        }
+      }
       float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
+      for (int j = 0; j < PMAXJ; ++j) {
+        const int c = li + PTPR * j;
         if (c >= nch) continue;
-        const f32x4 xv = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
-        const f32x4 x0v = *(const f32x4*)(x0 + (int64_t)r * D + 4 * c);
-        float bs[4] = {xv[0], xv[1], xv[2], xv[3]};
+        float bs[4] = {xv[j][0], xv[j][1], xv[j][2], xv[j][3]};
         if (skip) {
-          const f32x4 sv = *(const f32x4*)(skip + (int64_t)r * D + 4 * c);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float sc = skip_w[4 * c + e] * sv[e];
-            if (skip_g) bs[e] = lerp_t(sc, bs[e], sigmoidf(skip_g[4 * c + e]));
+            const float sc = swv[j][e] * sv[j][e];
+            if (skip_g) bs[e] = lerp_t(sc, bs[e], sigmoidf(sgv[j][e]));
             else bs[e] = bs[e] + sc;
           }
         }
-        float in[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) in[e] = mix[4 * c + e] * bs[e] + mix[D + 4 * c + e] * x0v[e];
+        for (int e = 0; e < 4; ++e) {
+          in[j][e] = m0v[j][e] * bs[e] + m1v[j][e] * x0v[j][e];
+          ss += in[j][e] * in[j][e];
+        }
         if (writer) {
           f32x4 o;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = parallel ? bs[e] : in[e];
+          for (int e = 0; e < 4; ++e) o[e] = parallel ? bs[e] : in[j][e];
           *(f32x4*)(base_out + (int64_t)r * D + 4 * c) = o;
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[j][e] = in[e];
-          ss += in[e] * in[e];
-        }
       }
-      ss = wave_sum(ss);
+      ss = row16_sum(ss);
       const float inv = rsqrtf(ss / (float)D + eps);
+      float gpart = 0.f;
 #pragma unroll
-      for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
+      for (int j = 0; j < PMAXJ; ++j) {
+        const int c = li + PTPR * j;
         if (c >= nch) continue;
+        float n[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float n = (v[j][e] * inv) * ln_scale;
-          a_store<AM>(As, row, 4 * c + e, K, n);
-          v[j][e] = n;
+          n[e] = (in[j][e] * inv) * ln_scale;
+          if (gater && j == 0) gpart += n[e] * gwl[e];  // zero weights past gw
         }
+        a_store4<AM>(As, row, 4 * c, K, n);
       }
-      if (writer && gate_w) {
-        for (int h = 0; h < H; ++h) {
-          float part = 0.f;
-#pragma unroll
-          for (int j = 0; j < MAXC; ++j) {
-            const int c = lane + 64 * j;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int k = 4 * c + e;
-              if (c < nch && k < gw) part += v[j][e] * gate_w[h * gw + k];
-            }
-          }
-          const float dot = wave_sum(part);
-          if (lane == 0) gate_out[(int64_t)r * H + h] = sigmoidf(gate_scale * dot);
-        }
+      if (gater) {
+        const float dot = row16_sum(gpart);
+        if (li == 0) gate_out[(int64_t)r * H + blockIdx.x] = sigmoidf(gate_scale * dot);
       }
     }
   }
@@ -269,50 +298,53 @@ struct ProQKV {
 
 // RMSNorm (* scale) of rows of x (MLP input, final norm; final may average lanes).
 struct ProNorm {
+  static constexpr bool kStage = true;
   const float* x;
   const float* x2;  // second lane (final parallel "mean") or NULL
   int lane_mode;    // 0: x, 1: 0.5*(x + x2)
   float scale, eps;
   int D;
-  template <int AM>
+  template <int AM, int NT>
   __device__ void stage(void* As, int m0, int R, int K, int) const {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int RPP = NT / PTPR < 16 ? NT / PTPR : 16;
+    const int t = threadIdx.x;
+    if (t >= RPP * PTPR) return;
+    const int li = t % PTPR;
     const int nch = D >> 2;
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * wave + i, r = m0 + row;
-      if (r >= R) {
-        for (int c = lane; c < nch; c += 64)
+    for (int row = t / PTPR; row < 16; row += RPP) {
+      const int r = m0 + row;
+      f32x4 v[PMAXJ], v2[PMAXJ];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) a_store<AM>(As, row, 4 * c + e, K, 0.f);
-        continue;
+      for (int j = 0; j < PMAXJ; ++j) {
+        const int c = li + PTPR * j;
+        if (c < nch && r < R) {
+          v[j] = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
+          if (lane_mode == 1) v2[j] = *(const f32x4*)(x2 + (int64_t)r * D + 4 * c);
+        }
       }
-      float v[MAXC][4];
       float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
+      for (int j = 0; j < PMAXJ; ++j) {
+        const int c = li + PTPR * j;
         if (c >= nch) continue;
-        const f32x4 xv = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
-        f32x4 yv = xv;
-        if (lane_mode == 1) {
-          const f32x4 x2v = *(const f32x4*)(x2 + (int64_t)r * D + 4 * c);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) yv[e] = 0.5f * (xv[e] + x2v[e]);
-        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[j][e] = yv[e];
-          ss += yv[e] * yv[e];
+          float y = r < R ? v[j][e] : 0.f;
+          if (lane_mode == 1 && r < R) y = 0.5f * (v[j][e] + v2[j][e]);
+          v[j][e] = y;
+          ss += y * y;
         }
       }
-      ss = wave_sum(ss);
-      const float inv = rsqrtf(ss / (float)D + eps);
+      ss = row16_sum(ss);
+      const float inv = r < R ? rsqrtf(ss / (float)D + eps) : 0.f;
 #pragma unroll
-      for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
+      for (int j = 0; j < PMAXJ; ++j) {
+        const int c = li + PTPR * j;
         if (c >= nch) continue;
+        float n[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a_store<AM>(As, row, 4 * c + e, K, (v[j][e] * inv) * scale);
+        for (int e = 0; e < 4; ++e) n[e] = (v[j][e] * inv) * scale;
+        a_store4<AM>(As, row, 4 * c, K, n);
       }
     }
   }
@@ -324,6 +356,7 @@ __device__ __forceinline__ int row_pos(const int32_t* pos, int W, int r) {
   return pos[r / W] + (r % W);
 }
 
+// One head (64 columns) per tile: QK-RMSNorm, RoPE, q_gain, KV-cache write.
 struct EpiQKV {
   float* q;          // [R, H, 64]
   char* kv;          // this slot's cache: [B][2][Hkv][max_len][64]
@@ -334,53 +367,94 @@ struct EpiQKV {
   const float* q_gain;
   float eps;
   int32_t* err;
-  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int wave,
-                             unsigned char* smem, int R, int) const {
-    // Exchange the 16x64 tile (one head) through LDS.
-    __syncthreads();  // every wave is done reading the A tile
-    float* C = (float*)smem;
-    constexpr int CS = HD + 1;
-    const int cl = wave * 16 + (lane & 15);
+  template <class Cfg> struct Pre {
+    static constexpr int TPR = Cfg::THREADS / 16, CPT = 64 / TPR;
+    int p;
+    float cs[CPT], sn[CPT], gain;
+  };
+  template <class Cfg>
+  __device__ Pre<Cfg> prefetch(int m0, int R, int) const {
+    using P = Pre<Cfg>;
+    P o;
+    const int row = threadIdx.x / P::TPR, c0 = (threadIdx.x % P::TPR) * P::CPT;
+    const int r = m0 + row;
+    o.p = r < R ? row_pos(pos, W, r) : 0;
+    const int nt = blockIdx.x;
+    o.gain = nt < H ? q_gain[nt] : 1.f;
+    const int half = rd >> 1;
+    const int pp = (o.p >= 0 && o.p < max_len) ? o.p : 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) C[(4 * (lane >> 4) + i) * CS + cl] = acc[i];
-    __syncthreads();
-    const int nt = blockIdx.x;  // head tile
+    for (int i = 0; i < P::CPT; ++i) {
+      const int c = c0 + i;
+      const int fi = c < half ? c : c - half;
+      o.cs[i] = (c < rd && nt < H + Hkv) ? cosb[(int64_t)pp * half + fi] : 1.f;
+      o.sn[i] = (c < rd && nt < H + Hkv) ? sinb[(int64_t)pp * half + fi] : 0.f;
+    }
+    return o;
+  }
+  template <class Cfg, class P>
+  __device__ void apply(const float* C, const P& pre, int m0, int, int R, int) const {
+    constexpr int TPR = P::TPR, CPT = P::CPT;
+    const int row = threadIdx.x / TPR, li = threadIdx.x % TPR, c0 = li * CPT;
+    const int r = m0 + row;
+    const int nt = blockIdx.x;
     const int kind = nt < H ? 0 : (nt < H + Hkv ? 1 : 2);
     const int head = kind == 0 ? nt : (kind == 1 ? nt - H : nt - H - Hkv);
-    const int64_t esz = kv_bf16 ? 2 : 4;
-    const int half = rd >> 1;
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * wave + i, r = m0 + row;
-      if (r >= R) continue;  // wave-uniform
-      float val = C[row * CS + lane];
-      int p = row_pos(pos, W, r);
-      const bool pos_ok = p >= 0 && p < max_len;
-      if (!pos_ok && lane == 0) flag_err(err, ALTXS_EDEV_POS);
-      if (kind < 2) {
-        const float ss = wave_sum(val * val);
-        val = val * rsqrtf(ss * (1.0f / HD) + eps);
-        const int pp = pos_ok ? p : 0;
-        const int partner = lane < half ? lane + half : lane - half;
-        const float pv = __shfl(val, partner & 63, WAVE);
-        if (lane < rd) {
-          const int fi = lane < half ? lane : lane - half;
-          const float cs = cosb[(int64_t)pp * half + fi];
-          const float sn = sinb[(int64_t)pp * half + fi];
-          val = lane < half ? (val * cs + pv * sn) : (pv * -sn + val * cs);
-        }
+    float v[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) v[i] = C[row * Cfg::CS + c0 + i];
+    if (kind < 2) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) ss += v[i] * v[i];
+#pragma unroll
+      for (int m = TPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, WAVE);
+      const float inv = rsqrtf(ss * (1.0f / HD) + eps);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) v[i] *= inv;
+      // partner column c +- rd/2 lives (rd/2)/CPT lanes away
+      const int off = (rd >> 1) / CPT;
+      float pv[CPT];
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const float up = __shfl_down(v[i], off, WAVE);
+        const float dn = __shfl_up(v[i], off, WAVE);
+        pv[i] = (c0 < (rd >> 1)) ? up : dn;
       }
-      if (kind == 0) {
-        q[((int64_t)r * H + head) * HD + lane] = val * q_gain[head];
-      } else if (pos_ok) {
-        const int b = r / W;
-        const int64_t off =
-            ((((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len + p) * HD + lane;
-        if (kv_bf16) ((uint16_t*)kv)[off] = f32_to_bf16(val);
-        else ((float*)kv)[off] = val;
-        (void)esz;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = c0 + i;
+        if (c < (rd >> 1)) v[i] = v[i] * pre.cs[i] + pv[i] * pre.sn[i];
+        else if (c < rd) v[i] = pv[i] * -pre.sn[i] + v[i] * pre.cs[i];
       }
     }
+    if (r >= R) return;
+    const int p = pre.p;
+    const bool pos_ok = p >= 0 && p < max_len;
+    if (kind == 0) {
+      float* qo = q + ((int64_t)r * H + head) * HD + c0;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) qo[i] = v[i] * pre.gain;
+    } else if (pos_ok) {
+      const int b = r / W;
+      const int64_t off =
+          ((((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len + p) * HD + c0;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        if (kv_bf16) ((uint16_t*)kv)[off + i] = f32_to_bf16(v[i]);
+        else ((float*)kv)[off + i] = v[i];
+      }
+    } else if (li == 0) {
+      flag_err(err, ALTXS_EDEV_POS);
+    }
   }
+};
+
+// Elementwise epilogues: thread t handles tile elements t + THREADS*j.
+template <class Cfg> struct EW {
+  static constexpr int EPT = 16 * Cfg::NCOL / Cfg::THREADS;
+  __device__ static int row(int j) { return (threadIdx.x + Cfg::THREADS * j) / Cfg::NCOL; }
+  __device__ static int col(int j) { return (threadIdx.x + Cfg::THREADS * j) % Cfg::NCOL; }
 };
 
 struct EpiO {
@@ -388,17 +462,29 @@ struct EpiO {
   const float* attn_scale;
   float* xout;
   int D, parallel;
-  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
-                             int R, int) const {
-    const int col = nb * 16 + (lane & 15);
-    if (col >= D) return;
+  template <class Cfg> struct Pre { float base[EW<Cfg>::EPT], sc[EW<Cfg>::EPT]; };
+  template <class Cfg>
+  __device__ Pre<Cfg> prefetch(int m0, int R, int) const {
+    Pre<Cfg> o;
+    const int n0 = blockIdx.x * Cfg::NCOL;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m0 + 4 * (lane >> 4) + i;
-      if (r >= R) continue;
-      const int64_t o = (int64_t)r * D + col;
-      const float a = attn_scale[col] * acc[i];
-      xout[o] = parallel ? a : xin[o] + a;
+    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
+      const int r = m0 + EW<Cfg>::row(j), c = n0 + EW<Cfg>::col(j);
+      const bool ok = r < R && c < D;
+      o.base[j] = (ok && !parallel) ? xin[(int64_t)r * D + c] : 0.f;
+      o.sc[j] = ok ? attn_scale[c] : 0.f;
+    }
+    return o;
+  }
+  template <class Cfg, class P>
+  __device__ void apply(const float* C, const P& pre, int m0, int n0, int R, int) const {
+#pragma unroll
+    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
+      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
+      const int r = m0 + rr, c = n0 + cc;
+      if (r >= R || c >= D) continue;
+      const float a = pre.sc[j] * C[rr * Cfg::CS + cc];
+      xout[(int64_t)r * D + c] = parallel ? a : pre.base[j] + a;
     }
   }
 };
@@ -406,18 +492,20 @@ struct EpiO {
 struct EpiUp {
   void* h;  // [R, F] fp32 or bf16
   int F, hb16;
-  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
-                             int R, int) const {
-    const int col = nb * 16 + (lane & 15);
-    if (col >= F) return;
+  template <class Cfg> struct Pre {};
+  template <class Cfg>
+  __device__ Pre<Cfg> prefetch(int, int, int) const { return {}; }
+  template <class Cfg, class P>
+  __device__ void apply(const float* C, const P&, int m0, int n0, int R, int) const {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m0 + 4 * (lane >> 4) + i;
-      if (r >= R) continue;
-      const float v = acc[i];
+    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
+      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
+      const int r = m0 + rr, c = n0 + cc;
+      if (r >= R || c >= F) continue;
+      const float v = C[rr * Cfg::CS + cc];
       const float lr = v > 0.f ? v : 0.5f * v;
       const float o = lr * lr;
-      const int64_t idx = (int64_t)r * F + col;
+      const int64_t idx = (int64_t)r * F + c;
       if (hb16) ((uint16_t*)h)[idx] = f32_to_bf16(o);
       else ((float*)h)[idx] = o;
     }
@@ -434,22 +522,40 @@ struct EpiDown {
   const float* pr;     // par: [2]
   const float* pp;     // par: [2, 2]
   int D, parallel;
-  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
-                             int R, int) const {
-    const int col = nb * 16 + (lane & 15);
-    if (col >= D) return;
+  template <class Cfg> struct Pre {
+    float xo[EW<Cfg>::EPT], sc[EW<Cfg>::EPT], l0[EW<Cfg>::EPT], l1[EW<Cfg>::EPT];
+  };
+  template <class Cfg>
+  __device__ Pre<Cfg> prefetch(int m0, int R, int) const {
+    Pre<Cfg> o;
+    const int n0 = blockIdx.x * Cfg::NCOL;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m0 + 4 * (lane >> 4) + i;
-      if (r >= R) continue;
-      const int64_t o = (int64_t)r * D + col;
-      const float m = mlp_scale[col] * acc[i];
+    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
+      const int r = m0 + EW<Cfg>::row(j), c = n0 + EW<Cfg>::col(j);
+      const bool ok = r < R && c < D;
+      const int64_t idx = (int64_t)r * D + c;
+      o.xo[j] = ok ? xout[idx] : 0.f;
+      o.sc[j] = ok ? mlp_scale[c] : 0.f;
+      o.l0[j] = (ok && parallel) ? lane0[idx] : 0.f;
+      o.l1[j] = (ok && parallel) ? lane1[idx] : 0.f;
+    }
+    return o;
+  }
+  template <class Cfg, class P>
+  __device__ void apply(const float* C, const P& pre, int m0, int n0, int R, int) const {
+#pragma unroll
+    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
+      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
+      const int r = m0 + rr, c = n0 + cc;
+      if (r >= R || c >= D) continue;
+      const int64_t o = (int64_t)r * D + c;
+      const float m = pre.sc[j] * C[rr * Cfg::CS + cc];
       if (!parallel) {
-        out0[o] = xout[o] + m;
+        out0[o] = pre.xo[j] + m;
       } else {
-        const float a = xout[o];
-        out0[o] = pr[0] * lane0[o] + pp[0] * a + pp[2] * m;
-        out1[o] = pr[1] * lane1[o] + pp[1] * a + pp[3] * m;
+        const float a = pre.xo[j];
+        out0[o] = pr[0] * pre.l0[j] + pp[0] * a + pp[2] * m;
+        out1[o] = pr[1] * pre.l1[j] + pp[1] * a + pp[3] * m;
       }
     }
   }
@@ -460,23 +566,24 @@ struct EpiLogits {
   int V, asym;
   float cap;
   const float* cap_pn;
-  __device__ void operator()(const f32x4& acc, int m0, int nb, int lane, int, unsigned char*,
-                             int R, int) const {
-    const int col = nb * 16 + (lane & 15);
-    if (col >= V) return;
+  template <class Cfg> struct Pre { float cp, cn; };
+  template <class Cfg>
+  __device__ Pre<Cfg> prefetch(int, int, int) const {
+    Pre<Cfg> o;
+    o.cp = asym ? cap_pn[0] : cap;
+    o.cn = asym ? cap_pn[1] : cap;
+    return o;
+  }
+  template <class Cfg, class P>
+  __device__ void apply(const float* C, const P& pre, int m0, int n0, int R, int) const {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m0 + 4 * (lane >> 4) + i;
-      if (r >= R) continue;
-      const float l = acc[i];
-      float o;
-      if (asym) {
-        const float c = l >= 0.f ? cap_pn[0] : cap_pn[1];
-        o = c * tanhf(l / c);
-      } else {
-        o = cap * tanhf(l / cap);
-      }
-      logits[(int64_t)r * V + col] = o;
+    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
+      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
+      const int r = m0 + rr, c = n0 + cc;
+      if (r >= R || c >= V) continue;
+      const float l = C[rr * Cfg::CS + cc];
+      const float cp = l >= 0.f ? pre.cp : pre.cn;
+      logits[(int64_t)r * V + c] = cp * tanhf(l / cp);
     }
   }
 };
@@ -548,7 +655,7 @@ int validate(const AltxsStepDesc* d) {
                 d->abi_version, ALTXS_ABI_VERSION);
   ALTXS_REQUIRE(d->head_dim == HD, "altxs_step: head_dim=%d (only 64 is built)", d->head_dim);
   ALTXS_REQUIRE(d->D == d->H * HD, "altxs_step: D != H*head_dim");
-  ALTXS_REQUIRE(d->D % 256 == 0 && d->D <= 1024, "altxs_step: D=%d must be a multiple of 256, <= 1024",
+  ALTXS_REQUIRE(d->D % 256 == 0 && d->D <= 512, "altxs_step: D=%d must be 256 or 512",
                 d->D);
   ALTXS_REQUIRE(d->F % 256 == 0 && d->F <= 8192, "altxs_step: F=%d must be a multiple of 256", d->F);
   ALTXS_REQUIRE(d->V >= 16 && d->V % 16 == 0 && d->V <= 65536, "altxs_step: V=%d must be a multiple of 16 in [16, 65536]",
@@ -561,7 +668,7 @@ int validate(const AltxsStepDesc* d) {
   ALTXS_REQUIRE(d->n_slots >= 1 && d->n_slots <= ALTXS_MAX_SLOTS, "altxs_step: n_slots");
   ALTXS_REQUIRE(d->max_len >= 256 && d->max_len % 256 == 0, "altxs_step: max_len=%d must be a multiple of 256",
                 d->max_len);
-  ALTXS_REQUIRE(d->rope_dims >= 2 && d->rope_dims <= HD && d->rope_dims % 2 == 0,
+  ALTXS_REQUIRE(d->rope_dims >= 8 && d->rope_dims <= HD && d->rope_dims % 8 == 0,
                 "altxs_step: rope_dims=%d", d->rope_dims);
   ALTXS_REQUIRE(d->gate_window >= 0 && d->gate_window <= d->D, "altxs_step: gate_window");
   ALTXS_REQUIRE(d->lora_rank == 0, "altxs_step: LoRA is not built in this version");
@@ -606,7 +713,6 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
   const int64_t Rp = align_up(R, 16);
   const int64_t D = d->D;
   const int hb16 = AM == A_BF16 ? 1 : 0;
-  const int xdt = AM == A_BF16 ? ALTXS_BF16 : ALTXS_F32;
   const int64_t esz = d->kv_bf16 ? 2 : 4;
   const int64_t slot_kv = (int64_t)d->B * 2 * d->Hkv * d->max_len * HD;
   hipError_t e;
@@ -646,7 +752,8 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
       epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = d->pos;
       epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
       epi.err = d->err;
-      if ((e = launch_qgemm_bits<AM>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+      if ((e = launch_qgemm_rt<AM, 4, 2>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
+                                         pro, epi, st)) != hipSuccess)
         return e;
     }
     // attention
@@ -666,27 +773,28 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
     }
     // out-projection + attention residual
     {
-      ProLoad pro{w.Y, xdt, 0};
       EpiO epi{w.XIN, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
-      if ((e = launch_qgemm_bits<AM>(L.o.bits, qt_of(L.o), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+      if ((e = launch_qgemm_rt<AM, 1, 2>(L.o.bits, qt_of(L.o), R, 1, 0, 0, ADirect{w.Y, 0}, ProNone{},
+                                         epi, st)) != hipSuccess)
         return e;
     }
     // MLP up + LeakyReLU(0.5)^2
     {
       ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       EpiUp epi{w.HB, d->F, hb16};
-      if ((e = launch_qgemm_bits<AM>(L.up.bits, qt_of(L.up), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+      if ((e = launch_qgemm_rt<AM, 2, 2>(L.up.bits, qt_of(L.up), R, 1, 0, 0, ADirect{nullptr, 0}, pro,
+                                         epi, st)) != hipSuccess)
         return e;
     }
     // MLP down + residual / lanes
     {
-      ProLoad pro{w.HB, xdt, 0};
       EpiDown epi;
       epi.xout = w.XOUT; epi.mlp_scale = L.mlp_scale;
       epi.out0 = w.X0 + (s + 1) * Rp * D; epi.out1 = w.X1 + (s + 1) * Rp * D;
       epi.lane0 = w.XIN; epi.lane1 = lane1_in; epi.pr = L.par_resid; epi.pp = L.par_post;
       epi.D = d->D; epi.parallel = par ? 1 : 0;
-      if ((e = launch_qgemm_bits<AM>(L.down.bits, qt_of(L.down), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+      if ((e = launch_qgemm_rt<AM, 1, 4>(L.down.bits, qt_of(L.down), R, 1, 0, 0, ADirect{w.HB, 0},
+                                         ProNone{}, epi, st)) != hipSuccess)
         return e;
     }
   }
@@ -705,7 +813,8 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
     ProNorm pro{xf, x2, mode, 1.0f, d->norm_eps, d->D};
     EpiLogits epi{d->logits, d->V, (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap,
                   d->softcap_pn};
-    if ((e = launch_qgemm_bits<AM>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, pro, epi, st)) != hipSuccess)
+    if ((e = launch_qgemm_rt<AM, 2, 2>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0}, pro,
+                                       epi, st)) != hipSuccess)
       return e;
   }
   if (d->probs || d->cum) {
