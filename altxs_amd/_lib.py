@@ -12,7 +12,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libaltxs_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MAX_LAYERS = 32
 MAX_SLOTS = 64
@@ -28,6 +28,8 @@ F_RENORM = 1 << 5
 F_FINAL_ATTN = 1 << 6
 F_FINAL_MLP = 1 << 7
 CDF_RENORM = 1
+ATTN_OPS_BF16 = 1
+KV_TILE = 64
 
 SLOT_SEQ, SLOT_PAR = 0, 1
 
@@ -63,7 +65,7 @@ class AttnArgs(ctypes.Structure):
                 ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
                 ("kv_seg_stride", ctypes.c_int64), ("pos", ctypes.c_void_p),
                 ("gate", ctypes.c_void_p), ("use_xsa", ctypes.c_int32),
-                ("reserved", ctypes.c_int32), ("y", ctypes.c_void_p), ("err", ctypes.c_void_p)]
+                ("flags", ctypes.c_int32), ("y", ctypes.c_void_p), ("err", ctypes.c_void_p)]
 
 
 class Layer(ctypes.Structure):

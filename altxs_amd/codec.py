@@ -209,3 +209,53 @@ def allocate_bits(sizes: list[tuple[str, int]], target: float) -> dict[str, int]
             bits[name] = 2
             break
     return bits
+
+
+# ---- bf16 KV cache tile layout (include/altxs.h, ALTXS_KV_TILE) -------------
+
+KV_TILE = 64
+
+
+def tile_kv(x, which: str):
+    """Natural [..., max_len, 64] K or V -> the bf16 cache's tiled operand order.
+
+    Works on numpy arrays and torch tensors (any device).  Per 64-key tile the
+    4096 elements are reordered so each lane's MFMA operand is 16 contiguous
+    bytes: K as (block, kstep, lanegroup, key%16, dim%8), V as (kstep,
+    dimblock, lanegroup, dim%16, key-half, key%4) -- the index formulas
+    kv_tile_k / kv_tile_v of altxs_amd/csrc/common.h.
+    """
+    *lead, L, hd = x.shape
+    if hd != 64 or L % KV_TILE:
+        raise ValueError(f"expected [..., multiple of {KV_TILE}, 64], got {tuple(x.shape)}")
+    nt = L // KV_TILE
+    n = len(lead)
+    if which == "k":   # key = 16*blk + r ; dim = 32*ks + 8*g + j
+        y = x.reshape(*lead, nt, 4, 16, 2, 4, 8)
+        perm = (0, 1, 3, 4, 2, 5)
+    elif which == "v":  # key = 32*s + 16*jb + 4*g + jr ; dim = 16*nb + dd
+        y = x.reshape(*lead, nt, 2, 2, 4, 4, 4, 16)
+        perm = (0, 1, 5, 3, 6, 2, 4)
+    else:
+        raise ValueError(which)
+    perm = tuple(range(n)) + tuple(n + p for p in perm)
+    y = y.transpose(perm) if isinstance(y, np.ndarray) else y.permute(perm)
+    return y.reshape(*lead, L, hd)
+
+
+def untile_kv(x, which: str):
+    """Inverse of :func:`tile_kv`."""
+    *lead, L, hd = x.shape
+    nt = L // KV_TILE
+    n = len(lead)
+    if which == "k":
+        y = x.reshape(*lead, nt, 4, 2, 4, 16, 8)   # (T, blk, ks, g, r, j)
+        perm = (0, 1, 4, 2, 3, 5)                  # -> (T, blk, r, ks, g, j)
+    elif which == "v":
+        y = x.reshape(*lead, nt, 2, 4, 4, 16, 2, 4)  # (T, s, nb, g, dd, jb, jr)
+        perm = (0, 1, 5, 3, 6, 2, 4)                 # -> (T, s, jb, g, jr, nb, dd)
+    else:
+        raise ValueError(which)
+    perm = tuple(range(n)) + tuple(n + p for p in perm)
+    y = y.transpose(perm) if isinstance(y, np.ndarray) else y.permute(perm)
+    return y.reshape(*lead, L, hd)

@@ -25,6 +25,20 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// ---- bf16 KV cache tile layout (include/altxs.h, ALTXS_KV_TILE) -------------
+// Offset of (key kt of a 64-key tile, dim d) inside the tile's 4096 elements.
+// K: the A operand of the score MFMA (lane 16g + r: key r of a 16-key block,
+//    dims 32*ks + 8*g + [0, 8)).
+// V: the B operand of the P x V MFMA (lane 16g + c: dim 16*nb + c, keys
+//    16*(2s + jb) + 4*g + jr for j = 4*jb + jr in [0, 8)).
+__host__ __device__ __forceinline__ int kv_tile_k(int kt, int d) {
+  return ((((kt >> 4) * 2 + (d >> 5)) * 4 + ((d >> 3) & 3)) * 16 + (kt & 15)) * 8 + (d & 7);
+}
+__host__ __device__ __forceinline__ int kv_tile_v(int kt, int d) {
+  return ((((kt >> 5) * 4 + (d >> 4)) * 4 + ((kt >> 2) & 3)) * 16 + (d & 15)) * 8 +
+         4 * ((kt >> 4) & 1) + (kt & 3);
+}
+
 // ---- wave reductions (fixed butterfly order: deterministic) ---------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -437,12 +437,17 @@ struct EpiQKV {
       for (int i = 0; i < CPT; ++i) qo[i] = v[i] * pre.gain;
     } else if (pos_ok) {
       const int b = r / W;
-      const int64_t off =
-          ((((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len + p) * HD + c0;
+      const int64_t head_base = (((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len * HD;
+      if (kv_bf16) {  // tiled operand layout (kv_tile_k / kv_tile_v)
+        uint16_t* tile = (uint16_t*)kv + head_base + (int64_t)(p / ALTXS_KV_TILE) * (ALTXS_KV_TILE * HD);
+        const int kt = p % ALTXS_KV_TILE;
 #pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        if (kv_bf16) ((uint16_t*)kv)[off + i] = f32_to_bf16(v[i]);
-        else ((float*)kv)[off + i] = v[i];
+        for (int i = 0; i < CPT; ++i)
+          tile[kind == 1 ? kv_tile_k(kt, c0 + i) : kv_tile_v(kt, c0 + i)] = f32_to_bf16(v[i]);
+      } else {
+        float* row = (float*)kv + head_base + (int64_t)p * HD + c0;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) row[i] = v[i];
       }
     } else if (li == 0) {
       flag_err(err, ALTXS_EDEV_POS);
@@ -766,6 +771,7 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
       a.kv_seg_stride = 2ll * d->Hkv * d->max_len * HD; a.pos = d->pos;
       a.gate = (d->flags & ALTXS_F_SPARSE_GATE) ? w.GATE : nullptr;
       a.use_xsa = L.use_xsa; a.y = w.Y; a.err = d->err;
+      a.flags = AM == A_BF16 ? ALTXS_ATTN_OPS_BF16 : 0;
       hipEvent_t* ev = (hipEvent_t*)d->attn_events;
       if (ev && (e = hipEventRecord(ev[2 * s], st)) != hipSuccess) return e;
       if ((e = altxs_launch_attn(a, st)) != hipSuccess) return e;

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define ALTXS_ABI_VERSION 1
+#define ALTXS_ABI_VERSION 2
 
 enum {
   ALTXS_OK = 0,
@@ -109,24 +109,46 @@ int32_t altxs_qgemm_stream(const AltxsQTensor *w, int64_t count, int64_t codes_s
                            int64_t rows, float *y, altxs_stream_t stream);
 
 /*
+ * KV cache layout.  Per (segment, kv head) the cache holds max_len keys of
+ * head_dim = 64 in 64-key tiles (ALTXS_KV_TILE); max_len % 64 == 0.
+ *   fp32 cache: natural order, element (key, d) at key*64 + d.
+ *   bf16 cache: each 4096-element tile is stored in MFMA operand order so one
+ *   16-byte load per lane feeds v_mfma_f32_16x16x32_bf16.  For key kt = key % 64
+ *   of tile key / 64 and dim d (tile base + offset):
+ *     K: ((((kt>>4)*2 + (d>>5))*4 + ((d>>3)&3))*16 + (kt&15))*8 + (d&7)
+ *     V: ((((kt>>5)*4 + (d>>4))*4 + ((kt>>2)&3))*16 + (d&15))*8
+ *          + 4*((kt>>4)&1) + (kt&3)
+ *   altxs_amd.codec.tile_kv() converts a natural [.., max_len, 64] tensor.
+ */
+#define ALTXS_KV_TILE 64
+
+/* AltxsAttnArgs.flags */
+#define ALTXS_ATTN_OPS_BF16 1 /* bf16 cache: round q and the softmax weights to
+                                 bf16 for the MFMA products (the reference's
+                                 tl.dot arithmetic, split_attn.py:86-141);
+                                 0 = fp32-faithful (3-part bf16 splits) */
+
+/*
  * Decode attention over a KV cache.  For row r = b*W + t the query sits at
  * position p = pos[b] + t and attends to keys [0, p] of segment b.  Keys are
- * scanned in fixed 256-key chunks and merged left to right, so a row's result
- * does not depend on B or W.  Replaces run_split_attn (split_attn.py:341-425)
- * and the eager _static_window_attention (model.py:550-585).
+ * scanned in fixed 64-key tiles (tile T by wave T % waves) and the per-wave
+ * partials merged in wave order, so a row's result does not depend on B or W.
+ * Replaces run_split_attn (split_attn.py:341-425) and the eager
+ * _static_window_attention (model.py:550-585).
  */
 typedef struct AltxsAttnArgs {
   int32_t B, W, H, Hkv, head_dim, max_len;
   int32_t kv_bf16;  /* KV element type: 0 fp32, 1 bf16 */
   int32_t y_bf16;   /* output element type: 0 fp32, 1 bf16 */
   const float *q;   /* [B*W, H, head_dim] fp32 */
-  const void *k;    /* [B, Hkv, max_len, head_dim], seg stride kv_seg_stride elems */
+  const void *k;    /* [B, Hkv, max_len, head_dim] in the cache layout above,
+                       seg stride kv_seg_stride elems; 16-byte aligned */
   const void *v;
   int64_t kv_seg_stride; /* elements between segments (both K and V) */
   const int32_t *pos;    /* [B] */
   const float *gate;     /* [B*W, H] multiplier (sparse attention gate) or NULL */
   int32_t use_xsa;       /* subtract the current value direction (model.py:760-768) */
-  int32_t reserved;
+  int32_t flags;         /* ALTXS_ATTN_* */
   void *y;               /* [B*W, H*head_dim] */
   int32_t *err;          /* device error word or NULL */
 } AltxsAttnArgs;
@@ -205,7 +227,7 @@ typedef struct AltxsStepDesc {
   int32_t *pos;          /* [B] window start position of each segment */
   float *prev_raw;       /* [B, D] raw embedding of each segment's previous token */
   float *cand_raw;       /* [B, D] raw embedding of the window's last token */
-  void *kv;              /* [n_slots, B, 2, Hkv, max_len, head_dim] */
+  void *kv;              /* [n_slots, B, 2, Hkv, max_len, head_dim], cache layout above */
   void *ws;              /* workspace, altxs_step_workspace_bytes() bytes */
   int64_t ws_bytes;
   float *logits;         /* [B*W, V] */

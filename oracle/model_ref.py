@@ -21,9 +21,12 @@ and, with every motif switch off, against a textbook pre-norm GPT written
 with F.scaled_dot_product_attention (tests/test_oracle_model.py).
 
 ``act="bf16"`` additionally rounds, exactly where the GPU's bf16 mode does,
-the GEMM inputs (normed activations, attention output, MLP hidden) and the
+the GEMM inputs (normed activations, attention output, MLP hidden), the
 K/V entries written to the cache (the cached values are the ones attention
-and XSA read).  ``act="fp32"`` is the reference's arithmetic.
+and XSA read) and the query as the score operand.  The GPU's bf16 mode also
+rounds the unnormalised softmax weights to bf16 for the P x V product (as
+the reference's tl.dot does, split_attn.py:131-141); that rounding depends on
+the kernel's key tiling and is not emulated here.  ``act="fp32"`` is the reference's arithmetic.
 """
 
 from __future__ import annotations
@@ -214,6 +217,7 @@ class OracleModel:
         pos = torch.arange(st.pos, st.pos + T)
         q, k, v = self._qkv(i, n, pos)
         k, v = self._r(k), self._r(v)  # cache storage rounding (bf16 mode)
+        q = self._r(q)  # bf16 score operand (split_attn.py:86-93 rounds q to bf16)
         st.k[slot][st.pos:st.pos + T] = k
         st.v[slot][st.pos:st.pos + T] = v
         Lv = st.pos + T

@@ -113,3 +113,36 @@ def test_shipped_asset_sizes_match_closed_forms():
                                            mode=meta.get("codebook_mode", "lloyd"))
         assert ch.shape == (bits.size, width) and np.isfinite(ch).all()
         assert np.all(ch[bits == 0] == 0)
+
+
+def test_kv_tile_layout_roundtrip_and_operand_runs():
+    """tile_kv/untile_kv are inverse permutations; each MFMA operand is a 16-byte run.
+
+    K: lane 16g + r of k-step ks in block blk reads key 16*blk + r, dims
+    32*ks + 8*g + [0, 8); V: lane 16g + c of k-step s, dim block nb reads dim
+    16*nb + c of keys 16*(2s + j//4) + 4g + j%4 for j = 0..7.  Both must be the
+    8 consecutive elements at offset 8 * (64 * step + lane) of the tile.
+    """
+    from altxs_amd.codec import tile_kv, untile_kv
+
+    rng = np.random.default_rng(5)
+    x = rng.integers(0, 1 << 30, size=(2, 3, 192, 64))
+    for which in ("k", "v"):
+        t = tile_kv(x, which)
+        assert np.array_equal(untile_kv(t, which), x)
+        assert sorted(t.reshape(-1).tolist()) == sorted(x.reshape(-1).tolist())
+    tk = tile_kv(x, "k").reshape(2, 3, 3, 4096)
+    tv = tile_kv(x, "v").reshape(2, 3, 3, 4096)
+    for T in range(3):
+        for lane in range(64):
+            g, c = divmod(lane, 16)
+            for blk in range(4):
+                for ks in range(2):
+                    run = tk[1, 2, T, 8 * (64 * (2 * blk + ks) + lane):][:8]
+                    want = x[1, 2, 64 * T + 16 * blk + c, 32 * ks + 8 * g: 32 * ks + 8 * g + 8]
+                    assert np.array_equal(run, want)
+            for s in range(2):
+                for nb in range(4):
+                    run = tv[1, 2, T, 8 * (64 * (4 * s + nb) + lane):][:8]
+                    keys = [64 * T + 16 * (2 * s + j // 4) + 4 * g + j % 4 for j in range(8)]
+                    assert np.array_equal(run, x[1, 2, keys, 16 * nb + c])

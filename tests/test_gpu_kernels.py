@@ -199,6 +199,35 @@ def test_decode_attention_against_reference(kv, H, Hkv):
     assert (y.cpu().double() - ref).abs().max() < 2e-5
 
 
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (8, 2), (8, 8)])
+def test_decode_attention_bf16_operands(H, Hkv):
+    """bf16 q and softmax weights (the reference's tl.dot arithmetic).
+
+    Against an fp64 reference on the bf16-rounded q: what remains is the bf16
+    rounding of the unnormalised weights exp(s - m) in [0, 1] (relative error
+    <= 2^-9 each), so |y - ref| <= 2^-8 * max|v| bounds it with margin.
+    """
+    from altxs_amd import ops
+
+    _log(f"attn bf16 operands H={H} Hkv={Hkv}")
+    B, W, L = 3, 2, 768
+    gen = torch.Generator().manual_seed(H * 100 + Hkv)
+    pos = torch.tensor([0, 300, 700], dtype=torch.int32)
+    k = torch.randn(B, Hkv, L, 64, generator=gen).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, L, 64, generator=gen).to(torch.bfloat16)
+    q = torch.randn(B * W, H, 64, generator=gen) * 3
+    y = ops.decode_attn(q.to(DEV), k.to(DEV), v.to(DEV), pos.to(DEV), W=W, ops_bf16=True)
+    qr = (q * 0.125).to(torch.bfloat16).float() * 8.0
+    ref = _attn_ref(qr, k.float(), v.float(), pos, W, None, False)
+    err = (y.cpu().double() - ref).abs().max().item()
+    vmax = v.float().abs().max().item()
+    assert err <= vmax * 2.0 ** -8, err
+    # the fp32-faithful path on the same inputs is an order of magnitude closer
+    y32 = ops.decode_attn(q.to(DEV), k.to(DEV), v.to(DEV), pos.to(DEV), W=W)
+    ref32 = _attn_ref(q, k.float(), v.float(), pos, W, None, False)
+    assert (y32.cpu().double() - ref32).abs().max().item() < 2e-5
+
+
 def test_decode_attention_window_equals_rows():
     """Row at position p computes the same bits as W=1 and inside a W=4 window."""
     from altxs_amd import ops
@@ -210,11 +239,12 @@ def test_decode_attention_window_equals_rows():
     v = torch.randn(B, H, L, 64, generator=gen).to(torch.bfloat16).to(DEV)
     q = (torch.randn(B * 4, H, 64, generator=gen) * 3).to(DEV)
     pos = torch.tensor([253, 510], dtype=torch.int32, device=DEV)  # windows cross chunk edges
-    y4 = ops.decode_attn(q, k, v, pos, W=4, use_xsa=True)
-    for t in range(4):
-        q1 = q.view(B, 4, H, 64)[:, t].contiguous()
-        y1 = ops.decode_attn(q1, k, v, pos + t, W=1, use_xsa=True)
-        assert torch.equal(y1, y4.view(B, 4, -1)[:, t])
+    for ob in (False, True):
+        y4 = ops.decode_attn(q, k, v, pos, W=4, use_xsa=True, ops_bf16=ob)
+        for t in range(4):
+            q1 = q.view(B, 4, H, 64)[:, t].contiguous()
+            y1 = ops.decode_attn(q1, k, v, pos + t, W=1, use_xsa=True, ops_bf16=ob)
+            assert torch.equal(y1, y4.view(B, 4, -1)[:, t])
 
 
 def test_attention_position_error_flag():
