@@ -184,8 +184,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
         if (k0 + 16 * blk + 4 * lg + i >= nkeys) S[blk][i] = -INFINITY;
         mt = fmaxf(mt, S[blk][i]);
       }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+    mt = rows_max(mt);
     const float m_new = fmaxf(m_run, mt);
     const float alpha = __expf(m_run - m_new);
     float ps = 0.f;
@@ -227,8 +226,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
     }
   }
   // l: this lane's keys only; add the four lane groups (fixed butterfly).
-  l_part += __shfl_xor(l_part, 16, WAVE);
-  l_part += __shfl_xor(l_part, 32, WAVE);
+  l_part = rows_sum(l_part);
   // acc row h (lane group 0, register h) is head h for h < G: dims 16*nb + col.
   if (lg == 0) {
 #pragma unroll

@@ -131,6 +131,113 @@ __global__ __launch_bounds__(CDF_THREADS) void cdf_kernel(const float* __restric
   }
 }
 
+// ---- row-parallel softmax -> CDF from per-tile statistics -------------------
+//
+// The LM head leaves, for every (row, 64-column tile), the tile max m_t and
+// s_t = sum exp(l - m_t).  Workgroup (chunk c, row) first forms the row's
+// M = max m_t and S = sum s_t * exp(m_t - M) in a fixed order (identical in
+// every workgroup of the row), then p_i = exp(l_i - M) * (1 / S).  Its CDF offset is
+// the exact integer sum of the counts of all elements before the chunk, which
+// it recomputes itself (integer sums do not depend on order), so no workgroup
+// waits for another.  Its own chunk is scanned and stored.
+
+constexpr int CH_THREADS = 1024;
+constexpr int CH_WAVES = CH_THREADS / WAVE;
+
+__device__ __forceinline__ float block_max_n(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < CH_WAVES; ++i) m = fmaxf(m, red[i]);
+  __syncthreads();
+  return m;
+}
+
+__device__ __forceinline__ float block_sum_n(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float s = red[0];
+#pragma unroll
+  for (int i = 1; i < CH_WAVES; ++i) s += red[i];
+  __syncthreads();
+  return s;
+}
+
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* wred) {
+  v = wave_sum_u32(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) wred[w] = v;
+  __syncthreads();
+  uint32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < CH_WAVES; ++i) s += wred[i];
+  __syncthreads();
+  return s;
+}
+
+template <int EPT>
+__global__ __launch_bounds__(CH_THREADS) void cdf_chunk_kernel(const float* __restrict__ logits,
+                                                                const float2* __restrict__ stats,
+                                                                int V, int chunk,
+                                                                float* __restrict__ probs,
+                                                                uint32_t* __restrict__ cum) {
+  __shared__ float red[CH_WAVES];
+  __shared__ uint32_t wred[CH_WAVES];
+  const int64_t row = blockIdx.y;
+  const int c0 = blockIdx.x * chunk;
+  const int t = threadIdx.x;
+  const float* x = logits + row * (int64_t)V;
+  const int ntile = V / 64;
+  const float2* st = stats + row * (int64_t)ntile;
+  // this thread's chunk elements (issued first)
+  float v[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int i = c0 + t * EPT + k;
+    v[k] = i < c0 + chunk ? x[i] : 0.f;
+  }
+  // M, S over the tiles (fixed order: thread-strided, wave butterfly, waves in order)
+  float mt = -INFINITY;
+  for (int i = t; i < ntile; i += CH_THREADS) mt = fmaxf(mt, st[i].x);
+  const float M = block_max_n(mt, red);
+  float sp = 0.f;
+  for (int i = t; i < ntile; i += CH_THREADS) {
+    const float2 q = st[i];
+    sp += q.y * __expf(q.x - M);
+  }
+  const float S = block_sum_n(sp, red);
+  const float iS = 1.f / S;
+  // CDF offset: counts of every element before the chunk (exact integers)
+  uint32_t before = 0;
+  for (int i = t; i < c0; i += CH_THREADS) before += scale_count(__expf(x[i] - M) * iS);
+  const uint32_t offset = block_sum_u32(before, wred);
+  // own chunk
+  uint32_t f[EPT];
+  uint32_t tot = 0;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int i = c0 + t * EPT + k;
+    const float p = __expf(v[k] - M) * iS;
+    if (probs && i < c0 + chunk) probs[row * (int64_t)V + i] = p;
+    f[k] = i < c0 + chunk ? scale_count(p) : 0u;
+    tot += f[k];
+  }
+  uint32_t run = offset + block_excl_scan(tot, wred);
+  uint32_t* co = cum + row * (int64_t)(V + 1);
+  if (c0 == 0 && t == 0) co[0] = 0u;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int i = c0 + t * EPT + k;
+    run += f[k];
+    if (i < c0 + chunk) co[i + 1] = run;
+  }
+}
+
 template <bool FROM_LOGITS>
 hipError_t launch_cdf(const float* in, int64_t rows, int V, int flags, float* probs,
                       uint32_t* cum, hipStream_t s) {
@@ -154,6 +261,20 @@ hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, boo
   if (rows <= 0) return hipSuccess;
   return from_logits ? launch_cdf<true>(in, rows, V, flags, probs, cum, s)
                      : launch_cdf<false>(in, rows, V, flags, probs, cum, s);
+}
+
+hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int64_t rows, int V,
+                                  float* probs, uint32_t* cum, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (V % 64) return hipErrorInvalidValue;
+  const int chunk = V < 2048 ? V : 2048;
+  if (V % chunk) return hipErrorInvalidValue;
+  dim3 grid((unsigned)(V / chunk), (unsigned)rows), block(CH_THREADS);
+  if (chunk > CH_THREADS)
+    hipLaunchKernelGGL(cdf_chunk_kernel<2>, grid, block, 0, s, logits, stats, V, chunk, probs, cum);
+  else
+    hipLaunchKernelGGL(cdf_chunk_kernel<1>, grid, block, 0, s, logits, stats, V, chunk, probs, cum);
+  return hipGetLastError();
 }
 
 extern "C" int32_t altxs_scale_cum(const float* probs, int64_t rows, int64_t V, uint32_t* cum,

@@ -1,28 +1,34 @@
 // Dequant-fused MFMA GEMM: Y[r, n] = sum_k A[r, k] * W[n, k], W packed as
-// symmetric group-64 codes with fp16 scales (see include/altxs.h, AltxsQTensor).
+// symmetric group-64 codes with fp16 scales (include/altxs.h, AltxsQTensor).
 //
-// Tiling.  A workgroup owns one 16-row M tile and NB 16-column n-blocks; its
-// NB*KS waves split the work as (n-block, K-slice): wave w computes n-block
-// w % NB over the K-slice w / NB.  Every wave issues the loads of its weight
-// blocks (16 rows x 256 k each, <= 2 in flight) before anything else, so the
-// HBM latency overlaps the activation prologue.  In the tiled layout lane l of
-// a wave owns the 64 codes of row (l % 16) at k = 32*s + 8*(l / 16) + i
-// (s, i < 8) -- exactly the B operand of v_mfma_f32_16x16x32_{bf16,f16} for the
-// block's eight k-steps -- so a block arrives as one or two 16-byte loads per
-// lane.  Codes become (c - (2^b-1)/2), exact in bf16/fp16; each 64-wide group's
-// fp32 partial is scaled by its fp16 scale.
+// The unit of work is a *task*: one 16-row tile (rows m0 .. m0+15) and a
+// strided list of column tiles nt = nt0, nt0 + nstep, ... (16*NB columns
+// each).  A task runs on one workgroup of NB*KS waves; wave w computes
+// n-block w % NB of the current column tile over K-slice w / NB.  Tasks are
+// placed by a kernel (one per workgroup, or several per workgroup when a
+// persistent team walks a stage), so the same code serves every launch shape.
 //
-// A operand: either staged in LDS by a prologue functor (RMSNorm, residual
-// mixes and skips fused there) or, for plain inputs, loaded by each lane
-// straight into MFMA registers.
+// Per column tile every wave issues the loads of its first two weight blocks
+// (16 rows x 256 k each) before anything else -- for the first tile even
+// before the A prologue -- so HBM latency overlaps the activation work.  In the
+// tiled layout lane l of a wave owns the 64 codes of row (l % 16) at
+// k = 32*s + 8*(l / 16) + i (s, i < 8) -- exactly the B operand of
+// v_mfma_f32_16x16x32_{bf16,f16} for the block's eight k-steps -- so a block
+// arrives as one or two 16-byte loads per lane.  Codes become (c - (2^b-1)/2),
+// exact in bf16/fp16; each 64-wide group's fp32 partial is scaled by its fp16
+// scale.
+//
+// A operand: staged once per task in LDS by a prologue functor (RMSNorm,
+// residual mixes and skips fused there) or, for plain inputs, loaded by each
+// lane straight into MFMA registers.
 //
 // Reduction and determinism.  Inside a wave: the MFMA's fixed internal order,
 // then groups in increasing k.  Across the KS K-slices: partial tiles go to LDS
-// and are added in slice order.  The order depends only on K and the kernel's
-// (NB, KS), never on the number of rows, so results are bit-identical for any
-// batch or window size.
+// and are added in slice order.  The order depends only on K and (NB, KS),
+// never on the number of rows or on how tasks are placed, so results are
+// bit-identical for any batch, window size or launch shape.
 //
-// Epilogue: a tile functor.  Epi::prefetch() runs first (issue loads of
+// Epilogue: a functor.  Epi::prefetch() runs before the MFMAs (issue loads of
 // residuals, positions, RoPE tables early); Epi::apply() gets the reduced
 // 16 x (16*NB) fp32 tile in LDS and runs on all threads.
 #pragma once
@@ -50,20 +56,7 @@ struct QT {
 __host__ __device__ constexpr int lds_stride(int K, int am) { return K + (am == A_F32 ? 4 : 8); }
 __host__ __device__ constexpr int a_esz(int am) { return am == A_F32 ? 4 : 2; }
 
-// Store one fp32 activation value into an LDS A tile in the mode's format.
-template <int AM>
-__device__ __forceinline__ void a_store(void* As, int row, int col, int K, float v) {
-  if constexpr (AM == A_F32) {
-    ((float*)As)[row * lds_stride(K, AM) + col] = v;
-  } else if constexpr (AM == A_BF16) {
-    ((uint16_t*)As)[row * lds_stride(K, AM) + col] = f32_to_bf16(v);
-  } else {
-    _Float16 h = (_Float16)v;
-    ((uint16_t*)As)[row * lds_stride(K, AM) + col] = __builtin_bit_cast(uint16_t, h);
-  }
-}
-
-// Store four consecutive fp32 values (col % 4 == 0).
+// Store four consecutive fp32 values (col % 4 == 0) into an LDS A tile.
 template <int AM>
 __device__ __forceinline__ void a_store4(void* As, int row, int col, int K, const float (&v)[4]) {
   if constexpr (AM == A_F32) {
@@ -267,8 +260,9 @@ __device__ __forceinline__ void compute_blk(const Blk<BITS, AM, ADIRECT>& b, con
 // Prologue that stages nothing (A comes straight from global memory).
 struct ProNone {
   static constexpr bool kStage = false;
+  static constexpr size_t kScratch = 0;
   template <int AM, int NT>
-  __device__ void stage(void*, int, int, int, int) const {}
+  __device__ void stage(void*, void*, int, int, int, int, bool) const {}
 };
 
 template <int NB, int KS>
@@ -279,73 +273,82 @@ struct TileCfg {
   static constexpr int CS = NCOL + 1;  // padded C tile stride (floats)
 };
 
-// LDS layout: [A tile (if staged)] [C partial tiles: KS x 16 x CS floats]
-template <int NB, int KS>
-__host__ __device__ constexpr size_t c_tile_bytes() {
-  return (size_t)KS * 16 * TileCfg<NB, KS>::CS * 4;
+// LDS of a task: [A tile (if staged)] [C partial tiles: KS x 16 x CS floats]
+// [prologue scratch].
+template <int AM, int NB, int KS, class Pro>
+__host__ __device__ constexpr size_t task_lds_bytes(int K) {
+  return (Pro::kStage ? (size_t)16 * lds_stride(K, AM) * a_esz(AM) : 0) +
+         (size_t)KS * 16 * TileCfg<NB, KS>::CS * 4 + Pro::kScratch;
 }
 
+// One task: rows [m0, m0+16) x column tiles nt0, nt0 + nstep, ... < ntiles.
 template <int BITS, int AM, int NB, int KS, class Pro, class Epi>
-__global__ __launch_bounds__(64 * NB * KS) void qgemm_kernel(
-    QT w, int R, int64_t codes_stride, int64_t scales_stride, ADirect ad, Pro pro, Epi epi) {
+__device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, int nstep,
+                                          const ADirect& ad, const Pro& pro, const Epi& epi,
+                                          unsigned char* smem, int batch = 0) {
   using Cfg = TileCfg<NB, KS>;
   constexpr bool STAGE = Pro::kStage;
   constexpr bool ADIRECT = !STAGE;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int batch = blockIdx.z;
-  QT wb = w;
-  wb.codes += batch * codes_stride;
-  wb.scales += batch * scales_stride;
-  const int m0 = blockIdx.y * 16;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nbi = wave % NB, ks = wave / NB;
-  const int nb = blockIdx.x * NB + nbi;
-  const bool active = nb * 16 < w.N;
+  const int ntiles = (w.N + Cfg::NCOL - 1) / Cfg::NCOL;
   const int KB = w.K >> 8;
   const int kb0 = ks * (KB / KS), kb1 = kb0 + KB / KS;  // host guarantees KB % KS == 0
   void* As = smem;
-  float* Cp = (float*)(smem + (STAGE ? (size_t)16 * lds_stride(w.K, AM) * a_esz(AM) : 0));
+  const size_t a_bytes = STAGE ? (size_t)16 * lds_stride(w.K, AM) * a_esz(AM) : 0;
+  float* Cp = (float*)(smem + a_bytes);
+  void* scratch = smem + a_bytes + (size_t)KS * 16 * Cfg::CS * 4;
 
-  const auto pre = epi.template prefetch<Cfg>(m0, R, batch);
   Blk<BITS, AM, ADIRECT> b0, b1;
-  if (active) {
-    if (kb0 < kb1) load_blk(b0, wb, nb, kb0, lane, ad, m0, R, batch);
-    if (kb0 + 1 < kb1) load_blk(b1, wb, nb, kb0 + 1, lane, ad, m0, R, batch);
-  }
+  auto issue = [&](int nt) {
+    const int nb = nt * NB + nbi;
+    if (nb * 16 < w.N) {
+      if (kb0 < kb1) load_blk(b0, w, nb, kb0, lane, ad, m0, R, batch);
+      if (kb0 + 1 < kb1) load_blk(b1, w, nb, kb0 + 1, lane, ad, m0, R, batch);
+    }
+  };
+  if (nt0 < ntiles) issue(nt0);
   if constexpr (STAGE) {
-    pro.template stage<AM, Cfg::THREADS>(As, m0, R, w.K, batch);
+    pro.template stage<AM, Cfg::THREADS>(As, scratch, m0, R, w.K, batch, nt0 == 0);
     __syncthreads();
   }
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (active) {
-    for (int kb = kb0; kb < kb1; kb += 2) {
-      compute_blk(b0, As, w.K, kb, lane, acc);
-      if (kb + 2 < kb1) load_blk(b0, wb, nb, kb + 2, lane, ad, m0, R, batch);
-      if (kb + 1 < kb1) {
-        compute_blk(b1, As, w.K, kb + 1, lane, acc);
-        if (kb + 3 < kb1) load_blk(b1, wb, nb, kb + 3, lane, ad, m0, R, batch);
+  for (int nt = nt0; nt < ntiles; nt += nstep) {
+    const int n0 = nt * Cfg::NCOL;
+    const int nb = nt * NB + nbi;
+    const bool active = nb * 16 < w.N;
+    const auto pre = epi.template prefetch<Cfg>(m0, n0, R, batch);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (active) {
+      for (int kb = kb0; kb < kb1; kb += 2) {
+        compute_blk(b0, As, w.K, kb, lane, acc);
+        if (kb + 2 < kb1) load_blk(b0, w, nb, kb + 2, lane, ad, m0, R, batch);
+        if (kb + 1 < kb1) {
+          compute_blk(b1, As, w.K, kb + 1, lane, acc);
+          if (kb + 3 < kb1) load_blk(b1, w, nb, kb + 3, lane, ad, m0, R, batch);
+        }
       }
     }
-  }
-  // partial tile of this wave -> LDS slice ks (MFMA layout: rows 4*(l/16)+i, col l%16)
-  {
-    float* C = Cp + (size_t)ks * 16 * Cfg::CS;
-    const int col = nbi * 16 + (lane & 15);
+    if (nt + nstep < ntiles) issue(nt + nstep);  // next tile's weights fly during the epilogue
+    {  // partial tile of this wave -> LDS slice ks (MFMA layout: rows 4*(l/16)+i, col l%16)
+      float* C = Cp + (size_t)ks * 16 * Cfg::CS;
+      const int col = nbi * 16 + (lane & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) C[(4 * (lane >> 4) + i) * Cfg::CS + col] = acc[i];
-  }
-  __syncthreads();
-  if constexpr (KS > 1) {  // fixed-order reduction of the K-slices into slice 0
-    for (int e = threadIdx.x; e < 16 * Cfg::NCOL; e += Cfg::THREADS) {
-      const int r = e / Cfg::NCOL, c = e % Cfg::NCOL;
-      float s = Cp[r * Cfg::CS + c];
-#pragma unroll
-      for (int k = 1; k < KS; ++k) s += Cp[(size_t)k * 16 * Cfg::CS + r * Cfg::CS + c];
-      Cp[r * Cfg::CS + c] = s;
+      for (int i = 0; i < 4; ++i) C[(4 * (lane >> 4) + i) * Cfg::CS + col] = acc[i];
     }
     __syncthreads();
+    if constexpr (KS > 1) {  // fixed-order reduction of the K-slices into slice 0
+      for (int e = threadIdx.x; e < 16 * Cfg::NCOL; e += Cfg::THREADS) {
+        const int r = e / Cfg::NCOL, c = e % Cfg::NCOL;
+        float s = Cp[r * Cfg::CS + c];
+#pragma unroll
+        for (int k = 1; k < KS; ++k) s += Cp[(size_t)k * 16 * Cfg::CS + r * Cfg::CS + c];
+        Cp[r * Cfg::CS + c] = s;
+      }
+      __syncthreads();
+    }
+    epi.template apply<Cfg>(Cp, pre, As, m0, n0, R, batch);
+    __syncthreads();  // Cp (and As for epilogues that read it) are reused by the next tile
   }
-  epi.template apply<Cfg>(Cp, pre, m0, blockIdx.x * Cfg::NCOL, R, batch);
 }
 
 // ---- generic epilogue: y[batch][r][n] = acc -----------------------------------
@@ -355,9 +358,9 @@ struct EpiStore {
   int64_t y_batch_stride;
   struct Pre {};
   template <class Cfg>
-  __device__ Pre prefetch(int, int, int) const { return {}; }
+  __device__ Pre prefetch(int, int, int, int) const { return {}; }
   template <class Cfg, class P>
-  __device__ void apply(const float* C, const P&, int m0, int n0, int R, int batch) const {
+  __device__ void apply(const float* C, const P&, const void*, int m0, int n0, int R, int batch) const {
     for (int e = threadIdx.x; e < 16 * Cfg::NCOL; e += Cfg::THREADS) {
       const int r = e / Cfg::NCOL, c = e % Cfg::NCOL;
       if (m0 + r < R && n0 + c < N)
@@ -366,14 +369,40 @@ struct EpiStore {
   }
 };
 
-// Launch helper: sets the dynamic LDS limit once per instantiation.
+// A grid of tasks: blockIdx.y = row tile, blockIdx.x = first column tile,
+// stride gridDim.x; blockIdx.z = batch (tensors at fixed strides).
 template <int BITS, int AM, int NB, int KS, class Pro, class Epi>
-hipError_t launch_qgemm(const QT& w, int R, int batch, int64_t codes_stride,
-                        int64_t scales_stride, const ADirect& ad, const Pro& pro, const Epi& epi,
-                        hipStream_t s) {
-  auto kfn = qgemm_kernel<BITS, AM, NB, KS, Pro, Epi>;
-  const size_t lds = (Pro::kStage ? (size_t)16 * lds_stride(w.K, AM) * a_esz(AM) : 0) +
-                     c_tile_bytes<NB, KS>();
+__global__ __launch_bounds__(64 * NB * KS) void gemm_kernel(QT w, int R, int64_t codes_stride,
+                                                            int64_t scales_stride, ADirect ad,
+                                                            Pro pro, Epi epi) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int batch = blockIdx.z;
+  QT wb = w;
+  wb.codes += batch * codes_stride;
+  wb.scales += batch * scales_stride;
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id.  When the
+  // column-task count is a multiple of 8, renumber so that every row tile of a
+  // column task lands on the same XCD: its weights then come into that XCD's
+  // L2 once instead of once per row tile.
+  int cx = blockIdx.x, ry = blockIdx.y;
+  if (gridDim.x % 8 == 0) {
+    const int bid = blockIdx.x + gridDim.x * blockIdx.y;
+    const int rest = bid / 8;
+    ry = rest % gridDim.y;
+    cx = (rest / gridDim.y) * 8 + bid % 8;
+  }
+  gemm_task<BITS, AM, NB, KS>(wb, R, ry * 16, cx, gridDim.x, ad, pro, epi, smem, batch);
+}
+
+// Launch helper: column tiles are spread over `col_wgs` workgroups per row tile
+// (0 = one workgroup per column tile).  Sets the dynamic LDS limit once per
+// instantiation.
+template <int BITS, int AM, int NB, int KS, class Pro, class Epi>
+hipError_t launch_gemm(const QT& w, int R, int batch, int64_t codes_stride, int64_t scales_stride,
+                       const ADirect& ad, const Pro& pro, const Epi& epi, int col_wgs,
+                       hipStream_t s) {
+  auto kfn = gemm_kernel<BITS, AM, NB, KS, Pro, Epi>;
+  const size_t lds = task_lds_bytes<AM, NB, KS, Pro>(w.K);
   static size_t configured = 0;
   if (lds > 65536 && lds > configured) {
     hipError_t e = hipFuncSetAttribute((const void*)kfn,
@@ -381,36 +410,56 @@ hipError_t launch_qgemm(const QT& w, int R, int batch, int64_t codes_stride,
     if (e != hipSuccess) return e;
     configured = lds;
   }
-  dim3 grid((unsigned)((w.N + 16 * NB - 1) / (16 * NB)), (unsigned)((R + 15) / 16), (unsigned)batch);
+  const int ntiles = (w.N + 16 * NB - 1) / (16 * NB);
+  const int cw = (col_wgs <= 0 || col_wgs > ntiles) ? ntiles : col_wgs;
+  dim3 grid((unsigned)cw, (unsigned)((R + 15) / 16), (unsigned)batch);
   hipLaunchKernelGGL(kfn, grid, dim3(TileCfg<NB, KS>::THREADS), lds, s, w, R, codes_stride,
                      scales_stride, ad, pro, epi);
   return hipGetLastError();
 }
 
-// Dispatch on the runtime bit width and K-split.  KS is the largest of
-// {4, 2, 1} that is <= ks_max and divides K/256.
-template <int AM, int NB, int KSMAX, class Pro, class Epi>
-hipError_t launch_qgemm_rt(int bits, const QT& w, int R, int batch, int64_t codes_stride,
-                           int64_t scales_stride, const ADirect& ad, const Pro& pro,
-                           const Epi& epi, hipStream_t s) {
-  const int KB = w.K >> 8;
-  auto go = [&](auto ks_tag) -> hipError_t {
-    constexpr int KS = decltype(ks_tag)::value;
-    switch (bits) {
-      case 2: return launch_qgemm<2, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, s);
-      case 3: return launch_qgemm<3, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, s);
-      case 4: return launch_qgemm<4, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, s);
-      case 6: return launch_qgemm<6, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, s);
-      default: return hipErrorInvalidValue;
-    }
-  };
-  if constexpr (KSMAX >= 4) {
-    if (KB % 4 == 0) return go(std::integral_constant<int, 4>{});
+// Dispatch on the runtime bit width.
+template <int AM, int NB, int KS, class Pro, class Epi>
+hipError_t launch_gemm_bits(int bits, const QT& w, int R, int batch, int64_t codes_stride,
+                            int64_t scales_stride, const ADirect& ad, const Pro& pro,
+                            const Epi& epi, int col_wgs, hipStream_t s) {
+  switch (bits) {
+    case 2: return launch_gemm<2, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+    case 3: return launch_gemm<3, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+    case 4: return launch_gemm<4, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+    case 6: return launch_gemm<6, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+    default: return hipErrorInvalidValue;
   }
-  if constexpr (KSMAX >= 2) {
-    if (KB % 2 == 0) return go(std::integral_constant<int, 2>{});
+}
+
+// 4-wave task shapes: (NB, KS) in {(4,1), (2,2), (1,4)}.  The K-split is the
+// largest KS <= ks_max that divides K/256 (a property of the tensor, so every
+// launch shape of a stage uses the same reduction order).
+__host__ __device__ constexpr int pick_ks(int K, int ks_max) {
+  return (ks_max >= 4 && (K >> 8) % 4 == 0) ? 4 : (ks_max >= 2 && (K >> 8) % 2 == 0) ? 2 : 1;
+}
+
+template <int AM, class Pro, class Epi>
+hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect& ad,
+                        const Pro& pro, const Epi& epi, int col_wgs, hipStream_t s) {
+  switch (pick_ks(w.K, ks_max)) {
+    case 4: return launch_gemm_bits<AM, 1, 4>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
+    case 2: return launch_gemm_bits<AM, 2, 2>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
+    default: return launch_gemm_bits<AM, 4, 1>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
   }
-  return go(std::integral_constant<int, 1>{});
+}
+
+// Run a task with the bit width chosen at run time (uniform branch).
+template <int AM, int NB, int KS, class Pro, class Epi>
+__device__ __forceinline__ void gemm_task_bits(int bits, const QT& w, int R, int m0, int nt0,
+                                               int nstep, const ADirect& ad, const Pro& pro,
+                                               const Epi& epi, unsigned char* smem) {
+  switch (bits) {
+    case 2: gemm_task<2, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
+    case 3: gemm_task<3, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
+    case 4: gemm_task<4, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
+    default: gemm_task<6, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
+  }
 }
 
 }  // namespace altxs

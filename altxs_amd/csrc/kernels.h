@@ -6,5 +6,10 @@
 hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, bool from_logits,
                             float* probs, uint32_t* cum, hipStream_t s);
 
+// Row-parallel softmax -> CDF from the LM head's per-64-column tile statistics
+// (no renormalisation); V % 64 == 0.
+hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int64_t rows, int V,
+                                  float* probs, uint32_t* cum, hipStream_t s);
+
 struct AltxsAttnArgs;
 hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s);

@@ -2,7 +2,7 @@
 // and interop path), the fused dequant GEMM/GEMV, and its multi-tensor
 // streaming form used to measure HBM throughput over many distinct matrices.
 #include "common.h"
-#include "qgemm.h"
+#include "gemm.h"
 
 using namespace altxs;
 
@@ -56,8 +56,15 @@ hipError_t run_gemm(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss
                     int64_t rows, float* y, hipStream_t s) {
   QT q = to_qt(w);
   EpiStore epi{y, q.N, rows * q.N};
-  return launch_qgemm_rt<AM, 2, 4>(w->bits, q, (int)rows, (int)count, cs, ss,
-                                   ADirect{x, 0}, ProNone{}, epi, s);
+  const int KB = (int)(w->K / 256);
+  if (KB % 4 == 0)
+    return launch_gemm_bits<AM, 2, 4>(w->bits, q, (int)rows, (int)count, cs, ss, ADirect{x, 0},
+                                      ProNone{}, epi, 0, s);
+  if (KB % 2 == 0)
+    return launch_gemm_bits<AM, 2, 2>(w->bits, q, (int)rows, (int)count, cs, ss, ADirect{x, 0},
+                                      ProNone{}, epi, 0, s);
+  return launch_gemm_bits<AM, 2, 1>(w->bits, q, (int)rows, (int)count, cs, ss, ADirect{x, 0},
+                                    ProNone{}, epi, 0, s);
 }
 
 int32_t gemm_common(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss, const void* x,

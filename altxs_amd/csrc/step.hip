@@ -4,7 +4,7 @@
 //   QKV  : prologue = U-Net skip + resid_mix + RMSNorm*ln_scale (+ sparse-gate
 //          logits), MFMA dequant GEMM, epilogue = per-head QK-RMSNorm, RoPE,
 //          q_gain, K/V written into the cache at pos+t.
-//   ATTN : attn.hip (split over fixed 256-key chunks, fixed-order merge).
+//   ATTN : attn.hip (fixed 64-key tiles, per-wave online softmax, fixed-order merge).
 //   O    : out-projection; epilogue = attention residual (or parallel lane term).
 //   UP   : prologue = RMSNorm*ln_scale of the attention output; epilogue =
 //          LeakyReLU(0.5)^2.
@@ -24,7 +24,7 @@
 
 #include "common.h"
 #include "kernels.h"
-#include "qgemm.h"
+#include "gemm.h"
 
 using namespace altxs;
 
@@ -37,6 +37,11 @@ __device__ __forceinline__ float lerp_t(float start, float end, float w) {
   return (fabsf(w) < 0.5f) ? start + w * (end - start) : end - (end - start) * (1.f - w);
 }
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+// tanh(x) = sign(x) * (1 - 2 / (exp(2|x|) + 1)); absolute error ~1e-7.
+__device__ __forceinline__ float tanh_fast(float x) {
+  const float e = __expf(2.f * fabsf(x));
+  return copysignf(1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f), x);
+}
 
 // ---- embedding (+ SmearGate) ------------------------------------------------
 
@@ -87,12 +92,18 @@ struct EmbedP {
   const float* smear_lambda;
   float* x0;  // [R, D]
   int32_t* err;
+  int* sync;  // step counters, zeroed here (this is the step's first kernel)
+  int nsync;
+  const float* mix0;  // resid_mix of slot 0's layer [2, D]
+  float* xin0;        // slot 0's x_in = m0*x0 + m1*x0 (sequential, no skip)
 };
 
 constexpr int MAX_RUNS = 4;  // D <= 64 lanes * 4 runs * 8 = 2048
 
 __global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
   const int r = blockIdx.x, lane = threadIdx.x;
+  if (r == 0)
+    for (int i = lane; i < a.nsync; i += 64) a.sync[i] = 0;
   const int b = r / a.W, t = r % a.W;
   auto tok_at = [&](int tt) {
     int tk = a.tokens[(int64_t)b * a.W + tt];
@@ -161,8 +172,13 @@ __global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
     const int run = lane + 64 * j;
     if (run >= nruns) continue;
     float* xo = a.x0 + (int64_t)r * a.D + 8 * run;
+    float* xi = a.xin0 + (int64_t)r * a.D + 8 * run;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xo[i] = x[j][i] * inv;
+    for (int i = 0; i < 8; ++i) {
+      const float v = x[j][i] * inv;
+      xo[i] = v;
+      xi[i] = a.mix0[8 * run + i] * v + a.mix0[a.D + 8 * run + i] * v;
+    }
     if (t == a.W - 1) {
       float* co = a.cand_raw + (int64_t)b * a.D + 8 * run;
 #pragma unroll
@@ -180,173 +196,136 @@ __global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
 constexpr int PTPR = 16;                  // prologue threads per row
 constexpr int PMAXJ = 512 / 4 / PTPR;     // float4 chunks per lane (D <= 512)
 
-__device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
-  return v;
-}
 
-// Attention-side input of a slot: skip, resid_mix, RMSNorm * ln_scale.
-struct ProQKV {
-  static constexpr bool kStage = true;
-  const float* x;      // slot input (x, or lane0 for a parallel slot)
-  const float* x0;     // embedding output
-  const float* skip;   // popped encoder output or NULL
-  const float* skip_w; // [D] row of skip_weights
-  const float* skip_g; // [D] row of skip_gates or NULL
-  const float* mix;    // [2, D]
-  float* base_out;     // x_in (sequential) / lane0 after skip (parallel); tile x==0 writes
-  const float* gate_w; // [H, gw] or NULL
-  float* gate_out;     // [R, H]; tile x==h (< H) writes head h
-  float ln_scale, eps, gate_scale;
-  int D, H, gw, parallel;
-  template <int AM, int NT>
-  __device__ void stage(void* As, int m0, int R, int K, int) const {
-    constexpr int RPP = NT / PTPR < 16 ? NT / PTPR : 16;  // rows per pass
-    const int t = threadIdx.x;
-    if (t >= RPP * PTPR) return;
-    const int li = t % PTPR;
-    const int nch = D >> 2;
-    const bool writer = blockIdx.x == 0;
-    const bool gater = gate_w && (int)blockIdx.x < H;
-    // this lane's gate weights (the gate reads only the first gw <= 16 features)
-    float gwl[4] = {0.f, 0.f, 0.f, 0.f};
-    if (gater) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (4 * li + e < gw) gwl[e] = gate_w[blockIdx.x * gw + 4 * li + e];
-    }
-    for (int row = t / PTPR; row < 16; row += RPP) {
-      const int r = m0 + row;
-      float in[PMAXJ][4];
-      if (r >= R) {
-#pragma unroll
-        for (int j = 0; j < PMAXJ; ++j) {
-          const int c = li + PTPR * j;
-          if (c < nch) {
-            const float z[4] = {0.f, 0.f, 0.f, 0.f};
-            a_store4<AM>(As, row, 4 * c, K, z);
-          }
-        }
-        continue;
-      }
-      // every load of the row is issued here, before any use
-      f32x4 xv[PMAXJ], x0v[PMAXJ], sv[PMAXJ], m0v[PMAXJ], m1v[PMAXJ], swv[PMAXJ], sgv[PMAXJ];
-#pragma unroll
-      for (int j = 0; j < PMAXJ; ++j) {
-        const int c = li + PTPR * j;
-        if (c < nch) {
-          xv[j] = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
-          x0v[j] = *(const f32x4*)(x0 + (int64_t)r * D + 4 * c);
-          m0v[j] = *(const f32x4*)(mix + 4 * c);
-          m1v[j] = *(const f32x4*)(mix + D + 4 * c);
-          if (skip) {
-            sv[j] = *(const f32x4*)(skip + (int64_t)r * D + 4 * c);
-            swv[j] = *(const f32x4*)(skip_w + 4 * c);
-            if (skip_g) sgv[j] = *(const f32x4*)(skip_g + 4 * c);
-          }
-        }
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < PMAXJ; ++j) {
-        const int c = li + PTPR * j;
-        if (c >= nch) continue;
-        float bs[4] = {xv[j][0], xv[j][1], xv[j][2], xv[j][3]};
-        if (skip) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float sc = swv[j][e] * sv[j][e];
-            if (skip_g) bs[e] = lerp_t(sc, bs[e], sigmoidf(sgv[j][e]));
-            else bs[e] = bs[e] + sc;
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          in[j][e] = m0v[j][e] * bs[e] + m1v[j][e] * x0v[j][e];
-          ss += in[j][e] * in[j][e];
-        }
-        if (writer) {
-          f32x4 o;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = parallel ? bs[e] : in[j][e];
-          *(f32x4*)(base_out + (int64_t)r * D + 4 * c) = o;
-        }
-      }
-      ss = row16_sum(ss);
-      const float inv = rsqrtf(ss / (float)D + eps);
-      float gpart = 0.f;
-#pragma unroll
-      for (int j = 0; j < PMAXJ; ++j) {
-        const int c = li + PTPR * j;
-        if (c >= nch) continue;
-        float n[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          n[e] = (in[j][e] * inv) * ln_scale;
-          if (gater && j == 0) gpart += n[e] * gwl[e];  // zero weights past gw
-        }
-        a_store4<AM>(As, row, 4 * c, K, n);
-      }
-      if (gater) {
-        const float dot = row16_sum(gpart);
-        if (li == 0) gate_out[(int64_t)r * H + blockIdx.x] = sigmoidf(gate_scale * dot);
-      }
-    }
-  }
-};
-
-// RMSNorm (* scale) of rows of x (MLP input, final norm; final may average lanes).
+// RMSNorm (* scale) of 16 rows of x staged as the A tile.  Inputs of the
+// attention side (the QKV prologue) also carry the sparse attention gate
+// (model.py:854-862): the task that owns column tile 0 (`first`) forms
+// sigmoid(gate_scale * n[:gw] . W_gate[h]) for every head from the normalised
+// row.  The final norm before the LM head may average the two parallel lanes.
 struct ProNorm {
   static constexpr bool kStage = true;
+  static constexpr size_t kScratch = 0;
   const float* x;
   const float* x2;  // second lane (final parallel "mean") or NULL
   int lane_mode;    // 0: x, 1: 0.5*(x + x2)
   float scale, eps;
   int D;
+  const float* gate_w = nullptr;  // [H, gw] or NULL
+  float* gate_out = nullptr;      // [R, H]
+  float gate_scale = 0.f;
+  int H = 0, gw = 0;
   template <int AM, int NT>
-  __device__ void stage(void* As, int m0, int R, int K, int) const {
-    constexpr int RPP = NT / PTPR < 16 ? NT / PTPR : 16;
-    const int t = threadIdx.x;
-    if (t >= RPP * PTPR) return;
-    const int li = t % PTPR;
+  __device__ void stage(void* As, void*, int m0, int R, int K, int, bool first) const {
+    static_assert(NT == 16 * PTPR, "one row per 16 lanes, 16 rows per task");
+    constexpr int HMAX = 8;  // D <= 512 -> H <= 8
+    const int t = threadIdx.x, row = t / PTPR, li = t % PTPR;
+    const int r = m0 + row;
     const int nch = D >> 2;
-    for (int row = t / PTPR; row < 16; row += RPP) {
-      const int r = m0 + row;
-      f32x4 v[PMAXJ], v2[PMAXJ];
+    f32x4 v[PMAXJ], v2[PMAXJ];
 #pragma unroll
-      for (int j = 0; j < PMAXJ; ++j) {
-        const int c = li + PTPR * j;
-        if (c < nch && r < R) {
-          v[j] = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
-          if (lane_mode == 1) v2[j] = *(const f32x4*)(x2 + (int64_t)r * D + 4 * c);
-        }
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < PMAXJ; ++j) {
-        const int c = li + PTPR * j;
-        if (c >= nch) continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float y = r < R ? v[j][e] : 0.f;
-          if (lane_mode == 1 && r < R) y = 0.5f * (v[j][e] + v2[j][e]);
-          v[j][e] = y;
-          ss += y * y;
-        }
-      }
-      ss = row16_sum(ss);
-      const float inv = r < R ? rsqrtf(ss / (float)D + eps) : 0.f;
-#pragma unroll
-      for (int j = 0; j < PMAXJ; ++j) {
-        const int c = li + PTPR * j;
-        if (c >= nch) continue;
-        float n[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) n[e] = (v[j][e] * inv) * scale;
-        a_store4<AM>(As, row, 4 * c, K, n);
+    for (int j = 0; j < PMAXJ; ++j) {
+      const int c = li + PTPR * j;
+      if (c < nch && r < R) {
+        v[j] = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
+        if (lane_mode == 1) v2[j] = *(const f32x4*)(x2 + (int64_t)r * D + 4 * c);
       }
     }
+    const bool gating = first && gate_w;
+    float gwv[HMAX][4];
+    if (gating) {  // gate of head h reads features [0, gw), gw <= 16: lanes 0-3, chunk 0
+#pragma unroll
+      for (int h = 0; h < HMAX; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          gwv[h][e] = (h < H && 4 * li + e < gw) ? gate_w[h * gw + 4 * li + e] : 0.f;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < PMAXJ; ++j) {
+      const int c = li + PTPR * j;
+      if (c >= nch) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float y = r < R ? v[j][e] : 0.f;
+        if (lane_mode == 1 && r < R) y = 0.5f * (v[j][e] + v2[j][e]);
+        v[j][e] = y;
+        ss += y * y;
+      }
+    }
+    ss = row16_sum(ss);
+    const float inv = r < R ? rsqrtf(ss / (float)D + eps) : 0.f;
+    float n0[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < PMAXJ; ++j) {
+      const int c = li + PTPR * j;
+      if (c >= nch) continue;
+      float n[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) n[e] = (v[j][e] * inv) * scale;
+      if (j == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) n0[e] = n[e];
+      }
+      a_store4<AM>(As, row, 4 * c, K, n);
+    }
+    if (gating) {
+      float part[HMAX];
+#pragma unroll
+      for (int h = 0; h < HMAX; ++h) {
+        part[h] = 0.f;
+        if (li < 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part[h] += n0[e] * gwv[h][e];
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < HMAX; ++h) part[h] = row16_sum(part[h]);
+      if (li < H && r < R) {
+        float dot = part[0];
+#pragma unroll
+        for (int h = 1; h < HMAX; ++h) dot = li == h ? part[h] : dot;
+        gate_out[(int64_t)r * H + li] = sigmoidf(gate_scale * dot);
+      }
+    }
+  }
+};
+
+// The next slot's inputs, formed elementwise where the current slot's output
+// is produced (DOWN epilogue; the embedding for slot 0): decoder skip (lerp
+// gate or add, model.py:1275-1291), then resid_mix with x0 (model.py:947-950,
+// 1310-1316).  base = x_in (sequential) or lane0 after the skip (parallel) --
+// the residual base the O/DOWN epilogues of that slot use; attn = the
+// pre-RMSNorm attention input m0*base + m1*x0.
+struct NextIn {
+  const float* x0 = nullptr;
+  const float* skip = nullptr;    // popped encoder output or NULL
+  const float* skip_w = nullptr;  // [D]
+  const float* skip_g = nullptr;  // [D] gate logits or NULL
+  const float* mix = nullptr;     // next layer's resid_mix [2, D]
+  float* base = nullptr;          // NULL: no next slot
+  float* attn = nullptr;          // may equal base (sequential slot)
+  int parallel = 0;
+  int skip_self = 0;  // the popped encoder output is the value being produced here
+  struct El { float x0, sk, sw, sg, m0, m1; };
+  __device__ El load(int64_t idx, int c, int D) const {
+    El e;
+    e.x0 = x0[idx];
+    e.m0 = mix[c];
+    e.m1 = mix[D + c];
+    e.sk = (skip && !skip_self) ? skip[idx] : 0.f;
+    e.sw = skip ? skip_w[c] : 0.f;
+    e.sg = skip_g ? skip_g[c] : 0.f;
+    return e;
+  }
+  __device__ void put(int64_t idx, float x, const El& e) const {
+    float bs = x;
+    if (skip) {
+      const float sc = e.sw * (skip_self ? x : e.sk);
+      bs = skip_g ? lerp_t(sc, x, sigmoidf(e.sg)) : x + sc;
+    }
+    const float in = e.m0 * bs + e.m1 * e.x0;
+    base[idx] = parallel ? bs : in;
+    if (attn != base) attn[idx] = in;
   }
 };
 
@@ -373,13 +352,14 @@ struct EpiQKV {
     float cs[CPT], sn[CPT], gain;
   };
   template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int m0, int R, int) const {
+  __device__ Pre<Cfg> prefetch(int m0, int n0, int R, int) const {
     using P = Pre<Cfg>;
+    static_assert(Cfg::NCOL == HD, "one head per column tile");
     P o;
     const int row = threadIdx.x / P::TPR, c0 = (threadIdx.x % P::TPR) * P::CPT;
     const int r = m0 + row;
     o.p = r < R ? row_pos(pos, W, r) : 0;
-    const int nt = blockIdx.x;
+    const int nt = n0 / HD;
     o.gain = nt < H ? q_gain[nt] : 1.f;
     const int half = rd >> 1;
     const int pp = (o.p >= 0 && o.p < max_len) ? o.p : 0;
@@ -393,11 +373,11 @@ struct EpiQKV {
     return o;
   }
   template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, int m0, int, int R, int) const {
+  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
     constexpr int TPR = P::TPR, CPT = P::CPT;
     const int row = threadIdx.x / TPR, li = threadIdx.x % TPR, c0 = li * CPT;
     const int r = m0 + row;
-    const int nt = blockIdx.x;
+    const int nt = n0 / HD;
     const int kind = nt < H ? 0 : (nt < H + Hkv ? 1 : 2);
     const int head = kind == 0 ? nt : (kind == 1 ? nt - H : nt - H - Hkv);
     float v[CPT];
@@ -407,8 +387,8 @@ struct EpiQKV {
       float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < CPT; ++i) ss += v[i] * v[i];
-#pragma unroll
-      for (int m = TPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, WAVE);
+      static_assert(TPR == 16, "a head's 64 columns are one 16-lane row");
+      ss = row16_sum(ss);
       const float inv = rsqrtf(ss * (1.0f / HD) + eps);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) v[i] *= inv;
@@ -469,9 +449,8 @@ struct EpiO {
   int D, parallel;
   template <class Cfg> struct Pre { float base[EW<Cfg>::EPT], sc[EW<Cfg>::EPT]; };
   template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int m0, int R, int) const {
+  __device__ Pre<Cfg> prefetch(int m0, int n0, int R, int) const {
     Pre<Cfg> o;
-    const int n0 = blockIdx.x * Cfg::NCOL;
 #pragma unroll
     for (int j = 0; j < EW<Cfg>::EPT; ++j) {
       const int r = m0 + EW<Cfg>::row(j), c = n0 + EW<Cfg>::col(j);
@@ -482,7 +461,7 @@ struct EpiO {
     return o;
   }
   template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, int m0, int n0, int R, int) const {
+  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
 #pragma unroll
     for (int j = 0; j < EW<Cfg>::EPT; ++j) {
       const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
@@ -499,9 +478,9 @@ struct EpiUp {
   int F, hb16;
   template <class Cfg> struct Pre {};
   template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int, int, int) const { return {}; }
+  __device__ Pre<Cfg> prefetch(int, int, int, int) const { return {}; }
   template <class Cfg, class P>
-  __device__ void apply(const float* C, const P&, int m0, int n0, int R, int) const {
+  __device__ void apply(const float* C, const P&, const void*, int m0, int n0, int R, int) const {
 #pragma unroll
     for (int j = 0; j < EW<Cfg>::EPT; ++j) {
       const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
@@ -527,13 +506,14 @@ struct EpiDown {
   const float* pr;     // par: [2]
   const float* pp;     // par: [2, 2]
   int D, parallel;
+  NextIn next;  // inputs of the following slot (next.base == NULL: none)
   template <class Cfg> struct Pre {
     float xo[EW<Cfg>::EPT], sc[EW<Cfg>::EPT], l0[EW<Cfg>::EPT], l1[EW<Cfg>::EPT];
+    NextIn::El nx[EW<Cfg>::EPT];
   };
   template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int m0, int R, int) const {
+  __device__ Pre<Cfg> prefetch(int m0, int n0, int R, int) const {
     Pre<Cfg> o;
-    const int n0 = blockIdx.x * Cfg::NCOL;
 #pragma unroll
     for (int j = 0; j < EW<Cfg>::EPT; ++j) {
       const int r = m0 + EW<Cfg>::row(j), c = n0 + EW<Cfg>::col(j);
@@ -543,11 +523,12 @@ struct EpiDown {
       o.sc[j] = ok ? mlp_scale[c] : 0.f;
       o.l0[j] = (ok && parallel) ? lane0[idx] : 0.f;
       o.l1[j] = (ok && parallel) ? lane1[idx] : 0.f;
+      if (ok && next.base) o.nx[j] = next.load(idx, c, D);
     }
     return o;
   }
   template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, int m0, int n0, int R, int) const {
+  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
 #pragma unroll
     for (int j = 0; j < EW<Cfg>::EPT; ++j) {
       const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
@@ -555,40 +536,71 @@ struct EpiDown {
       if (r >= R || c >= D) continue;
       const int64_t o = (int64_t)r * D + c;
       const float m = pre.sc[j] * C[rr * Cfg::CS + cc];
+      float x;
       if (!parallel) {
-        out0[o] = pre.xo[j] + m;
+        x = pre.xo[j] + m;
+        out0[o] = x;
       } else {
         const float a = pre.xo[j];
-        out0[o] = pr[0] * pre.l0[j] + pp[0] * a + pp[2] * m;
+        x = pr[0] * pre.l0[j] + pp[0] * a + pp[2] * m;
+        out0[o] = x;
         out1[o] = pr[1] * pre.l1[j] + pp[1] * a + pp[3] * m;
       }
+      if (next.base) next.put(o, x, pre.nx[j]);
     }
   }
 };
 
+// Softcapped logits, plus per (row, 64-column tile) softmax statistics
+// (tile max m and sum of exp(l - m)) for the row-parallel CDF kernel.
 struct EpiLogits {
   float* logits;
+  float2* stats;  // [R][V/64] or NULL
   int V, asym;
   float cap;
   const float* cap_pn;
-  template <class Cfg> struct Pre { float cp, cn; };
+  template <class Cfg> struct Pre { float cp, cn, icp, icn; };
   template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int, int, int) const {
+  __device__ Pre<Cfg> prefetch(int, int, int, int) const {
     Pre<Cfg> o;
     o.cp = asym ? cap_pn[0] : cap;
     o.cn = asym ? cap_pn[1] : cap;
+    o.icp = 1.f / o.cp;
+    o.icn = 1.f / o.cn;
     return o;
   }
   template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, int m0, int n0, int R, int) const {
+  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
+    static_assert(Cfg::NCOL == 64 && Cfg::THREADS == 256, "a wave holds one row of a 64-column tile");
+    constexpr int EPT = EW<Cfg>::EPT;
+    float v[EPT];
 #pragma unroll
-    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
+    for (int j = 0; j < EPT; ++j) {
       const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
       const int r = m0 + rr, c = n0 + cc;
-      if (r >= R || c >= V) continue;
-      const float l = C[rr * Cfg::CS + cc];
-      const float cp = l >= 0.f ? pre.cp : pre.cn;
-      logits[(int64_t)r * V + c] = cp * tanhf(l / cp);
+      v[j] = -INFINITY;
+      if (r < R && c < V) {
+        const float l = C[rr * Cfg::CS + cc];
+        const bool pos = l >= 0.f;
+        v[j] = (pos ? pre.cp : pre.cn) * tanh_fast(l * (pos ? pre.icp : pre.icn));
+        logits[(int64_t)r * V + c] = v[j];
+      }
+    }
+    if (stats) {  // wave w holds rows w + 4j of the tile, one column per lane
+      float m[EPT], e[EPT];
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) m[j] = wave_max(v[j]);
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) e[j] = v[j] == -INFINITY ? 0.f : __expf(v[j] - m[j]);
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) e[j] = wave_sum(e[j]);
+      if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const int r = m0 + EW<Cfg>::row(j);
+          if (r < R) stats[(int64_t)r * (V / 64) + n0 / 64] = make_float2(m[j], e[j]);
+        }
+      }
     }
   }
 };
@@ -604,11 +616,20 @@ __global__ void commit_kernel(int32_t* pos, float* prev_raw, const float* cand_r
 // ---- host side --------------------------------------------------------------
 
 struct WS {
-  float *X0, *X1, *XIN, *XOUT, *Q, *GATE;
+  float *X0, *X1, *XIN, *QIN, *XOUT, *Q, *GATE;  // XIN, QIN: [2][Rp][D] (slot parity)
   void *Y, *HB;
+  float2* STATS;
+  int* SYNC;
+  int nsync;
 };
 
 int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// LM head: workgroups per 16-row tile (0 = one per 64-column tile).
+constexpr int kLmHeadColWgs = 0;
+// Preferred K-splits of the 4-wave GEMM stages (QKV and the LM head use
+// (NB, KS) = (4, 1): one 64-column head tile per task).
+constexpr int kKsO = 2, kKsUp = 2, kKsDown = 4;
 
 int64_t carve(const AltxsStepDesc* d, WS* w, char* base) {
   const int64_t R = (int64_t)d->B * d->W, Rp = align_up(R, 16);
@@ -621,15 +642,21 @@ int64_t carve(const AltxsStepDesc* d, WS* w, char* base) {
   };
   char* x0 = take((n + 1) * Rp * D * 4);
   char* x1 = take((n + 1) * Rp * D * 4);
-  char* xin = take(Rp * D * 4);
+  char* xin = take(2 * Rp * D * 4);
+  char* qin = take(2 * Rp * D * 4);
   char* xout = take(Rp * D * 4);
   char* q = take(Rp * d->H * HD * 4);
   char* gate = take(Rp * d->H * 4);
   char* y = take(Rp * D * 4);
   char* hb = take(Rp * (int64_t)d->F * 4);
+  char* stats = take(Rp * (int64_t)(d->V / 64 + 1) * 8);
+  const int nsync = (int)(Rp / 16);
+  char* sync = take(nsync * 4);
   if (w) {
-    w->X0 = (float*)x0; w->X1 = (float*)x1; w->XIN = (float*)xin; w->XOUT = (float*)xout;
+    w->X0 = (float*)x0; w->X1 = (float*)x1; w->XIN = (float*)xin; w->QIN = (float*)qin;
+    w->XOUT = (float*)xout;
     w->Q = (float*)q; w->GATE = (float*)gate; w->Y = y; w->HB = hb;
+    w->STATS = (float2*)stats; w->SYNC = (int*)sync; w->nsync = nsync;
   }
   return off;
 }
@@ -704,12 +731,26 @@ int validate(const AltxsStepDesc* d) {
     ALTXS_REQUIRE(S.layer >= 0 && S.layer < d->n_layers, "altxs_step: slot %d layer", s);
     ALTXS_REQUIRE(S.kind == ALTXS_SLOT_SEQ || S.kind == ALTXS_SLOT_PAR, "altxs_step: slot %d kind", s);
     ALTXS_REQUIRE(S.skip_src < s, "altxs_step: slot %d pops a later slot", s);
+    if (s == 0)
+      ALTXS_REQUIRE(S.kind == ALTXS_SLOT_SEQ && S.skip_src < 0,
+                    "altxs_step: slot 0 must be a sequential slot without a skip");
     if (S.skip_src >= 0) ALTXS_REQUIRE(S.skip_idx >= 0 && d->skip_weights, "altxs_step: slot %d skip", s);
     if (S.kind == ALTXS_SLOT_PAR)
       ALTXS_REQUIRE(d->layers[S.layer].par_resid && d->layers[S.layer].par_post,
                     "altxs_step: slot %d parallel lambdas missing", s);
   }
   return ALTXS_OK;
+}
+
+// Final hidden state: 0 = x (or the attention lane), 1 = mean of the two
+// parallel lanes, 2 = the MLP lane (model.py:1357-1362).
+int final_mode(const AltxsStepDesc* d) {
+  bool any_par = false;
+  for (int s = 0; s < d->n_slots; ++s) any_par |= d->slots[s].kind == ALTXS_SLOT_PAR;
+  if (!any_par) return 0;
+  if (d->flags & ALTXS_F_FINAL_MLP) return 2;
+  if (d->flags & ALTXS_F_FINAL_ATTN) return 0;
+  return 1;
 }
 
 template <int AM>
@@ -728,6 +769,8 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
     p.gw = d->gate_window; p.smear = (d->flags & ALTXS_F_SMEAR) ? 1 : 0; p.eps = d->norm_eps;
     p.tokens = d->tokens; p.prev_raw = d->prev_raw; p.cand_raw = d->cand_raw;
     p.smear_w = d->smear_w; p.smear_lambda = d->smear_lambda; p.x0 = w.X0; p.err = d->err;
+    p.sync = w.SYNC; p.nsync = w.nsync;
+    p.mix0 = d->layers[d->slots[0].layer].resid_mix; p.xin0 = w.XIN;
     hipLaunchKernelGGL(embed_kernel, dim3(R), dim3(64), 0, st, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
@@ -738,27 +781,21 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
     const bool par = S.kind == ALTXS_SLOT_PAR;
     float* xin_slot = w.X0 + s * Rp * D;           // x or lane0 entering the slot
     const float* lane1_in = par ? (S.first_parallel ? xin_slot : w.X1 + s * Rp * D) : nullptr;
+    float* base_s = w.XIN + (s & 1) * Rp * D;      // x_in (seq) / lane0 after skip (par)
+    const float* attn_in = par ? w.QIN + (s & 1) * Rp * D : base_s;
     char* kv = (char*)d->kv + s * slot_kv * esz;
-    // QKV
+    // QKV: RMSNorm * ln_scale of the attention input (+ sparse-gate multipliers)
     {
-      ProQKV pro;
-      pro.x = xin_slot; pro.x0 = x0;
-      pro.skip = S.skip_src >= 0 ? w.X0 + (S.skip_src + 1) * Rp * D : nullptr;
-      pro.skip_w = S.skip_src >= 0 ? d->skip_weights + (int64_t)S.skip_idx * D : nullptr;
-      pro.skip_g = (S.skip_src >= 0 && (d->flags & ALTXS_F_SKIP_GATES) && d->skip_gates)
-                       ? d->skip_gates + (int64_t)S.skip_idx * D : nullptr;
-      pro.mix = L.resid_mix; pro.base_out = w.XIN;
+      ProNorm pro{attn_in, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       pro.gate_w = (d->flags & ALTXS_F_SPARSE_GATE) ? L.attn_gate_w : nullptr;
-      pro.gate_out = w.GATE; pro.ln_scale = L.ln_scale; pro.eps = d->norm_eps;
-      pro.gate_scale = d->gate_scale; pro.D = d->D; pro.H = d->H; pro.gw = d->gate_window;
-      pro.parallel = par ? 1 : 0;
+      pro.gate_out = w.GATE; pro.gate_scale = d->gate_scale; pro.H = d->H; pro.gw = d->gate_window;
       EpiQKV epi;
       epi.q = w.Q; epi.kv = kv; epi.kv_bf16 = d->kv_bf16; epi.H = d->H; epi.Hkv = d->Hkv;
       epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = d->pos;
       epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
       epi.err = d->err;
-      if ((e = launch_qgemm_rt<AM, 4, 2>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
-                                         pro, epi, st)) != hipSuccess)
+      if ((e = launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
+                                          pro, epi, 0, st)) != hipSuccess)
         return e;
     }
     // attention
@@ -779,17 +816,17 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
     }
     // out-projection + attention residual
     {
-      EpiO epi{w.XIN, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
-      if ((e = launch_qgemm_rt<AM, 1, 2>(L.o.bits, qt_of(L.o), R, 1, 0, 0, ADirect{w.Y, 0}, ProNone{},
-                                         epi, st)) != hipSuccess)
+      EpiO epi{base_s, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
+      if ((e = launch_gemm4<AM>(kKsO, L.o.bits, qt_of(L.o), R, ADirect{w.Y, 0}, ProNone{}, epi, 0,
+                                st)) != hipSuccess)
         return e;
     }
     // MLP up + LeakyReLU(0.5)^2
     {
       ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       EpiUp epi{w.HB, d->F, hb16};
-      if ((e = launch_qgemm_rt<AM, 2, 2>(L.up.bits, qt_of(L.up), R, 1, 0, 0, ADirect{nullptr, 0}, pro,
-                                         epi, st)) != hipSuccess)
+      if ((e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0,
+                                st)) != hipSuccess)
         return e;
     }
     // MLP down + residual / lanes
@@ -797,36 +834,50 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
       EpiDown epi;
       epi.xout = w.XOUT; epi.mlp_scale = L.mlp_scale;
       epi.out0 = w.X0 + (s + 1) * Rp * D; epi.out1 = w.X1 + (s + 1) * Rp * D;
-      epi.lane0 = w.XIN; epi.lane1 = lane1_in; epi.pr = L.par_resid; epi.pp = L.par_post;
+      epi.lane0 = base_s; epi.lane1 = lane1_in; epi.pr = L.par_resid; epi.pp = L.par_post;
       epi.D = d->D; epi.parallel = par ? 1 : 0;
-      if ((e = launch_qgemm_rt<AM, 1, 4>(L.down.bits, qt_of(L.down), R, 1, 0, 0, ADirect{w.HB, 0},
-                                         ProNone{}, epi, st)) != hipSuccess)
+      if (s + 1 < d->n_slots) {  // the next slot's residual base and attention input
+        const AltxsSlot& S1 = d->slots[s + 1];
+        const bool par1 = S1.kind == ALTXS_SLOT_PAR;
+        NextIn& nx = epi.next;
+        nx.x0 = x0;
+        nx.skip = S1.skip_src >= 0 ? w.X0 + (S1.skip_src + 1) * Rp * D : nullptr;
+        nx.skip_w = S1.skip_src >= 0 ? d->skip_weights + (int64_t)S1.skip_idx * D : nullptr;
+        nx.skip_g = (S1.skip_src >= 0 && (d->flags & ALTXS_F_SKIP_GATES) && d->skip_gates)
+                        ? d->skip_gates + (int64_t)S1.skip_idx * D : nullptr;
+        nx.mix = d->layers[S1.layer].resid_mix;
+        nx.base = w.XIN + ((s + 1) & 1) * Rp * D;
+        nx.attn = par1 ? w.QIN + ((s + 1) & 1) * Rp * D : nx.base;
+        nx.parallel = par1 ? 1 : 0;
+        nx.skip_self = S1.skip_src == s ? 1 : 0;
+      }
+
+      if ((e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
+                                epi, 0, st)) != hipSuccess)
         return e;
     }
   }
   // final norm + LM head + softcap
+  const bool fast_cdf = !(d->flags & ALTXS_F_RENORM) && d->V % 64 == 0;
   {
-    const int n = d->n_slots;
-    bool any_par = false;
-    for (int s = 0; s < n; ++s) any_par |= d->slots[s].kind == ALTXS_SLOT_PAR;
-    const float* xf = w.X0 + n * Rp * D;
-    const float* x2 = nullptr;
-    int mode = 0;
-    if (any_par) {
-      if (d->flags & ALTXS_F_FINAL_MLP) xf = w.X1 + n * Rp * D;
-      else if (!(d->flags & ALTXS_F_FINAL_ATTN)) { x2 = w.X1 + n * Rp * D; mode = 1; }
-    }
-    ProNorm pro{xf, x2, mode, 1.0f, d->norm_eps, d->D};
-    EpiLogits epi{d->logits, d->V, (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap,
-                  d->softcap_pn};
-    if ((e = launch_qgemm_rt<AM, 2, 2>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0}, pro,
-                                       epi, st)) != hipSuccess)
+    const int n = d->n_slots, fm = final_mode(d);
+    const float* xf = (fm == 2 ? w.X1 : w.X0) + n * Rp * D;
+    ProNorm pro{xf, fm == 1 ? w.X1 + n * Rp * D : nullptr, fm == 1 ? 1 : 0, 1.0f, d->norm_eps, d->D};
+    EpiLogits epi{d->logits, fast_cdf ? w.STATS : nullptr, d->V,
+                  (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap, d->softcap_pn};
+    if ((e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0}, pro,
+                                        epi, kLmHeadColWgs, st)) != hipSuccess)
       return e;
   }
   if (d->probs || d->cum) {
-    const int fl = (d->flags & ALTXS_F_RENORM) ? ALTXS_CDF_RENORM : 0;
-    if ((e = altxs_launch_cdf(d->logits, R, d->V, fl, true, d->probs, d->cum, st)) != hipSuccess)
-      return e;
+    if (fast_cdf && d->cum) {
+      if ((e = altxs_launch_cdf_stats(d->logits, w.STATS, R, d->V, d->probs, d->cum, st)) != hipSuccess)
+        return e;
+    } else {
+      const int fl = (d->flags & ALTXS_F_RENORM) ? ALTXS_CDF_RENORM : 0;
+      if ((e = altxs_launch_cdf(d->logits, R, d->V, fl, true, d->probs, d->cum, st)) != hipSuccess)
+        return e;
+    }
   }
   if (d->flags & ALTXS_F_COMMIT) {
     hipLaunchKernelGGL(commit_kernel, dim3(d->B), dim3(256), 0, st, d->pos, d->prev_raw,

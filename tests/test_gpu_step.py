@@ -166,3 +166,18 @@ def test_positions_and_state_advance():
     T = CASES["tiny"][1]
     assert torch.equal(st.pos.cpu(), torch.full((st.batch,), T, dtype=torch.int32))
     assert int(st.err.item()) == 0
+
+
+@pytest.mark.parametrize("profile", ["tiny", "cfg1"])
+def test_step_probs_and_cdf_rule(profile):
+    """The step's probabilities are a softmax of its logits, and its integer CDFs
+    are exactly _scale_cum_np of those probabilities (row-parallel CDF kernel:
+    V=256 in one chunk, V=4096 in two)."""
+    from oracle import coder
+
+    _log(f"probs/cdf rule {profile}")
+    _, cm, model, st = _gpu_decode(profile, "bf16")
+    lg = st.logits.cpu()
+    pr = st.probs.cpu()
+    assert (pr - torch.softmax(lg.double(), -1).float()).abs().max().item() < 1e-6
+    assert np.array_equal(st.cum.cpu().numpy().astype(np.int64), coder.scale_cum(pr.numpy()))
