@@ -12,7 +12,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libaltxs_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MAX_LAYERS = 32
 MAX_SLOTS = 64
@@ -109,7 +109,8 @@ class StepDesc(ctypes.Structure):
                 ("kv", ctypes.c_void_p), ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_int64),
                 ("logits", ctypes.c_void_p), ("probs", ctypes.c_void_p),
                 ("cum", ctypes.c_void_p), ("err", ctypes.c_void_p),
-                ("attn_events", ctypes.c_void_p)]
+                ("attn_events", ctypes.c_void_p),
+                ("aux_stream", ctypes.c_void_p), ("sync_events", ctypes.c_void_p)]
 
 
 _lib = None

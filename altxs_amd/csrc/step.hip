@@ -631,8 +631,8 @@ constexpr int kLmHeadColWgs = 0;
 // (NB, KS) = (4, 1): one 64-column head tile per task).
 constexpr int kKsO = 2, kKsUp = 2, kKsDown = 4;
 
-int64_t carve(const AltxsStepDesc* d, WS* w, char* base) {
-  const int64_t R = (int64_t)d->B * d->W, Rp = align_up(R, 16);
+int64_t carve(const AltxsStepDesc* d, int nb, WS* w, char* base) {
+  const int64_t R = (int64_t)nb * d->W, Rp = align_up(R, 16);
   const int64_t D = d->D, n = d->n_slots;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -659,6 +659,15 @@ int64_t carve(const AltxsStepDesc* d, WS* w, char* base) {
     w->STATS = (float2*)stats; w->SYNC = (int*)sync; w->nsync = nsync;
   }
   return off;
+}
+
+// Two segment groups (split mode) when the caller hands in a second stream.
+bool split_mode(const AltxsStepDesc* d) { return d->aux_stream != nullptr && d->B >= 2; }
+int64_t ws_bytes_needed(const AltxsStepDesc* d) {
+  const int nb0 = (d->B + 1) / 2;
+  const int64_t one = carve(d, d->B, nullptr, nullptr);
+  const int64_t two = carve(d, nb0, nullptr, nullptr) + carve(d, d->B - nb0, nullptr, nullptr);
+  return one > two ? one : two;
 }
 
 QT qt_of(const AltxsQTensor& t) {
@@ -707,7 +716,8 @@ int validate(const AltxsStepDesc* d) {
   ALTXS_REQUIRE(d->tokens && d->pos && d->prev_raw && d->cand_raw && d->kv && d->ws && d->logits &&
                     d->rope_cos && d->rope_sin && d->err,
                 "altxs_step: null state/output pointer");
-  ALTXS_REQUIRE(d->ws_bytes >= carve(d, nullptr, nullptr), "altxs_step: workspace too small");
+  ALTXS_REQUIRE(d->ws_bytes >= ws_bytes_needed(d), "altxs_step: workspace too small");
+  if (d->aux_stream) ALTXS_REQUIRE(d->sync_events, "altxs_step: aux_stream needs sync_events");
   if (d->flags & ALTXS_F_SMEAR)
     ALTXS_REQUIRE(d->smear_w && d->smear_lambda, "altxs_step: smear params missing");
   if (d->flags & ALTXS_F_ASYM_SOFTCAP) ALTXS_REQUIRE(d->softcap_pn, "altxs_step: softcap_pn missing");
@@ -753,84 +763,130 @@ int final_mode(const AltxsStepDesc* d) {
   return 1;
 }
 
-template <int AM>
-hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
-  const int R = d->B * d->W;
-  const int64_t Rp = align_up(R, 16);
-  const int64_t D = d->D;
-  const int hb16 = AM == A_BF16 ? 1 : 0;
-  const int64_t esz = d->kv_bf16 ? 2 : 4;
-  const int64_t slot_kv = (int64_t)d->B * 2 * d->Hkv * d->max_len * HD;
-  hipError_t e;
+// A contiguous range of segments run as one batch: segments [b0, b0 + nb).
+// Pointers are the caller's state offset to the group; the KV slot stride
+// stays that of the whole batch.
+struct Group {
+  int b0, nb;
+  const int32_t* tokens;
+  int32_t* pos;
+  float* prev_raw;
+  float* cand_raw;
+  char* kv;  // slot 0, segment b0
+  float* logits;
+  float* probs;
+  uint32_t* cum;
+  WS w;
+};
 
-  {  // embedding
+Group make_group(const AltxsStepDesc* d, int b0, int nb, char* ws) {
+  Group g;
+  g.b0 = b0; g.nb = nb;
+  const int64_t r0 = (int64_t)b0 * d->W;
+  const int64_t esz = d->kv_bf16 ? 2 : 4;
+  g.tokens = d->tokens + r0;
+  g.pos = d->pos + b0;
+  g.prev_raw = d->prev_raw + (int64_t)b0 * d->D;
+  g.cand_raw = d->cand_raw + (int64_t)b0 * d->D;
+  g.kv = (char*)d->kv + (int64_t)b0 * 2 * d->Hkv * d->max_len * HD * esz;
+  g.logits = d->logits + r0 * d->V;
+  g.probs = d->probs ? d->probs + r0 * d->V : nullptr;
+  g.cum = d->cum ? d->cum + r0 * (d->V + 1) : nullptr;
+  carve(d, nb, &g.w, ws);
+  return g;
+}
+
+template <int AM>
+struct StepRun {
+  const AltxsStepDesc* d;
+  static constexpr int hb16 = AM == A_BF16 ? 1 : 0;
+
+  hipError_t embed(const Group& G, hipStream_t st) const {
+    const WS& w = G.w;
     EmbedP p;
     p.emb = qt_of(d->emb); p.bits = d->emb.bits; p.V = d->V; p.D = d->D; p.W = d->W;
     p.gw = d->gate_window; p.smear = (d->flags & ALTXS_F_SMEAR) ? 1 : 0; p.eps = d->norm_eps;
-    p.tokens = d->tokens; p.prev_raw = d->prev_raw; p.cand_raw = d->cand_raw;
+    p.tokens = G.tokens; p.prev_raw = G.prev_raw; p.cand_raw = G.cand_raw;
     p.smear_w = d->smear_w; p.smear_lambda = d->smear_lambda; p.x0 = w.X0; p.err = d->err;
     p.sync = w.SYNC; p.nsync = w.nsync;
     p.mix0 = d->layers[d->slots[0].layer].resid_mix; p.xin0 = w.XIN;
-    hipLaunchKernelGGL(embed_kernel, dim3(R), dim3(64), 0, st, p);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(embed_kernel, dim3(G.nb * d->W), dim3(64), 0, st, p);
+    return hipGetLastError();
   }
-  const float* x0 = w.X0;
-  for (int s = 0; s < d->n_slots; ++s) {
+
+  // QKV of slot s: RMSNorm * ln_scale of the attention input (+ sparse-gate multipliers)
+  hipError_t qkv(const Group& G, int s, hipStream_t st) const {
+    const WS& w = G.w;
+    const int R = G.nb * d->W;
+    const int64_t Rp = align_up(R, 16), D = d->D;
+    const AltxsSlot& S = d->slots[s];
+    const AltxsLayer& L = d->layers[S.layer];
+    const bool par = S.kind == ALTXS_SLOT_PAR;
+    const float* attn_in = par ? w.QIN + (s & 1) * Rp * D : w.XIN + (s & 1) * Rp * D;
+    ProNorm pro{attn_in, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
+    pro.gate_w = (d->flags & ALTXS_F_SPARSE_GATE) ? L.attn_gate_w : nullptr;
+    pro.gate_out = w.GATE; pro.gate_scale = d->gate_scale; pro.H = d->H; pro.gw = d->gate_window;
+    EpiQKV epi;
+    epi.q = w.Q; epi.kv = slot_kv(G, s); epi.kv_bf16 = d->kv_bf16; epi.H = d->H; epi.Hkv = d->Hkv;
+    epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = G.pos;
+    epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
+    epi.err = d->err;
+    return launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
+                                      pro, epi, 0, st);
+  }
+
+  char* slot_kv(const Group& G, int s) const {
+    const int64_t esz = d->kv_bf16 ? 2 : 4;
+    return G.kv + (int64_t)s * d->B * 2 * d->Hkv * d->max_len * HD * esz;
+  }
+
+  hipError_t attn(const Group& G, int s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) const {
+    const WS& w = G.w;
+    const AltxsLayer& L = d->layers[d->slots[s].layer];
+    const int64_t esz = d->kv_bf16 ? 2 : 4;
+    char* kv = slot_kv(G, s);
+    AltxsAttnArgs a;
+    memset(&a, 0, sizeof(a));
+    a.B = G.nb; a.W = d->W; a.H = d->H; a.Hkv = d->Hkv; a.head_dim = HD; a.max_len = d->max_len;
+    a.kv_bf16 = d->kv_bf16; a.y_bf16 = hb16; a.q = w.Q;
+    a.k = kv; a.v = kv + (int64_t)d->Hkv * d->max_len * HD * esz;
+    a.kv_seg_stride = 2ll * d->Hkv * d->max_len * HD; a.pos = G.pos;
+    a.gate = (d->flags & ALTXS_F_SPARSE_GATE) ? w.GATE : nullptr;
+    a.use_xsa = L.use_xsa; a.y = w.Y; a.err = d->err;
+    a.flags = AM == A_BF16 ? ALTXS_ATTN_OPS_BF16 : 0;
+    hipError_t e;
+    if (ev0 && (e = hipEventRecord(ev0, st)) != hipSuccess) return e;
+    if ((e = altxs_launch_attn(a, st)) != hipSuccess) return e;
+    if (ev1 && (e = hipEventRecord(ev1, st)) != hipSuccess) return e;
+    return hipSuccess;
+  }
+
+  // O, UP, DOWN of slot s (DOWN also forms slot s+1's inputs)
+  hipError_t mlp(const Group& G, int s, hipStream_t st) const {
+    const WS& w = G.w;
+    const int R = G.nb * d->W;
+    const int64_t Rp = align_up(R, 16), D = d->D;
     const AltxsSlot& S = d->slots[s];
     const AltxsLayer& L = d->layers[S.layer];
     const bool par = S.kind == ALTXS_SLOT_PAR;
     float* xin_slot = w.X0 + s * Rp * D;           // x or lane0 entering the slot
     const float* lane1_in = par ? (S.first_parallel ? xin_slot : w.X1 + s * Rp * D) : nullptr;
     float* base_s = w.XIN + (s & 1) * Rp * D;      // x_in (seq) / lane0 after skip (par)
-    const float* attn_in = par ? w.QIN + (s & 1) * Rp * D : base_s;
-    char* kv = (char*)d->kv + s * slot_kv * esz;
-    // QKV: RMSNorm * ln_scale of the attention input (+ sparse-gate multipliers)
-    {
-      ProNorm pro{attn_in, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
-      pro.gate_w = (d->flags & ALTXS_F_SPARSE_GATE) ? L.attn_gate_w : nullptr;
-      pro.gate_out = w.GATE; pro.gate_scale = d->gate_scale; pro.H = d->H; pro.gw = d->gate_window;
-      EpiQKV epi;
-      epi.q = w.Q; epi.kv = kv; epi.kv_bf16 = d->kv_bf16; epi.H = d->H; epi.Hkv = d->Hkv;
-      epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = d->pos;
-      epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
-      epi.err = d->err;
-      if ((e = launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
-                                          pro, epi, 0, st)) != hipSuccess)
-        return e;
-    }
-    // attention
-    {
-      AltxsAttnArgs a;
-      memset(&a, 0, sizeof(a));
-      a.B = d->B; a.W = d->W; a.H = d->H; a.Hkv = d->Hkv; a.head_dim = HD; a.max_len = d->max_len;
-      a.kv_bf16 = d->kv_bf16; a.y_bf16 = hb16; a.q = w.Q;
-      a.k = kv; a.v = kv + (int64_t)d->Hkv * d->max_len * HD * esz;
-      a.kv_seg_stride = 2ll * d->Hkv * d->max_len * HD; a.pos = d->pos;
-      a.gate = (d->flags & ALTXS_F_SPARSE_GATE) ? w.GATE : nullptr;
-      a.use_xsa = L.use_xsa; a.y = w.Y; a.err = d->err;
-      a.flags = AM == A_BF16 ? ALTXS_ATTN_OPS_BF16 : 0;
-      hipEvent_t* ev = (hipEvent_t*)d->attn_events;
-      if (ev && (e = hipEventRecord(ev[2 * s], st)) != hipSuccess) return e;
-      if ((e = altxs_launch_attn(a, st)) != hipSuccess) return e;
-      if (ev && (e = hipEventRecord(ev[2 * s + 1], st)) != hipSuccess) return e;
-    }
-    // out-projection + attention residual
-    {
+    hipError_t e;
+    {  // out-projection + attention residual
       EpiO epi{base_s, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
       if ((e = launch_gemm4<AM>(kKsO, L.o.bits, qt_of(L.o), R, ADirect{w.Y, 0}, ProNone{}, epi, 0,
                                 st)) != hipSuccess)
         return e;
     }
-    // MLP up + LeakyReLU(0.5)^2
-    {
+    {  // MLP up + LeakyReLU(0.5)^2
       ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       EpiUp epi{w.HB, d->F, hb16};
       if ((e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0,
                                 st)) != hipSuccess)
         return e;
     }
-    // MLP down + residual / lanes
-    {
+    {  // MLP down + residual / lanes
       EpiDown epi;
       epi.xout = w.XOUT; epi.mlp_scale = L.mlp_scale;
       epi.out0 = w.X0 + (s + 1) * Rp * D; epi.out1 = w.X1 + (s + 1) * Rp * D;
@@ -840,7 +896,7 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
         const AltxsSlot& S1 = d->slots[s + 1];
         const bool par1 = S1.kind == ALTXS_SLOT_PAR;
         NextIn& nx = epi.next;
-        nx.x0 = x0;
+        nx.x0 = w.X0;
         nx.skip = S1.skip_src >= 0 ? w.X0 + (S1.skip_src + 1) * Rp * D : nullptr;
         nx.skip_w = S1.skip_src >= 0 ? d->skip_weights + (int64_t)S1.skip_idx * D : nullptr;
         nx.skip_g = (S1.skip_src >= 0 && (d->flags & ALTXS_F_SKIP_GATES) && d->skip_gates)
@@ -851,56 +907,123 @@ hipError_t run_step(const AltxsStepDesc* d, const WS& w, hipStream_t st) {
         nx.parallel = par1 ? 1 : 0;
         nx.skip_self = S1.skip_src == s ? 1 : 0;
       }
-
       if ((e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
                                 epi, 0, st)) != hipSuccess)
         return e;
     }
+    return hipSuccess;
   }
-  // final norm + LM head + softcap
-  const bool fast_cdf = !(d->flags & ALTXS_F_RENORM) && d->V % 64 == 0;
-  {
-    const int n = d->n_slots, fm = final_mode(d);
-    const float* xf = (fm == 2 ? w.X1 : w.X0) + n * Rp * D;
-    ProNorm pro{xf, fm == 1 ? w.X1 + n * Rp * D : nullptr, fm == 1 ? 1 : 0, 1.0f, d->norm_eps, d->D};
-    EpiLogits epi{d->logits, fast_cdf ? w.STATS : nullptr, d->V,
-                  (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap, d->softcap_pn};
-    if ((e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0}, pro,
-                                        epi, kLmHeadColWgs, st)) != hipSuccess)
-      return e;
-  }
-  if (d->probs || d->cum) {
-    if (fast_cdf && d->cum) {
-      if ((e = altxs_launch_cdf_stats(d->logits, w.STATS, R, d->V, d->probs, d->cum, st)) != hipSuccess)
-        return e;
-    } else {
-      const int fl = (d->flags & ALTXS_F_RENORM) ? ALTXS_CDF_RENORM : 0;
-      if ((e = altxs_launch_cdf(d->logits, R, d->V, fl, true, d->probs, d->cum, st)) != hipSuccess)
+
+  // final norm + LM head + softcap, softmax -> CDF, commit
+  hipError_t head(const Group& G, hipStream_t st) const {
+    const WS& w = G.w;
+    const int R = G.nb * d->W;
+    const int64_t Rp = align_up(R, 16), D = d->D;
+    const bool fast_cdf = !(d->flags & ALTXS_F_RENORM) && d->V % 64 == 0;
+    hipError_t e;
+    {
+      const int n = d->n_slots, fm = final_mode(d);
+      const float* xf = (fm == 2 ? w.X1 : w.X0) + n * Rp * D;
+      ProNorm pro{xf, fm == 1 ? w.X1 + n * Rp * D : nullptr, fm == 1 ? 1 : 0, 1.0f, d->norm_eps, d->D};
+      EpiLogits epi{G.logits, fast_cdf ? w.STATS : nullptr, d->V,
+                    (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap, d->softcap_pn};
+      if ((e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0},
+                                          pro, epi, kLmHeadColWgs, st)) != hipSuccess)
         return e;
     }
+    if (G.probs || G.cum) {
+      if (fast_cdf && G.cum) {
+        if ((e = altxs_launch_cdf_stats(G.logits, w.STATS, R, d->V, G.probs, G.cum, st)) != hipSuccess)
+          return e;
+      } else {
+        const int fl = (d->flags & ALTXS_F_RENORM) ? ALTXS_CDF_RENORM : 0;
+        if ((e = altxs_launch_cdf(G.logits, R, d->V, fl, true, G.probs, G.cum, st)) != hipSuccess)
+          return e;
+      }
+    }
+    if (d->flags & ALTXS_F_COMMIT) {
+      hipLaunchKernelGGL(commit_kernel, dim3(G.nb), dim3(256), 0, st, G.pos, G.prev_raw,
+                         (const float*)G.cand_raw, G.nb, d->D, d->W);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
   }
-  if (d->flags & ALTXS_F_COMMIT) {
-    hipLaunchKernelGGL(commit_kernel, dim3(d->B), dim3(256), 0, st, d->pos, d->prev_raw,
-                       (const float*)d->cand_raw, d->B, d->D, d->W);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+};
+
+// One group on one stream.
+template <int AM>
+hipError_t run_single(const AltxsStepDesc* d, const Group& G, hipStream_t st) {
+  StepRun<AM> run{d};
+  hipError_t e;
+  hipEvent_t* ev = (hipEvent_t*)d->attn_events;
+  if ((e = run.embed(G, st)) != hipSuccess) return e;
+  for (int s = 0; s < d->n_slots; ++s) {
+    if ((e = run.qkv(G, s, st)) != hipSuccess) return e;
+    if ((e = run.attn(G, s, st, ev ? ev[2 * s] : nullptr, ev ? ev[2 * s + 1] : nullptr)) != hipSuccess)
+      return e;
+    if ((e = run.mlp(G, s, st)) != hipSuccess) return e;
   }
-  return hipSuccess;
+  return run.head(G, st);
+}
+
+// Two segment groups on two streams.  Attention launches alternate
+// A0 B0 A1 B1 ... (event dependencies), so each group's GEMM chain runs while
+// the other group's attention streams the KV cache.  Every kernel computes a
+// row from that row's inputs only, so the split changes no bits.
+template <int AM>
+hipError_t run_split(const AltxsStepDesc* d, const Group (&G)[2], hipStream_t s0, hipStream_t s1) {
+  StepRun<AM> run{d};
+  hipEvent_t* sync = (hipEvent_t*)d->sync_events;  // [0] fork, [1] join, [2 + 2s + g] attention done
+  hipEvent_t* ev = (hipEvent_t*)d->attn_events;    // timing hook: [(g*n + s)*2 + 0/1]
+  const hipStream_t st[2] = {s0, s1};
+  const int n = d->n_slots;
+  hipError_t e;
+  if ((e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
+  if ((e = hipStreamWaitEvent(s1, sync[0], 0)) != hipSuccess) return e;
+  for (int g = 0; g < 2; ++g)
+    if ((e = run.embed(G[g], st[g])) != hipSuccess) return e;
+  for (int s = 0; s < n; ++s) {
+    for (int g = 0; g < 2; ++g) {
+      if ((e = run.qkv(G[g], s, st[g])) != hipSuccess) return e;
+      // wait for the previous attention launch (B of slot s-1 before A of s; A of s before B of s)
+      hipEvent_t prev = g == 0 ? (s > 0 ? sync[2 + 2 * (s - 1) + 1] : nullptr) : sync[2 + 2 * s];
+      if (prev && (e = hipStreamWaitEvent(st[g], prev, 0)) != hipSuccess) return e;
+      const int k = (g * n + s) * 2;
+      if ((e = run.attn(G[g], s, st[g], ev ? ev[k] : nullptr, ev ? ev[k + 1] : nullptr)) != hipSuccess)
+        return e;
+      if ((e = hipEventRecord(sync[2 + 2 * s + g], st[g])) != hipSuccess) return e;
+    }
+    for (int g = 0; g < 2; ++g)
+      if ((e = run.mlp(G[g], s, st[g])) != hipSuccess) return e;
+  }
+  for (int g = 0; g < 2; ++g)
+    if ((e = run.head(G[g], st[g])) != hipSuccess) return e;
+  if ((e = hipEventRecord(sync[1], s1)) != hipSuccess) return e;
+  return hipStreamWaitEvent(s0, sync[1], 0);
 }
 
 }  // namespace
 
 extern "C" int64_t altxs_step_workspace_bytes(const AltxsStepDesc* d) {
   if (!d) return -1;
-  return carve(d, nullptr, nullptr);
+  return ws_bytes_needed(d);
 }
 
 extern "C" int32_t altxs_step(const AltxsStepDesc* d, altxs_stream_t stream) {
   int rc = validate(d);
   if (rc) return rc;
-  WS w;
-  carve(d, &w, (char*)d->ws);
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e = d->act_bf16 ? run_step<A_BF16>(d, w, st) : run_step<A_F32>(d, w, st);
+  hipError_t e;
+  if (split_mode(d)) {
+    const int nb0 = (d->B + 1) / 2;
+    Group G[2] = {make_group(d, 0, nb0, (char*)d->ws),
+                  make_group(d, nb0, d->B - nb0, (char*)d->ws + carve(d, nb0, nullptr, nullptr))};
+    hipStream_t s1 = (hipStream_t)d->aux_stream;
+    e = d->act_bf16 ? run_split<A_BF16>(d, G, st, s1) : run_split<A_F32>(d, G, st, s1);
+  } else {
+    const Group G = make_group(d, 0, d->B, (char*)d->ws);
+    e = d->act_bf16 ? run_single<A_BF16>(d, G, st) : run_single<A_F32>(d, G, st);
+  }
   ALTXS_CHECK_HIP(e);
   return ALTXS_OK;
 }

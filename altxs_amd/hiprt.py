@@ -21,6 +21,8 @@ def _lib():
         p = ctypes.c_void_p
         _hip.hipEventCreate.argtypes = [ctypes.POINTER(p)]
         _hip.hipEventCreate.restype = ctypes.c_int
+        _hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(p), ctypes.c_uint]
+        _hip.hipEventCreateWithFlags.restype = ctypes.c_int
         _hip.hipEventDestroy.argtypes = [p]
         _hip.hipEventDestroy.restype = ctypes.c_int
         _hip.hipEventSynchronize.argtypes = [p]
@@ -30,16 +32,25 @@ def _lib():
     return _hip
 
 
-class EventArray:
-    """n hipEvent_t handles in a C array (pass ``.ptr`` where a void** is expected)."""
+HIP_EVENT_DISABLE_TIMING = 0x2
 
-    def __init__(self, n: int):
+
+class EventArray:
+    """n hipEvent_t handles in a C array (pass ``.ptr`` where a void** is expected).
+
+    ``timing=False`` creates them with hipEventDisableTiming (ordering only).
+    """
+
+    def __init__(self, n: int, timing: bool = True):
         L = _lib()
         self.n = n
         self.arr = (ctypes.c_void_p * n)()
         for i in range(n):
             h = ctypes.c_void_p()
-            rc = L.hipEventCreate(ctypes.byref(h))
+            if timing:
+                rc = L.hipEventCreate(ctypes.byref(h))
+            else:
+                rc = L.hipEventCreateWithFlags(ctypes.byref(h), HIP_EVENT_DISABLE_TIMING)
             if rc != 0:
                 raise RuntimeError(f"hipEventCreate failed ({rc})")
             self.arr[i] = h.value

@@ -27,7 +27,7 @@ import sys
 import numpy as np
 import torch
 
-from . import _lib
+from . import _lib, hiprt
 from .config import AltxsConfig, slot_itinerary
 from .synth import SynthModel, rope_table
 
@@ -70,7 +70,7 @@ class StaticState:
     """Caller-owned device buffers of a B x W step (addresses stay fixed)."""
 
     def __init__(self, model: "StepModel", batch: int, win: int, max_len: int,
-                 want_probs: bool = True, want_cdf: bool = True):
+                 want_probs: bool = True, want_cdf: bool = True, split: bool = False):
         cfg, dev = model.cfg, model.device
         if max_len % CHUNK:
             raise ValueError(f"max_len must be a multiple of {CHUNK}")
@@ -89,6 +89,11 @@ class StaticState:
         self.probs = torch.zeros(R, V, dtype=torch.float32, device=dev) if want_probs else None
         self.cum = torch.zeros(R, V + 1, dtype=torch.int32, device=dev) if want_cdf else None
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        # split mode: a second stream + ordering events, owned here (the C-ABI never allocates)
+        self.split = bool(split) and B >= 2
+        self.aux_stream = torch.cuda.Stream(device=dev) if self.split else None
+        self.sync_events = (hiprt.EventArray(2 * model.n_slots + 2, timing=False)
+                            if self.split else None)
         self._descs: dict[int, _lib.StepDesc] = {}
         desc = self._desc(0)
         nbytes = _lib.load().altxs_step_workspace_bytes(ctypes.byref(desc))
@@ -165,8 +170,10 @@ class StepModel:
         return t
 
     def make_static_state(self, max_len: int, device=None, win: int = 1, batch: int = 1,
-                          want_probs: bool = True, want_cdf: bool = True) -> StaticState:
-        return StaticState(self, batch, win, max_len, want_probs, want_cdf)
+                          want_probs: bool = True, want_cdf: bool = True,
+                          split: bool = False) -> StaticState:
+        """``split``: run the segments as two groups on two streams (B >= 2)."""
+        return StaticState(self, batch, win, max_len, want_probs, want_cdf, split)
 
     def _fill_desc(self, st: StaticState, flags: int) -> _lib.StepDesc:
         cfg = self.cfg
@@ -236,6 +243,9 @@ class StepModel:
         d.probs = st.probs.data_ptr() if st.probs is not None else None
         d.cum = st.cum.data_ptr() if st.cum is not None else None
         d.err = st.err.data_ptr()
+        if getattr(st, "split", False):
+            d.aux_stream = int(st.aux_stream.cuda_stream)
+            d.sync_events = st.sync_events.ptr
         return d
 
     # ---- the step -------------------------------------------------------------

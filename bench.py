@@ -95,6 +95,8 @@ def main() -> int:
     ap.add_argument("--act", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--kv", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
+    ap.add_argument("--streams", type=int, default=1, choices=[1, 2],
+                    help="2: two segment groups on two streams, attention launches alternating")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
@@ -119,7 +121,9 @@ def main() -> int:
     sm = synth.make_model(cfg)
     log(f"model {a.profile}: {sm.bits_summary()['bpw']:.4f} bpw, built in {time.time() - t0:.1f}s")
     model = StepModel(sm, act=a.act, kv=a.kv)
-    st = model.make_static_state(max_len, win=1, batch=B, want_probs=False, want_cdf=True)
+    st = model.make_static_state(max_len, win=1, batch=B, want_probs=False, want_cdf=True,
+                                 split=a.streams == 2)
+    groups = 2 if st.split else 1
     g = torch.Generator(device="cuda").manual_seed(0)
     st.kv.normal_(generator=g)
     st.pos.fill_(ctx - 1)
@@ -162,23 +166,25 @@ def main() -> int:
 
     # ---- dominant kernel: HIP events around every attention launch ----------
     n_slots = model.n_slots
-    ev = hiprt.EventArray(2 * n_slots * a.steps)
+    per_step = 2 * n_slots * groups
+    ev = hiprt.EventArray(per_step * a.steps)
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     s0.record()
     for k in range(a.steps):
-        model.step(st, attn_events=ev.ptr + k * 2 * n_slots * 8)
+        model.step(st, attn_events=ev.ptr + k * per_step * 8)
     s1.record()
     torch.cuda.synchronize()
     eager_ms = s0.elapsed_time(s1) / a.steps
-    durs = [ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(n_slots * a.steps)]
+    durs = [ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(n_slots * groups * a.steps)]
     ev.close()
     attn_ms = float(np.mean(durs))
     kvb = 2 if a.kv == "bf16" else 4
     ab = synth.algorithmic_step_bytes(sm, B, ctx, kv_bytes=kvb)
     ybytes = 2 if a.act == "bf16" else 4
+    # algorithmic bytes of one attention launch (one slot, one group: B/groups segments)
     attn_bytes = (ab["kv_read"] // ab["n_slots"] + B * cfg.num_heads * cfg.head_dim * (4 + ybytes)
-                  + B * cfg.num_heads * 4)
+                  + B * cfg.num_heads * 4) / groups
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
     step_gbs = ab["total"] / (ms * 1e-3) / 1e9
     log(f"attention: {attn_ms * 1e3:.1f} us/launch, {achieved:.0f} GB/s; eager step {eager_ms:.3f} ms; "
@@ -211,10 +217,11 @@ def main() -> int:
                          f"{sm.bits_summary()['bpw']:.3f} bpw group-64 weights, "
                          f"{a.act} activations, {a.kv} KV"),
             "segments": B, "ctx": ctx, "timing": "hip-graph" if graph is not None else "eager",
+            "streams": groups,
             "eager_ms_per_step": round(eager_ms, 4),
         },
         "roofline": {
-            "kernel": "attn_kernel (decode attention)",
+            "kernel": "attn_mfma_kernel (decode attention)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define ALTXS_ABI_VERSION 2
+#define ALTXS_ABI_VERSION 3
 
 enum {
   ALTXS_OK = 0,
@@ -234,10 +234,18 @@ typedef struct AltxsStepDesc {
   float *probs;          /* [B*W, V] or NULL */
   uint32_t *cum;         /* [B*W, V+1] or NULL */
   int32_t *err;          /* [1] device error word */
-  /* Optional timing hook: NULL, or 2*n_slots hipEvent_t handles; events 2s and
-   * 2s+1 are recorded on `stream` right before and after slot s's attention
-   * launch (the dominant kernel), so a caller can time it on its own stream. */
+  /* Optional timing hook: NULL, or hipEvent_t handles recorded right before and
+   * after every attention launch (the dominant kernel) on the stream that runs
+   * it: events 2s, 2s+1 for slot s (one group); (g*n_slots + s)*2 + {0,1} for
+   * group g in split mode. */
   void **attn_events;
+  /* Split mode (B >= 2): a second stream and 2*n_slots + 2 caller-created
+   * events (hipEventDisableTiming).  Segments [0, ceil(B/2)) run on `stream`,
+   * the rest on aux_stream; their attention launches alternate so one group's
+   * projections and MLP overlap the other group's KV streaming.  Results are
+   * bit-identical to the single-stream step.  NULL = one stream. */
+  void *aux_stream;
+  void **sync_events;
 } AltxsStepDesc;
 
 /* Workspace bytes altxs_step needs for this descriptor (host-only). */

@@ -181,3 +181,62 @@ def test_step_probs_and_cdf_rule(profile):
     pr = st.probs.cpu()
     assert (pr - torch.softmax(lg.double(), -1).float()).abs().max().item() < 1e-6
     assert np.array_equal(st.cum.cpu().numpy().astype(np.int64), coder.scale_cum(pr.numpy()))
+
+
+@pytest.mark.parametrize("profile,W", [("tiny", 1), ("cfg1", 1), ("tiny", 4)])
+def test_split_streams_bit_identical(profile, W):
+    """Two segment groups on two streams (alternating attention) give the same
+    bits as the single-stream step: every kernel is row-local."""
+    from altxs_amd.model import StepModel
+
+    _log(f"split streams {profile} W={W}")
+    sm = _synth(profile)
+    toks = _tokens(profile)
+    B, T = toks.shape
+    outs = []
+    for split in (False, True):
+        model = StepModel(sm, act="bf16")
+        st = model.make_static_state(256, win=W, batch=B, split=split)
+        assert st.split == split
+        lg, cm = [], []
+        for w0 in range(0, T, W):
+            st.token.copy_(torch.from_numpy(toks[:, w0:w0 + W].astype(np.int32)))
+            model.step(st, commit=True)
+            lg.append(st.logits.cpu().clone())
+            cm.append(st.cum.cpu().clone())
+        torch.cuda.synchronize()
+        st.check_errors()
+        outs.append((torch.stack(lg), torch.stack(cm), st.pos.cpu().clone()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][2], outs[1][2])
+
+
+def test_split_streams_graph_replay():
+    """The two-stream step captures into one graph; replays match eager steps."""
+    from altxs_amd.model import StepModel
+
+    _log("split streams graph replay")
+    sm = _synth("cfg1")
+    B = 4
+    toks = torch.from_numpy(_tokens("cfg1")[:2, :2].reshape(-1)[:B].reshape(B, 1).astype(np.int32))
+    model = StepModel(sm, act="bf16")
+    st = model.make_static_state(256, win=1, batch=B, split=True)
+    st.token.copy_(toks)
+    st.pos.fill_(7)
+    model.step(st)
+    torch.cuda.synchronize()
+    want = st.cum.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        model.step(st)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        model.step(st)
+    for _ in range(3):
+        st.cum.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(st.cum, want)
