@@ -12,7 +12,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libaltxs_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MAX_LAYERS = 32
 MAX_SLOTS = 64
@@ -43,6 +43,8 @@ EXPORTS = (
     "altxs_qgemm_stream",
     "altxs_decode_attn",
     "altxs_step_workspace_bytes",
+    "altxs_step_plan_bytes",
+    "altxs_step_plan_build",
     "altxs_step",
 )
 
@@ -110,7 +112,9 @@ class StepDesc(ctypes.Structure):
                 ("logits", ctypes.c_void_p), ("probs", ctypes.c_void_p),
                 ("cum", ctypes.c_void_p), ("err", ctypes.c_void_p),
                 ("attn_events", ctypes.c_void_p),
-                ("aux_stream", ctypes.c_void_p), ("sync_events", ctypes.c_void_p)]
+                ("aux_stream", ctypes.c_void_p), ("sync_events", ctypes.c_void_p),
+                ("plan_dev", ctypes.c_void_p), ("plan_host", ctypes.c_void_p),
+                ("plan_bytes", ctypes.c_int64)]
 
 
 _lib = None
@@ -149,6 +153,10 @@ def load(path: str | None = None):
     L.altxs_decode_attn.argtypes = [ctypes.POINTER(AttnArgs), p]
     L.altxs_step_workspace_bytes.restype = i64
     L.altxs_step_workspace_bytes.argtypes = [ctypes.POINTER(StepDesc)]
+    L.altxs_step_plan_bytes.restype = i64
+    L.altxs_step_plan_bytes.argtypes = [ctypes.POINTER(StepDesc)]
+    L.altxs_step_plan_build.restype = i32
+    L.altxs_step_plan_build.argtypes = [ctypes.POINTER(StepDesc), p, p, i64, p]
     L.altxs_step.restype = i32
     L.altxs_step.argtypes = [ctypes.POINTER(StepDesc), p]
     v = L.altxs_abi_version()

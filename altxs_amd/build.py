@@ -21,7 +21,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libaltxs_hip.so")
 BUILD_DIR = os.path.join(ROOT, "_build", "altxs_hip")
-SOURCES = ("api.cpp", "cdf.hip", "qgemm.hip", "attn.hip", "step.hip")
+SOURCES = ("api.cpp", "cdf.hip", "qgemm.hip", "attn.hip", "step.hip", "persist.hip")
 ARCH = os.environ.get("ALTXS_ARCH", "gfx950")
 
 
@@ -51,7 +51,7 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 5) -> str:
+def build(jobs: int = 6) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(_compile, SOURCES))

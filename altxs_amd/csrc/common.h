@@ -104,6 +104,7 @@ __device__ __forceinline__ float rows_max(float v) {
 enum : int32_t {
   ALTXS_EDEV_POS = 1,    // position >= max_len (KV write/read skipped)
   ALTXS_EDEV_TOKEN = 2,  // token id outside [0, V) (clamped)
+  ALTXS_EDEV_SPIN = 4,   // a persistent-kernel wait gave up (results invalid, kernel exited)
 };
 __device__ __forceinline__ void flag_err(int32_t* err, int32_t code) {
   if (err) atomicOr(err, code);

@@ -38,7 +38,11 @@
 
 namespace altxs {
 
+// BITS == 0 selects the run-time bit-width specialisation: one code path that
+// decodes any width with uniform selects (used where one kernel serves tensors
+// of several widths); it feeds the MFMAs exactly the operands of BITS = b.
 template <int BITS> struct Planes;
+template <> struct Planes<0> { static constexpr int P0 = 4, P1 = 2; };  // storage maxima
 template <> struct Planes<2> { static constexpr int P0 = 2, P1 = 0; };
 template <> struct Planes<3> { static constexpr int P0 = 2, P1 = 1; };
 template <> struct Planes<4> { static constexpr int P0 = 4, P1 = 0; };
@@ -51,6 +55,7 @@ struct QT {
   const uint8_t* codes;
   const uint16_t* scales;
   int N, K;
+  int bits;  // read only by the run-time-width specialisation (BITS == 0)
 };
 
 __host__ __device__ constexpr int lds_stride(int K, int am) { return K + (am == A_F32 ? 4 : 8); }
@@ -97,11 +102,53 @@ __device__ __forceinline__ void codes_step(const uint32_t* p0, const uint32_t* p
   }
 }
 
+// Run-time width (BITS == 0).  A block is loaded in its stored layout and, once
+// its data is in registers, rewritten in place into the 6-bit layout: p0[s]
+// holds the low nibbles of k-step s (code i at bits 4i), p1[s >> 1] the two
+// high bits (code i at bits 16 (s & 1) + 2i).  Codes of 2 and 3 bits fit in a
+// nibble, so their p1 is zero.  Every index is a compile-time constant and the
+// only branch is on the (uniform) width, so nothing goes to scratch.
+__device__ __forceinline__ uint32_t spread2to4(uint32_t x) {  // 8 fields of 2 bits -> nibbles
+  x = (x | (x << 8)) & 0x00FF00FFu;
+  x = (x | (x << 4)) & 0x0F0F0F0Fu;
+  return (x | (x << 2)) & 0x33333333u;
+}
+__device__ __forceinline__ uint32_t spread1to4(uint32_t x) {  // 8 bits -> bit i at 4i
+  x = (x | (x << 12)) & 0x000F000Fu;
+  x = (x | (x << 6)) & 0x03030303u;
+  return (x | (x << 3)) & 0x11111111u;
+}
+__device__ __forceinline__ void planes_to6(int bits, uint32_t (&p0)[8], uint32_t (&p1)[4]) {
+  if (bits <= 3) {
+    uint32_t t[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) t[s] = spread2to4((p0[s >> 1] >> (16 * (s & 1))) & 0xFFFFu);
+    if (bits == 3) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) t[s] |= spread1to4((p1[s >> 2] >> (8 * (s & 3))) & 0xFFu) << 2;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) p0[s] = t[s];
+  }
+  if (bits != 6) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p1[i] = 0u;
+  }
+}
+
 template <int BITS>
-__device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* p1, int s) {
-  constexpr float center = 0.5f * (float)((1 << BITS) - 1);
+__device__ __forceinline__ float code_center(int bits) {
+  if constexpr (BITS == 0) return 0.5f * (float)((1 << bits) - 1);
+  else return 0.5f * (float)((1 << BITS) - 1);
+}
+
+// B operand of k-step s: codes - center.  BITS == 0 expects the 6-bit layout
+// (planes_to6 already applied).
+template <int BITS>
+__device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
+  const float center = code_center<BITS>(bits);
   uint32_t c[8];
-  codes_step<BITS>(p0, p1, s, c);
+  codes_step<BITS == 0 ? 6 : BITS>(p0, p1, s, c);
   bf16x8 r;
 #pragma unroll
   for (int i = 0; i < 8; ++i) r[i] = (__bf16)((float)c[i] - center);
@@ -109,10 +156,10 @@ __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* 
 }
 
 template <int BITS>
-__device__ __forceinline__ f16x8 b_op_f16(const uint32_t* p0, const uint32_t* p1, int s) {
-  constexpr float center = 0.5f * (float)((1 << BITS) - 1);
+__device__ __forceinline__ f16x8 b_op_f16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
+  const float center = code_center<BITS>(bits);
   uint32_t c[8];
-  codes_step<BITS>(p0, p1, s, c);
+  codes_step<BITS == 0 ? 6 : BITS>(p0, p1, s, c);
   f16x8 r;
 #pragma unroll
   for (int i = 0; i < 8; ++i) r[i] = (_Float16)((float)c[i] - center);
@@ -136,34 +183,64 @@ struct ADirect {
   int64_t batch_stride;  // elements
 };
 
+// Weight codes + scales of block (nb, kb) for this lane.
 template <int BITS, int AM, bool ADIRECT>
-__device__ __forceinline__ void load_blk(Blk<BITS, AM, ADIRECT>& b, const QT& w, int nb, int kb,
-                                         int lane, const ADirect& ad, int m0, int R, int batch) {
-  constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
+__device__ __forceinline__ void load_w(Blk<BITS, AM, ADIRECT>& b, const QT& w, int nb, int kb,
+                                       int lane) {
   const int KB = w.K >> 8;
   const size_t bi = (size_t)nb * KB + kb;
-  const uint8_t* blk = w.codes + bi * (512 * BITS);
-  const uint8_t* a0 = blk + lane * (8 * P0);
-  if constexpr (P0 == 4) {
+  if constexpr (BITS == 0) {
+    // every element is defined on every path (whole-vector phis), so the block
+    // stays in registers; the branches are on the uniform width only
+    const int nbits = w.bits;
+    const bool wide = nbits >= 4;
+    const uint8_t* blk = w.codes + bi * (512 * nbits);
+    const uint8_t* a0 = blk + lane * (wide ? 32 : 16);
+    const uint8_t* a1 = blk + 512 * (wide ? 4 : 2);
     const u32x4 x = *(const u32x4*)a0;
-    const u32x4 y = *(const u32x4*)(a0 + 16);
+    u32x4 y = {0u, 0u, 0u, 0u}, z = {0u, 0u, 0u, 0u};
+    if (wide) y = *(const u32x4*)(a0 + 16);
+    if (nbits == 6) {
+      z = *(const u32x4*)(a1 + lane * 16);
+    } else if (nbits == 3) {
+      const u32x2 t = *(const u32x2*)(a1 + lane * 8);
+      z = u32x4{t[0], t[1], 0u, 0u};
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { b.p0[i] = x[i]; b.p0[4 + i] = y[i]; }
+    for (int i = 0; i < 4; ++i) { b.p0[i] = x[i]; b.p0[4 + i] = y[i]; b.p1[i] = z[i]; }
+    const u32x2 sv = *(const u32x2*)(w.scales + bi * 64 + (lane & 15) * 4);
+    b.sc[0] = sv[0]; b.sc[1] = sv[1];
   } else {
-    const u32x4 x = *(const u32x4*)a0;
+    constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
+    const uint8_t* blk = w.codes + bi * (512 * BITS);
+    const uint8_t* a0 = blk + lane * (8 * P0);
+    if constexpr (P0 == 4) {
+      const u32x4 x = *(const u32x4*)a0;
+      const u32x4 y = *(const u32x4*)(a0 + 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) b.p0[i] = x[i];
-  }
-  if constexpr (P1 == 1) {
-    const u32x2 x = *(const u32x2*)(blk + 512 * P0 + lane * 8);
-    b.p1[0] = x[0]; b.p1[1] = x[1];
-  } else if constexpr (P1 == 2) {
-    const u32x4 x = *(const u32x4*)(blk + 512 * P0 + lane * 16);
+      for (int i = 0; i < 4; ++i) { b.p0[i] = x[i]; b.p0[4 + i] = y[i]; }
+    } else {
+      const u32x4 x = *(const u32x4*)a0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) b.p1[i] = x[i];
+      for (int i = 0; i < 4; ++i) b.p0[i] = x[i];
+    }
+    if constexpr (P1 == 1) {
+      const u32x2 x = *(const u32x2*)(blk + 512 * P0 + lane * 8);
+      b.p1[0] = x[0]; b.p1[1] = x[1];
+    } else if constexpr (P1 == 2) {
+      const u32x4 x = *(const u32x4*)(blk + 512 * P0 + lane * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b.p1[i] = x[i];
+    }
+    const u32x2 sv = *(const u32x2*)(w.scales + bi * 64 + (lane & 15) * 4);
+    b.sc[0] = sv[0]; b.sc[1] = sv[1];
   }
-  const u32x2 sv = *(const u32x2*)(w.scales + bi * 64 + (lane & 15) * 4);
-  b.sc[0] = sv[0]; b.sc[1] = sv[1];
+}
+
+// The lane's slice of the A rows for block column kb (direct A only).
+template <int BITS, int AM, bool ADIRECT>
+__device__ __forceinline__ void load_a(Blk<BITS, AM, ADIRECT>& b, const QT& w, int kb, int lane,
+                                       const ADirect& ad, int m0, int R, int batch) {
   if constexpr (ADIRECT) {
     const int r = m0 + (lane & 15);
     const int kc = kb * 256 + 8 * (lane >> 4);
@@ -186,6 +263,20 @@ __device__ __forceinline__ void load_blk(Blk<BITS, AM, ADIRECT>& b, const QT& w,
     }
   }
 }
+
+template <int BITS, int AM, bool ADIRECT>
+__device__ __forceinline__ void load_blk(Blk<BITS, AM, ADIRECT>& b, const QT& w, int nb, int kb,
+                                         int lane, const ADirect& ad, int m0, int R, int batch) {
+  load_w(b, w, nb, kb, lane);
+  load_a(b, w, kb, lane, ad, m0, R, batch);
+}
+
+// Dependency hook of a task: runs after the first tile's weight loads are
+// issued and before anything that reads activations.  NoWait for kernels
+// whose inputs were produced by earlier launches.
+struct NoWait {
+  __device__ void operator()() const {}
+};
 
 __device__ __forceinline__ float half_lo(uint32_t v) {
   return __half2float(__ushort_as_half((uint16_t)(v & 0xffffu)));
@@ -211,9 +302,16 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8& a0, bf16x8& 
 // acc += W-block . A-slice (one 16x256 block, 8 MFMA k-steps).
 template <int BITS, int AM, bool ADIRECT>
 __device__ __forceinline__ void compute_blk(const Blk<BITS, AM, ADIRECT>& b, const void* As, int K,
-                                            int kb, int lane, f32x4& acc) {
+                                            int kb, int lane, f32x4& acc, int bits = BITS) {
   const float scale[4] = {half_lo(b.sc[0]), half_hi(b.sc[0]), half_lo(b.sc[1]), half_hi(b.sc[1])};
   const int row = lane & 15;
+  constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
+  uint32_t q0[2 * P0], q1[P1 > 0 ? 2 * P1 : 1];
+#pragma unroll
+  for (int i = 0; i < 2 * P0; ++i) q0[i] = b.p0[i];
+#pragma unroll
+  for (int i = 0; i < (P1 > 0 ? 2 * P1 : 1); ++i) q1[i] = b.p1[i];
+  if constexpr (BITS == 0) planes_to6(bits, q0, q1);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
@@ -235,7 +333,7 @@ __device__ __forceinline__ void compute_blk(const Blk<BITS, AM, ADIRECT>& b, con
         }
         bf16x8 a0, a1, a2;
         split3(x, a0, a1, a2);
-        const bf16x8 bo = b_op_bf16<BITS>(b.p0, b.p1, s);
+        const bf16x8 bo = b_op_bf16<BITS>(q0, q1, s, bits);
         t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bo, t, 0, 0, 0);
         t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bo, t, 0, 0, 0);
         t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bo, t, 0, 0, 0);
@@ -244,10 +342,10 @@ __device__ __forceinline__ void compute_blk(const Blk<BITS, AM, ADIRECT>& b, con
         if constexpr (ADIRECT) araw = b.a[s];
         else araw = *(const u32x4*)((const uint16_t*)As + row * lds_stride(K, AM) + kc);
         if constexpr (AM == A_BF16) {
-          const bf16x8 bo = b_op_bf16<BITS>(b.p0, b.p1, s);
+          const bf16x8 bo = b_op_bf16<BITS>(q0, q1, s, bits);
           t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, araw), bo, t, 0, 0, 0);
         } else {
-          const f16x8 bo = b_op_f16<BITS>(b.p0, b.p1, s);
+          const f16x8 bo = b_op_f16<BITS>(q0, q1, s, bits);
           t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, araw), bo, t, 0, 0, 0);
         }
       }
@@ -282,10 +380,11 @@ __host__ __device__ constexpr size_t task_lds_bytes(int K) {
 }
 
 // One task: rows [m0, m0+16) x column tiles nt0, nt0 + nstep, ... < ntiles.
-template <int BITS, int AM, int NB, int KS, class Pro, class Epi>
+template <int BITS, int AM, int NB, int KS, class Pro, class Epi, class Wait = NoWait>
 __device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, int nstep,
                                           const ADirect& ad, const Pro& pro, const Epi& epi,
-                                          unsigned char* smem, int batch = 0) {
+                                          unsigned char* smem, int batch = 0,
+                                          const Wait& wait = Wait{}) {
   using Cfg = TileCfg<NB, KS>;
   constexpr bool STAGE = Pro::kStage;
   constexpr bool ADIRECT = !STAGE;
@@ -300,14 +399,25 @@ __device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, i
   void* scratch = smem + a_bytes + (size_t)KS * 16 * Cfg::CS * 4;
 
   Blk<BITS, AM, ADIRECT> b0, b1;
-  auto issue = [&](int nt) {
+  auto issue_w = [&](int nt) {
     const int nb = nt * NB + nbi;
     if (nb * 16 < w.N) {
-      if (kb0 < kb1) load_blk(b0, w, nb, kb0, lane, ad, m0, R, batch);
-      if (kb0 + 1 < kb1) load_blk(b1, w, nb, kb0 + 1, lane, ad, m0, R, batch);
+      if (kb0 < kb1) load_w(b0, w, nb, kb0, lane);
+      if (kb0 + 1 < kb1) load_w(b1, w, nb, kb0 + 1, lane);
     }
   };
-  if (nt0 < ntiles) issue(nt0);
+  auto issue_a = [&](int nt) {
+    if constexpr (ADIRECT) {
+      if ((nt * NB + nbi) * 16 < w.N) {
+        if (kb0 < kb1) load_a(b0, w, kb0, lane, ad, m0, R, batch);
+        if (kb0 + 1 < kb1) load_a(b1, w, kb0 + 1, lane, ad, m0, R, batch);
+      }
+    }
+  };
+  auto issue = [&](int nt) { issue_w(nt); issue_a(nt); };
+  if (nt0 < ntiles) issue_w(nt0);
+  wait();
+  if (nt0 < ntiles) issue_a(nt0);
   if constexpr (STAGE) {
     pro.template stage<AM, Cfg::THREADS>(As, scratch, m0, R, w.K, batch, nt0 == 0);
     __syncthreads();
@@ -320,10 +430,10 @@ __device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, i
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (active) {
       for (int kb = kb0; kb < kb1; kb += 2) {
-        compute_blk(b0, As, w.K, kb, lane, acc);
+        compute_blk(b0, As, w.K, kb, lane, acc, w.bits);
         if (kb + 2 < kb1) load_blk(b0, w, nb, kb + 2, lane, ad, m0, R, batch);
         if (kb + 1 < kb1) {
-          compute_blk(b1, As, w.K, kb + 1, lane, acc);
+          compute_blk(b1, As, w.K, kb + 1, lane, acc, w.bits);
           if (kb + 3 < kb1) load_blk(b1, w, nb, kb + 3, lane, ad, m0, R, batch);
         }
       }
@@ -446,19 +556,6 @@ hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect&
     case 4: return launch_gemm_bits<AM, 1, 4>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
     case 2: return launch_gemm_bits<AM, 2, 2>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
     default: return launch_gemm_bits<AM, 4, 1>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
-  }
-}
-
-// Run a task with the bit width chosen at run time (uniform branch).
-template <int AM, int NB, int KS, class Pro, class Epi>
-__device__ __forceinline__ void gemm_task_bits(int bits, const QT& w, int R, int m0, int nt0,
-                                               int nstep, const ADirect& ad, const Pro& pro,
-                                               const Epi& epi, unsigned char* smem) {
-  switch (bits) {
-    case 2: gemm_task<2, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
-    case 3: gemm_task<3, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
-    case 4: gemm_task<4, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
-    default: gemm_task<6, AM, NB, KS>(w, R, m0, nt0, nstep, ad, pro, epi, smem); break;
   }
 }
 

@@ -48,6 +48,7 @@ QT to_qt(const AltxsQTensor* w) {
   q.scales = (const uint16_t*)w->scales;
   q.N = (int)w->N;
   q.K = (int)w->K;
+  q.bits = w->bits;
   return q;
 }
 

@@ -22,606 +22,20 @@
 // 1649-1781.
 #include <string.h>
 
+#include <vector>
+
 #include "common.h"
 #include "kernels.h"
-#include "gemm.h"
+#include "persist.h"
+#include "step_ops.h"
 
 using namespace altxs;
+using namespace altxs_sk;
 
 namespace {
 
-constexpr int HD = 64;
-
-// torch.lerp(start, end, w) (ATen's two-branch formula)
-__device__ __forceinline__ float lerp_t(float start, float end, float w) {
-  return (fabsf(w) < 0.5f) ? start + w * (end - start) : end - (end - start) * (1.f - w);
-}
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
-// tanh(x) = sign(x) * (1 - 2 / (exp(2|x|) + 1)); absolute error ~1e-7.
-__device__ __forceinline__ float tanh_fast(float x) {
-  const float e = __expf(2.f * fabsf(x));
-  return copysignf(1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f), x);
-}
-
-// ---- embedding (+ SmearGate) ------------------------------------------------
-
-// Dequantise 8 consecutive weights [8*run, 8*run+8) of row n of a packed tensor.
-template <int BITS>
-__device__ void dequant_run(const QT& w, int n, int run, float (&out)[8]) {
-  constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
-  constexpr float center = 0.5f * (float)((1 << BITS) - 1);
-  const int KB = w.K >> 8;
-  const int k0 = 8 * run, kb = k0 >> 8, kk = k0 & 255;
-  const int s = kk >> 5, lg = (kk & 31) >> 3;
-  const int L = (n & 15) + 16 * lg;
-  const size_t bi = (size_t)(n >> 4) * KB + kb;
-  const uint8_t* blk = w.codes + bi * (512 * BITS);
-  uint32_t p0[2 * P0], p1[P1 > 0 ? 2 * P1 : 1];
-  const uint32_t* a0 = (const uint32_t*)(blk + L * (8 * P0));
-#pragma unroll
-  for (int i = 0; i < 2 * P0; ++i) p0[i] = a0[i];
-  if constexpr (P1 > 0) {
-    const uint32_t* a1 = (const uint32_t*)(blk + 512 * P0 + L * (8 * P1));
-#pragma unroll
-    for (int i = 0; i < 2 * P1; ++i) p1[i] = a1[i];
-  }
-  uint32_t c[8];
-  codes_step<BITS>(p0, p1, s, c);
-  const float sc = __half2float(__ushort_as_half(w.scales[bi * 64 + (n & 15) * 4 + (kk >> 6)]));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = ((float)c[i] - center) * sc;
-}
-
-__device__ void dequant_run_bits(int bits, const QT& w, int n, int run, float (&out)[8]) {
-  switch (bits) {
-    case 2: dequant_run<2>(w, n, run, out); break;
-    case 3: dequant_run<3>(w, n, run, out); break;
-    case 4: dequant_run<4>(w, n, run, out); break;
-    default: dequant_run<6>(w, n, run, out); break;
-  }
-}
-
-struct EmbedP {
-  QT emb;
-  int bits, V, D, W, gw, smear;
-  float eps;
-  const int32_t* tokens;
-  const float* prev_raw;
-  float* cand_raw;
-  const float* smear_w;
-  const float* smear_lambda;
-  float* x0;  // [R, D]
-  int32_t* err;
-  int* sync;  // step counters, zeroed here (this is the step's first kernel)
-  int nsync;
-  const float* mix0;  // resid_mix of slot 0's layer [2, D]
-  float* xin0;        // slot 0's x_in = m0*x0 + m1*x0 (sequential, no skip)
-};
-
-constexpr int MAX_RUNS = 4;  // D <= 64 lanes * 4 runs * 8 = 2048
-
-__global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
-  const int r = blockIdx.x, lane = threadIdx.x;
-  if (r == 0)
-    for (int i = lane; i < a.nsync; i += 64) a.sync[i] = 0;
-  const int b = r / a.W, t = r % a.W;
-  auto tok_at = [&](int tt) {
-    int tk = a.tokens[(int64_t)b * a.W + tt];
-    if (tk < 0 || tk >= a.V) {
-      if (lane == 0) flag_err(a.err, ALTXS_EDEV_TOKEN);
-      tk = tk < 0 ? 0 : a.V - 1;
-    }
-    return tk;
-  };
-  const int tok = tok_at(t);
-  const int nruns = a.D / 8;
-  float raw[MAX_RUNS][8], prev[MAX_RUNS][8];
-#pragma unroll
-  for (int j = 0; j < MAX_RUNS; ++j) {
-    const int run = lane + 64 * j;
-    if (run < nruns) dequant_run_bits(a.bits, a.emb, tok, run, raw[j]);
-  }
-  float x[MAX_RUNS][8];
-  if (a.smear) {
-    const int ptok = t > 0 ? tok_at(t - 1) : -1;
-#pragma unroll
-    for (int j = 0; j < MAX_RUNS; ++j) {
-      const int run = lane + 64 * j;
-      if (run >= nruns) continue;
-      if (ptok >= 0) {
-        dequant_run_bits(a.bits, a.emb, ptok, run, prev[j]);
-      } else {
-        const float* pr = a.prev_raw + (int64_t)b * a.D + 8 * run;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) prev[j][i] = pr[i];
-      }
-    }
-    // g = lambda * sigmoid(raw[:gw] . w_smear)
-    float part = 0.f;
-#pragma unroll
-    for (int j = 0; j < MAX_RUNS; ++j) {
-      const int run = lane + 64 * j;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = 8 * run + i;
-        if (run < nruns && k < a.gw) part += raw[j][i] * a.smear_w[k];
-      }
-    }
-    const float gsum = wave_sum(part);
-    const float g = a.smear_lambda[0] * sigmoidf(gsum);
-#pragma unroll
-    for (int j = 0; j < MAX_RUNS; ++j)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[j][i] = raw[j][i] + g * prev[j][i];
-  } else {
-#pragma unroll
-    for (int j = 0; j < MAX_RUNS; ++j)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[j][i] = raw[j][i];
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < MAX_RUNS; ++j)
-    if (lane + 64 * j < nruns)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss += x[j][i] * x[j][i];
-  ss = wave_sum(ss);
-  const float inv = rsqrtf(ss / (float)a.D + a.eps);
-#pragma unroll
-  for (int j = 0; j < MAX_RUNS; ++j) {
-    const int run = lane + 64 * j;
-    if (run >= nruns) continue;
-    float* xo = a.x0 + (int64_t)r * a.D + 8 * run;
-    float* xi = a.xin0 + (int64_t)r * a.D + 8 * run;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float v = x[j][i] * inv;
-      xo[i] = v;
-      xi[i] = a.mix0[8 * run + i] * v + a.mix0[a.D + 8 * run + i] * v;
-    }
-    if (t == a.W - 1) {
-      float* co = a.cand_raw + (int64_t)b * a.D + 8 * run;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) co[i] = raw[j][i];
-    }
-  }
-}
-
-// ---- prologues -------------------------------------------------------------
-//
-// 256 threads stage the 16-row A tile: 16 lanes per row, each lane owning the
-// float4 chunks c = lane + 16*j of the row (D <= 512 -> j < 8).  All loads of
-// a row are issued before any arithmetic; the row's RMS is a 16-lane butterfly.
-
-constexpr int PTPR = 16;                  // prologue threads per row
-constexpr int PMAXJ = 512 / 4 / PTPR;     // float4 chunks per lane (D <= 512)
-
-
-// RMSNorm (* scale) of 16 rows of x staged as the A tile.  Inputs of the
-// attention side (the QKV prologue) also carry the sparse attention gate
-// (model.py:854-862): the task that owns column tile 0 (`first`) forms
-// sigmoid(gate_scale * n[:gw] . W_gate[h]) for every head from the normalised
-// row.  The final norm before the LM head may average the two parallel lanes.
-struct ProNorm {
-  static constexpr bool kStage = true;
-  static constexpr size_t kScratch = 0;
-  const float* x;
-  const float* x2;  // second lane (final parallel "mean") or NULL
-  int lane_mode;    // 0: x, 1: 0.5*(x + x2)
-  float scale, eps;
-  int D;
-  const float* gate_w = nullptr;  // [H, gw] or NULL
-  float* gate_out = nullptr;      // [R, H]
-  float gate_scale = 0.f;
-  int H = 0, gw = 0;
-  template <int AM, int NT>
-  __device__ void stage(void* As, void*, int m0, int R, int K, int, bool first) const {
-    static_assert(NT == 16 * PTPR, "one row per 16 lanes, 16 rows per task");
-    constexpr int HMAX = 8;  // D <= 512 -> H <= 8
-    const int t = threadIdx.x, row = t / PTPR, li = t % PTPR;
-    const int r = m0 + row;
-    const int nch = D >> 2;
-    f32x4 v[PMAXJ], v2[PMAXJ];
-#pragma unroll
-    for (int j = 0; j < PMAXJ; ++j) {
-      const int c = li + PTPR * j;
-      if (c < nch && r < R) {
-        v[j] = *(const f32x4*)(x + (int64_t)r * D + 4 * c);
-        if (lane_mode == 1) v2[j] = *(const f32x4*)(x2 + (int64_t)r * D + 4 * c);
-      }
-    }
-    const bool gating = first && gate_w;
-    float gwv[HMAX][4];
-    if (gating) {  // gate of head h reads features [0, gw), gw <= 16: lanes 0-3, chunk 0
-#pragma unroll
-      for (int h = 0; h < HMAX; ++h)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          gwv[h][e] = (h < H && 4 * li + e < gw) ? gate_w[h * gw + 4 * li + e] : 0.f;
-    }
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < PMAXJ; ++j) {
-      const int c = li + PTPR * j;
-      if (c >= nch) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float y = r < R ? v[j][e] : 0.f;
-        if (lane_mode == 1 && r < R) y = 0.5f * (v[j][e] + v2[j][e]);
-        v[j][e] = y;
-        ss += y * y;
-      }
-    }
-    ss = row16_sum(ss);
-    const float inv = r < R ? rsqrtf(ss / (float)D + eps) : 0.f;
-    float n0[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < PMAXJ; ++j) {
-      const int c = li + PTPR * j;
-      if (c >= nch) continue;
-      float n[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) n[e] = (v[j][e] * inv) * scale;
-      if (j == 0) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) n0[e] = n[e];
-      }
-      a_store4<AM>(As, row, 4 * c, K, n);
-    }
-    if (gating) {
-      float part[HMAX];
-#pragma unroll
-      for (int h = 0; h < HMAX; ++h) {
-        part[h] = 0.f;
-        if (li < 4) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) part[h] += n0[e] * gwv[h][e];
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < HMAX; ++h) part[h] = row16_sum(part[h]);
-      if (li < H && r < R) {
-        float dot = part[0];
-#pragma unroll
-        for (int h = 1; h < HMAX; ++h) dot = li == h ? part[h] : dot;
-        gate_out[(int64_t)r * H + li] = sigmoidf(gate_scale * dot);
-      }
-    }
-  }
-};
-
-// The next slot's inputs, formed elementwise where the current slot's output
-// is produced (DOWN epilogue; the embedding for slot 0): decoder skip (lerp
-// gate or add, model.py:1275-1291), then resid_mix with x0 (model.py:947-950,
-// 1310-1316).  base = x_in (sequential) or lane0 after the skip (parallel) --
-// the residual base the O/DOWN epilogues of that slot use; attn = the
-// pre-RMSNorm attention input m0*base + m1*x0.
-struct NextIn {
-  const float* x0 = nullptr;
-  const float* skip = nullptr;    // popped encoder output or NULL
-  const float* skip_w = nullptr;  // [D]
-  const float* skip_g = nullptr;  // [D] gate logits or NULL
-  const float* mix = nullptr;     // next layer's resid_mix [2, D]
-  float* base = nullptr;          // NULL: no next slot
-  float* attn = nullptr;          // may equal base (sequential slot)
-  int parallel = 0;
-  int skip_self = 0;  // the popped encoder output is the value being produced here
-  struct El { float x0, sk, sw, sg, m0, m1; };
-  __device__ El load(int64_t idx, int c, int D) const {
-    El e;
-    e.x0 = x0[idx];
-    e.m0 = mix[c];
-    e.m1 = mix[D + c];
-    e.sk = (skip && !skip_self) ? skip[idx] : 0.f;
-    e.sw = skip ? skip_w[c] : 0.f;
-    e.sg = skip_g ? skip_g[c] : 0.f;
-    return e;
-  }
-  __device__ void put(int64_t idx, float x, const El& e) const {
-    float bs = x;
-    if (skip) {
-      const float sc = e.sw * (skip_self ? x : e.sk);
-      bs = skip_g ? lerp_t(sc, x, sigmoidf(e.sg)) : x + sc;
-    }
-    const float in = e.m0 * bs + e.m1 * e.x0;
-    base[idx] = parallel ? bs : in;
-    if (attn != base) attn[idx] = in;
-  }
-};
-
-// ---- epilogues --------------------------------------------------------------
-
-__device__ __forceinline__ int row_pos(const int32_t* pos, int W, int r) {
-  return pos[r / W] + (r % W);
-}
-
-// One head (64 columns) per tile: QK-RMSNorm, RoPE, q_gain, KV-cache write.
-struct EpiQKV {
-  float* q;          // [R, H, 64]
-  char* kv;          // this slot's cache: [B][2][Hkv][max_len][64]
-  int kv_bf16, H, Hkv, W, max_len, rd;
-  const int32_t* pos;
-  const float* cosb;  // [max_len, rd/2]
-  const float* sinb;
-  const float* q_gain;
-  float eps;
-  int32_t* err;
-  template <class Cfg> struct Pre {
-    static constexpr int TPR = Cfg::THREADS / 16, CPT = 64 / TPR;
-    int p;
-    float cs[CPT], sn[CPT], gain;
-  };
-  template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int m0, int n0, int R, int) const {
-    using P = Pre<Cfg>;
-    static_assert(Cfg::NCOL == HD, "one head per column tile");
-    P o;
-    const int row = threadIdx.x / P::TPR, c0 = (threadIdx.x % P::TPR) * P::CPT;
-    const int r = m0 + row;
-    o.p = r < R ? row_pos(pos, W, r) : 0;
-    const int nt = n0 / HD;
-    o.gain = nt < H ? q_gain[nt] : 1.f;
-    const int half = rd >> 1;
-    const int pp = (o.p >= 0 && o.p < max_len) ? o.p : 0;
-#pragma unroll
-    for (int i = 0; i < P::CPT; ++i) {
-      const int c = c0 + i;
-      const int fi = c < half ? c : c - half;
-      o.cs[i] = (c < rd && nt < H + Hkv) ? cosb[(int64_t)pp * half + fi] : 1.f;
-      o.sn[i] = (c < rd && nt < H + Hkv) ? sinb[(int64_t)pp * half + fi] : 0.f;
-    }
-    return o;
-  }
-  template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
-    constexpr int TPR = P::TPR, CPT = P::CPT;
-    const int row = threadIdx.x / TPR, li = threadIdx.x % TPR, c0 = li * CPT;
-    const int r = m0 + row;
-    const int nt = n0 / HD;
-    const int kind = nt < H ? 0 : (nt < H + Hkv ? 1 : 2);
-    const int head = kind == 0 ? nt : (kind == 1 ? nt - H : nt - H - Hkv);
-    float v[CPT];
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) v[i] = C[row * Cfg::CS + c0 + i];
-    if (kind < 2) {
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) ss += v[i] * v[i];
-      static_assert(TPR == 16, "a head's 64 columns are one 16-lane row");
-      ss = row16_sum(ss);
-      const float inv = rsqrtf(ss * (1.0f / HD) + eps);
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) v[i] *= inv;
-      // partner column c +- rd/2 lives (rd/2)/CPT lanes away
-      const int off = (rd >> 1) / CPT;
-      float pv[CPT];
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        const float up = __shfl_down(v[i], off, WAVE);
-        const float dn = __shfl_up(v[i], off, WAVE);
-        pv[i] = (c0 < (rd >> 1)) ? up : dn;
-      }
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        const int c = c0 + i;
-        if (c < (rd >> 1)) v[i] = v[i] * pre.cs[i] + pv[i] * pre.sn[i];
-        else if (c < rd) v[i] = pv[i] * -pre.sn[i] + v[i] * pre.cs[i];
-      }
-    }
-    if (r >= R) return;
-    const int p = pre.p;
-    const bool pos_ok = p >= 0 && p < max_len;
-    if (kind == 0) {
-      float* qo = q + ((int64_t)r * H + head) * HD + c0;
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) qo[i] = v[i] * pre.gain;
-    } else if (pos_ok) {
-      const int b = r / W;
-      const int64_t head_base = (((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len * HD;
-      if (kv_bf16) {  // tiled operand layout (kv_tile_k / kv_tile_v)
-        uint16_t* tile = (uint16_t*)kv + head_base + (int64_t)(p / ALTXS_KV_TILE) * (ALTXS_KV_TILE * HD);
-        const int kt = p % ALTXS_KV_TILE;
-#pragma unroll
-        for (int i = 0; i < CPT; ++i)
-          tile[kind == 1 ? kv_tile_k(kt, c0 + i) : kv_tile_v(kt, c0 + i)] = f32_to_bf16(v[i]);
-      } else {
-        float* row = (float*)kv + head_base + (int64_t)p * HD + c0;
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) row[i] = v[i];
-      }
-    } else if (li == 0) {
-      flag_err(err, ALTXS_EDEV_POS);
-    }
-  }
-};
-
-// Elementwise epilogues: thread t handles tile elements t + THREADS*j.
-template <class Cfg> struct EW {
-  static constexpr int EPT = 16 * Cfg::NCOL / Cfg::THREADS;
-  __device__ static int row(int j) { return (threadIdx.x + Cfg::THREADS * j) / Cfg::NCOL; }
-  __device__ static int col(int j) { return (threadIdx.x + Cfg::THREADS * j) % Cfg::NCOL; }
-};
-
-struct EpiO {
-  const float* xin;
-  const float* attn_scale;
-  float* xout;
-  int D, parallel;
-  template <class Cfg> struct Pre { float base[EW<Cfg>::EPT], sc[EW<Cfg>::EPT]; };
-  template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int m0, int n0, int R, int) const {
-    Pre<Cfg> o;
-#pragma unroll
-    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
-      const int r = m0 + EW<Cfg>::row(j), c = n0 + EW<Cfg>::col(j);
-      const bool ok = r < R && c < D;
-      o.base[j] = (ok && !parallel) ? xin[(int64_t)r * D + c] : 0.f;
-      o.sc[j] = ok ? attn_scale[c] : 0.f;
-    }
-    return o;
-  }
-  template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
-#pragma unroll
-    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
-      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
-      const int r = m0 + rr, c = n0 + cc;
-      if (r >= R || c >= D) continue;
-      const float a = pre.sc[j] * C[rr * Cfg::CS + cc];
-      xout[(int64_t)r * D + c] = parallel ? a : pre.base[j] + a;
-    }
-  }
-};
-
-struct EpiUp {
-  void* h;  // [R, F] fp32 or bf16
-  int F, hb16;
-  template <class Cfg> struct Pre {};
-  template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int, int, int, int) const { return {}; }
-  template <class Cfg, class P>
-  __device__ void apply(const float* C, const P&, const void*, int m0, int n0, int R, int) const {
-#pragma unroll
-    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
-      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
-      const int r = m0 + rr, c = n0 + cc;
-      if (r >= R || c >= F) continue;
-      const float v = C[rr * Cfg::CS + cc];
-      const float lr = v > 0.f ? v : 0.5f * v;
-      const float o = lr * lr;
-      const int64_t idx = (int64_t)r * F + c;
-      if (hb16) ((uint16_t*)h)[idx] = f32_to_bf16(o);
-      else ((float*)h)[idx] = o;
-    }
-  }
-};
-
-struct EpiDown {
-  const float* xout;   // seq: x_out; par: attn term a
-  const float* mlp_scale;
-  float* out0;         // seq: slot output; par: lane0'
-  float* out1;         // par: lane1'
-  const float* lane0;  // par: lane0 after skip
-  const float* lane1;  // par: lane1 input
-  const float* pr;     // par: [2]
-  const float* pp;     // par: [2, 2]
-  int D, parallel;
-  NextIn next;  // inputs of the following slot (next.base == NULL: none)
-  template <class Cfg> struct Pre {
-    float xo[EW<Cfg>::EPT], sc[EW<Cfg>::EPT], l0[EW<Cfg>::EPT], l1[EW<Cfg>::EPT];
-    NextIn::El nx[EW<Cfg>::EPT];
-  };
-  template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int m0, int n0, int R, int) const {
-    Pre<Cfg> o;
-#pragma unroll
-    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
-      const int r = m0 + EW<Cfg>::row(j), c = n0 + EW<Cfg>::col(j);
-      const bool ok = r < R && c < D;
-      const int64_t idx = (int64_t)r * D + c;
-      o.xo[j] = ok ? xout[idx] : 0.f;
-      o.sc[j] = ok ? mlp_scale[c] : 0.f;
-      o.l0[j] = (ok && parallel) ? lane0[idx] : 0.f;
-      o.l1[j] = (ok && parallel) ? lane1[idx] : 0.f;
-      if (ok && next.base) o.nx[j] = next.load(idx, c, D);
-    }
-    return o;
-  }
-  template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
-#pragma unroll
-    for (int j = 0; j < EW<Cfg>::EPT; ++j) {
-      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
-      const int r = m0 + rr, c = n0 + cc;
-      if (r >= R || c >= D) continue;
-      const int64_t o = (int64_t)r * D + c;
-      const float m = pre.sc[j] * C[rr * Cfg::CS + cc];
-      float x;
-      if (!parallel) {
-        x = pre.xo[j] + m;
-        out0[o] = x;
-      } else {
-        const float a = pre.xo[j];
-        x = pr[0] * pre.l0[j] + pp[0] * a + pp[2] * m;
-        out0[o] = x;
-        out1[o] = pr[1] * pre.l1[j] + pp[1] * a + pp[3] * m;
-      }
-      if (next.base) next.put(o, x, pre.nx[j]);
-    }
-  }
-};
-
-// Softcapped logits, plus per (row, 64-column tile) softmax statistics
-// (tile max m and sum of exp(l - m)) for the row-parallel CDF kernel.
-struct EpiLogits {
-  float* logits;
-  float2* stats;  // [R][V/64] or NULL
-  int V, asym;
-  float cap;
-  const float* cap_pn;
-  template <class Cfg> struct Pre { float cp, cn, icp, icn; };
-  template <class Cfg>
-  __device__ Pre<Cfg> prefetch(int, int, int, int) const {
-    Pre<Cfg> o;
-    o.cp = asym ? cap_pn[0] : cap;
-    o.cn = asym ? cap_pn[1] : cap;
-    o.icp = 1.f / o.cp;
-    o.icn = 1.f / o.cn;
-    return o;
-  }
-  template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
-    static_assert(Cfg::NCOL == 64 && Cfg::THREADS == 256, "a wave holds one row of a 64-column tile");
-    constexpr int EPT = EW<Cfg>::EPT;
-    float v[EPT];
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
-      const int r = m0 + rr, c = n0 + cc;
-      v[j] = -INFINITY;
-      if (r < R && c < V) {
-        const float l = C[rr * Cfg::CS + cc];
-        const bool pos = l >= 0.f;
-        v[j] = (pos ? pre.cp : pre.cn) * tanh_fast(l * (pos ? pre.icp : pre.icn));
-        logits[(int64_t)r * V + c] = v[j];
-      }
-    }
-    if (stats) {  // wave w holds rows w + 4j of the tile, one column per lane
-      float m[EPT], e[EPT];
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) m[j] = wave_max(v[j]);
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) e[j] = v[j] == -INFINITY ? 0.f : __expf(v[j] - m[j]);
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) e[j] = wave_sum(e[j]);
-      if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-          const int r = m0 + EW<Cfg>::row(j);
-          if (r < R) stats[(int64_t)r * (V / 64) + n0 / 64] = make_float2(m[j], e[j]);
-        }
-      }
-    }
-  }
-};
-
-__global__ void commit_kernel(int32_t* pos, float* prev_raw, const float* cand_raw, int B, int D,
-                              int W) {
-  const int b = blockIdx.x;
-  for (int k = threadIdx.x; k < D; k += blockDim.x)
-    prev_raw[(int64_t)b * D + k] = cand_raw[(int64_t)b * D + k];
-  if (threadIdx.x == 0) pos[b] += W;
-}
-
 // ---- host side --------------------------------------------------------------
 
-struct WS {
-  float *X0, *X1, *XIN, *QIN, *XOUT, *Q, *GATE;  // XIN, QIN: [2][Rp][D] (slot parity)
-  void *Y, *HB;
-  float2* STATS;
-  int* SYNC;
-  int nsync;
-};
 
 int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
@@ -630,6 +44,10 @@ constexpr int kLmHeadColWgs = 0;
 // Preferred K-splits of the 4-wave GEMM stages (QKV and the LM head use
 // (NB, KS) = (4, 1): one 64-column head tile per task).
 constexpr int kKsO = 2, kKsUp = 2, kKsDown = 4;
+// Sync area layout (ints): ticket at 0, counters of (slot s, row tile m) at
+// kTicketPad + (s * nrt + m) * kCtrStride + stage.
+constexpr int kTicketPad = 64, kCtrStride = 16;
+static_assert(N_ST <= kCtrStride, "counter group too small");
 
 int64_t carve(const AltxsStepDesc* d, int nb, WS* w, char* base) {
   const int64_t R = (int64_t)nb * d->W, Rp = align_up(R, 16);
@@ -650,7 +68,9 @@ int64_t carve(const AltxsStepDesc* d, int nb, WS* w, char* base) {
   char* y = take(Rp * D * 4);
   char* hb = take(Rp * (int64_t)d->F * 4);
   char* stats = take(Rp * (int64_t)(d->V / 64 + 1) * 8);
-  const int nsync = (int)(Rp / 16);
+  // persistent-kernel counters: the ticket, then one 64-byte group of
+  // completion counters per (slot, row tile)
+  const int nsync = kTicketPad + (int)(n * (Rp / 16)) * kCtrStride;
   char* sync = take(nsync * 4);
   if (w) {
     w->X0 = (float*)x0; w->X1 = (float*)x1; w->XIN = (float*)xin; w->QIN = (float*)qin;
@@ -676,6 +96,7 @@ QT qt_of(const AltxsQTensor& t) {
   q.scales = (const uint16_t*)t.scales;
   q.N = (int)t.N;
   q.K = (int)t.K;
+  q.bits = t.bits;
   return q;
 }
 
@@ -950,6 +371,102 @@ struct StepRun {
   }
 };
 
+// ---- persistent layer kernel -------------------------------------------------
+
+bool persist_ok(const AltxsStepDesc* d) {
+  return d->kv_bf16 && 16 % d->W == 0 && !split_mode(d);
+}
+int64_t plan_slots_off() { return align_up((int64_t)sizeof(PersistArgs), 256); }
+int64_t plan_bytes_of(const AltxsStepDesc* d) {
+  return plan_slots_off() + (int64_t)d->n_slots * (int64_t)sizeof(SlotPlan);
+}
+
+// Field-by-field copies into the zeroed plan image: struct assignment would
+// also copy padding bytes, and the image is compared byte-wise.
+void put_qt(QT& q, const AltxsQTensor& t) {
+  q.codes = (const uint8_t*)t.codes;
+  q.scales = (const uint16_t*)t.scales;
+  q.N = (int)t.N;
+  q.K = (int)t.K;
+  q.bits = t.bits;
+}
+void put_ws(WS& o, const WS& w) {
+  o.X0 = w.X0; o.X1 = w.X1; o.XIN = w.XIN; o.QIN = w.QIN; o.XOUT = w.XOUT; o.Q = w.Q;
+  o.GATE = w.GATE; o.Y = w.Y; o.HB = w.HB; o.STATS = w.STATS; o.SYNC = w.SYNC; o.nsync = w.nsync;
+}
+
+// The plan image (host bytes) of the single-group step whose device copy is at dev.
+void fill_plan(const AltxsStepDesc* d, const Group& G, char* host, const char* dev) {
+  memset(host, 0, (size_t)plan_bytes_of(d));
+  PersistArgs& a = *(PersistArgs*)host;
+  SlotPlan* sp = (SlotPlan*)(host + plan_slots_off());
+  const int R = G.nb * d->W;
+  const int64_t Rp = align_up(R, 16), D = d->D;
+  a.plan = (const SlotPlan*)(dev + plan_slots_off());
+  a.n_slots = d->n_slots; a.R = R; a.W = d->W; a.D = d->D; a.H = d->H; a.Hkv = d->Hkv;
+  a.F = d->F; a.max_len = d->max_len; a.rd = d->rope_dims; a.gw = d->gate_window;
+  a.flags = d->flags & ALTXS_F_SPARSE_GATE;  // the only flag the layer tasks read
+  a.G = d->H / d->Hkv; a.eps = d->norm_eps; a.gate_scale = d->gate_scale;
+  a.nrt = (int)(Rp / 16);
+  const int ncol_o = 16 * (4 / pick_ks(d->D, kKsO)), ncol_d = 16 * (4 / pick_ks(d->F, kKsDown));
+  a.n_task[ST_QKV] = (d->D + 2 * d->Hkv * HD + 63) / 64;
+  a.n_task[ST_ATT] = 16 * d->Hkv;
+  a.n_task[ST_O] = (d->D + ncol_o - 1) / ncol_o;
+  a.n_task[ST_UP] = (d->F + ncol_o - 1) / ncol_o;
+  a.n_task[ST_DOWN] = (d->D + ncol_d - 1) / ncol_d;
+  a.per_unit = 0;
+  for (int st = 0; st < N_ST; ++st) a.per_unit += a.n_task[st];
+  a.ntasks = a.per_unit * a.n_slots * a.nrt;
+  a.pos = G.pos; a.kv = G.kv;
+  a.slot_kv_bytes = (int64_t)d->B * 2 * d->Hkv * d->max_len * HD * 2;
+  a.rope_cos = d->rope_cos; a.rope_sin = d->rope_sin;
+  put_ws(a.w, G.w);
+  a.ticket = G.w.SYNC;
+  a.done = G.w.SYNC + kTicketPad;
+  a.ctr_stride = kCtrStride;
+  a.err = d->err;
+  for (int s = 0; s < d->n_slots; ++s) {
+    const AltxsSlot& S = d->slots[s];
+    const AltxsLayer& L = d->layers[S.layer];
+    SlotPlan& P = sp[s];
+    put_qt(P.qkv, L.qkv); put_qt(P.o, L.o); put_qt(P.up, L.up); put_qt(P.down, L.down);
+    P.resid_mix = L.resid_mix; P.attn_scale = L.attn_scale; P.mlp_scale = L.mlp_scale;
+    P.q_gain = L.q_gain; P.gate_w = L.attn_gate_w; P.par_resid = L.par_resid;
+    P.par_post = L.par_post; P.ln_scale = L.ln_scale; P.use_xsa = L.use_xsa;
+    P.par = S.kind == ALTXS_SLOT_PAR ? 1 : 0;
+    P.first_parallel = S.first_parallel;
+    P.has_next = s + 1 < d->n_slots ? 1 : 0;
+    if (P.has_next) {
+      const AltxsSlot& S1 = d->slots[s + 1];
+      P.next_par = S1.kind == ALTXS_SLOT_PAR ? 1 : 0;
+      P.next_skip_src = S1.skip_src;
+      P.next_skip_self = S1.skip_src == s ? 1 : 0;
+      P.next_mix = d->layers[S1.layer].resid_mix;
+      P.next_skip_w = S1.skip_src >= 0 ? d->skip_weights + (int64_t)S1.skip_idx * D : nullptr;
+      P.next_skip_g = (S1.skip_src >= 0 && (d->flags & ALTXS_F_SKIP_GATES) && d->skip_gates)
+                          ? d->skip_gates + (int64_t)S1.skip_idx * D : nullptr;
+    } else {
+      P.next_skip_src = -1;
+    }
+  }
+}
+
+// embed -> one persistent launch for every slot -> head.
+template <int AM>
+hipError_t run_persist(const AltxsStepDesc* d, const Group& G, hipStream_t st) {
+  StepRun<AM> run{d};
+  hipError_t e;
+  hipEvent_t* ev = (hipEvent_t*)d->attn_events;
+  const PersistArgs& a = *(const PersistArgs*)d->plan_host;
+  if ((e = run.embed(G, st)) != hipSuccess) return e;
+  if (ev && (e = hipEventRecord(ev[0], st)) != hipSuccess) return e;
+  if ((e = launch_persist(a, (const PersistArgs*)d->plan_dev, AM == A_BF16 ? 1 : 0,
+                          pick_ks(d->D, kKsO), pick_ks(d->F, kKsDown), 0, st)) != hipSuccess)
+    return e;
+  if (ev && (e = hipEventRecord(ev[1], st)) != hipSuccess) return e;
+  return run.head(G, st);
+}
+
 // One group on one stream.
 template <int AM>
 hipError_t run_single(const AltxsStepDesc* d, const Group& G, hipStream_t st) {
@@ -1009,11 +526,49 @@ extern "C" int64_t altxs_step_workspace_bytes(const AltxsStepDesc* d) {
   return ws_bytes_needed(d);
 }
 
+extern "C" int64_t altxs_step_plan_bytes(const AltxsStepDesc* d) {
+  if (!d || d->n_slots < 1 || d->n_slots > ALTXS_MAX_SLOTS) return -1;
+  return plan_bytes_of(d);
+}
+
+extern "C" int32_t altxs_step_plan_build(const AltxsStepDesc* d, void* plan_host, void* plan_dev,
+                                         int64_t bytes, altxs_stream_t stream) {
+  int rc = validate(d);
+  if (rc) return rc;
+  ALTXS_REQUIRE(plan_host && plan_dev, "altxs_step_plan_build: null plan buffer");
+  ALTXS_REQUIRE(bytes >= plan_bytes_of(d), "altxs_step_plan_build: %lld bytes < %lld",
+                (long long)bytes, (long long)plan_bytes_of(d));
+  ALTXS_REQUIRE(persist_ok(d),
+                "altxs_step_plan_build: the persistent kernel needs a bf16 KV cache, W dividing 16 "
+                "and one stream");
+  const Group G = make_group(d, 0, d->B, (char*)d->ws);
+  fill_plan(d, G, (char*)plan_host, (const char*)plan_dev);
+  hipStream_t st = (hipStream_t)stream;
+  ALTXS_CHECK_HIP(hipMemcpyAsync(plan_dev, plan_host, (size_t)plan_bytes_of(d), hipMemcpyHostToDevice, st));
+  ALTXS_CHECK_HIP(hipStreamSynchronize(st));
+  return ALTXS_OK;
+}
+
 extern "C" int32_t altxs_step(const AltxsStepDesc* d, altxs_stream_t stream) {
   int rc = validate(d);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
+  if (d->plan_dev) {
+    ALTXS_REQUIRE(d->plan_host && d->plan_bytes >= plan_bytes_of(d),
+                  "altxs_step: plan_dev needs plan_host and plan_bytes");
+    ALTXS_REQUIRE(persist_ok(d),
+                  "altxs_step: the persistent kernel needs a bf16 KV cache, W dividing 16 and one stream");
+    const Group G = make_group(d, 0, d->B, (char*)d->ws);
+    static thread_local std::vector<char> img;
+    img.resize((size_t)plan_bytes_of(d));
+    fill_plan(d, G, img.data(), (const char*)d->plan_dev);
+    ALTXS_REQUIRE(memcmp(img.data(), d->plan_host, img.size()) == 0,
+                  "altxs_step: the plan was built for other pointers or shapes; rebuild it");
+    e = d->act_bf16 ? run_persist<A_BF16>(d, G, st) : run_persist<A_F32>(d, G, st);
+    ALTXS_CHECK_HIP(e);
+    return ALTXS_OK;
+  }
   if (split_mode(d)) {
     const int nb0 = (d->B + 1) / 2;
     Group G[2] = {make_group(d, 0, nb0, (char*)d->ws),

@@ -70,7 +70,8 @@ class StaticState:
     """Caller-owned device buffers of a B x W step (addresses stay fixed)."""
 
     def __init__(self, model: "StepModel", batch: int, win: int, max_len: int,
-                 want_probs: bool = True, want_cdf: bool = True, split: bool = False):
+                 want_probs: bool = True, want_cdf: bool = True, split: bool = False,
+                 persistent: bool = False):
         cfg, dev = model.cfg, model.device
         if max_len % CHUNK:
             raise ValueError(f"max_len must be a multiple of {CHUNK}")
@@ -99,6 +100,22 @@ class StaticState:
         nbytes = _lib.load().altxs_step_workspace_bytes(ctypes.byref(desc))
         self.ws = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
         self._descs.clear()
+        # persistent layer kernel: plan built once for these buffers (device copy + host image)
+        self.persistent = False  # set once the plan exists (the descriptor then points at it)
+        if persistent:
+            L = _lib.load()
+            desc = self._desc(0)
+            nb = int(L.altxs_step_plan_bytes(ctypes.byref(desc)))
+            if nb <= 0:
+                raise RuntimeError("altxs_step_plan_bytes failed")
+            self.plan_dev = torch.empty(nb, dtype=torch.uint8, device=dev)
+            self.plan_host = (ctypes.c_uint8 * nb)()
+            rc = L.altxs_step_plan_build(ctypes.byref(desc), ctypes.cast(self.plan_host, ctypes.c_void_p),
+                                         ctypes.c_void_p(self.plan_dev.data_ptr()), nb,
+                                         ctypes.c_void_p(_stream_ptr(dev)))
+            _lib.check(rc, "altxs_step_plan_build")
+            self.persistent = True
+            self._descs.clear()
 
     def kv_slot(self, slot: int) -> torch.Tensor:
         """[B, 2, Hkv, max_len, hd] view of one slot's cache."""
@@ -120,7 +137,7 @@ class StaticState:
         e = int(self.err.item())
         if e:
             raise RuntimeError(f"altxs device error flags 0x{e:x} (1 = position >= max_len, "
-                               "2 = token id out of range)")
+                               "2 = token id out of range, 4 = a persistent-kernel wait gave up)")
 
 
 class StepModel:
@@ -171,9 +188,10 @@ class StepModel:
 
     def make_static_state(self, max_len: int, device=None, win: int = 1, batch: int = 1,
                           want_probs: bool = True, want_cdf: bool = True,
-                          split: bool = False) -> StaticState:
-        """``split``: run the segments as two groups on two streams (B >= 2)."""
-        return StaticState(self, batch, win, max_len, want_probs, want_cdf, split)
+                          split: bool = False, persistent: bool = False) -> StaticState:
+        """``split``: run the segments as two groups on two streams (B >= 2).
+        ``persistent``: run every slot in one persistent launch (bf16 KV, W | 16)."""
+        return StaticState(self, batch, win, max_len, want_probs, want_cdf, split, persistent)
 
     def _fill_desc(self, st: StaticState, flags: int) -> _lib.StepDesc:
         cfg = self.cfg
@@ -246,6 +264,10 @@ class StepModel:
         if getattr(st, "split", False):
             d.aux_stream = int(st.aux_stream.cuda_stream)
             d.sync_events = st.sync_events.ptr
+        if getattr(st, "persistent", False):
+            d.plan_dev = st.plan_dev.data_ptr()
+            d.plan_host = ctypes.cast(st.plan_host, ctypes.c_void_p)
+            d.plan_bytes = st.plan_dev.numel()
         return d
 
     # ---- the step -------------------------------------------------------------
@@ -254,7 +276,8 @@ class StepModel:
         """Enqueue one step on the current stream.
 
         ``attn_events``: optional address of 2*n_slots hipEvent_t handles,
-        recorded around each slot's attention launch (timing hook).
+        recorded around each slot's attention launch (timing hook); with a
+        persistent state, events 0 and 1 bracket the layer kernel.
         """
         flags = (_lib.F_COMMIT if commit else 0) | (_lib.F_RENORM if renorm else 0)
         d = st._desc(flags)

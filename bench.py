@@ -97,6 +97,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--streams", type=int, default=1, choices=[1, 2],
                     help="2: two segment groups on two streams, attention launches alternating")
+    ap.add_argument("--persistent", action="store_true",
+                    help="run every slot in one persistent launch (tasks in dependency order)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
@@ -122,7 +124,7 @@ def main() -> int:
     log(f"model {a.profile}: {sm.bits_summary()['bpw']:.4f} bpw, built in {time.time() - t0:.1f}s")
     model = StepModel(sm, act=a.act, kv=a.kv)
     st = model.make_static_state(max_len, win=1, batch=B, want_probs=False, want_cdf=True,
-                                 split=a.streams == 2)
+                                 split=a.streams == 2, persistent=a.persistent)
     groups = 2 if st.split else 1
     g = torch.Generator(device="cuda").manual_seed(0)
     st.kv.normal_(generator=g)
@@ -176,18 +178,27 @@ def main() -> int:
     s1.record()
     torch.cuda.synchronize()
     eager_ms = s0.elapsed_time(s1) / a.steps
-    durs = [ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(n_slots * groups * a.steps)]
-    ev.close()
-    attn_ms = float(np.mean(durs))
     kvb = 2 if a.kv == "bf16" else 4
     ab = synth.algorithmic_step_bytes(sm, B, ctx, kv_bytes=kvb)
     ybytes = 2 if a.act == "bf16" else 4
-    # algorithmic bytes of one attention launch (one slot, one group: B/groups segments)
-    attn_bytes = (ab["kv_read"] // ab["n_slots"] + B * cfg.num_heads * cfg.head_dim * (4 + ybytes)
-                  + B * cfg.num_heads * 4) / groups
+    if a.persistent:
+        # one layer-kernel launch per step (events 0/1 of each step's block)
+        durs = [ev.elapsed_ms(k * per_step, k * per_step + 1) for k in range(a.steps)]
+        layer_w = sum(p.nbytes_codes + p.nbytes_scales for n, p in sm.packed.items() if n != "emb")
+        # algorithmic bytes of the launch: every slot's KV read + append, layer weights
+        attn_bytes = ab["kv_read"] + ab["kv_write"] + layer_w
+        kname = "layers_kernel (persistent: every slot's QKV, attention, O, MLP)"
+    else:
+        durs = [ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(n_slots * groups * a.steps)]
+        # algorithmic bytes of one attention launch (one slot, one group: B/groups segments)
+        attn_bytes = (ab["kv_read"] // ab["n_slots"] + B * cfg.num_heads * cfg.head_dim * (4 + ybytes)
+                      + B * cfg.num_heads * 4) / groups
+        kname = "attn_mfma_kernel (decode attention)"
+    ev.close()
+    attn_ms = float(np.mean(durs))
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
     step_gbs = ab["total"] / (ms * 1e-3) / 1e9
-    log(f"attention: {attn_ms * 1e3:.1f} us/launch, {achieved:.0f} GB/s; eager step {eager_ms:.3f} ms; "
+    log(f"{kname.split(' ')[0]}: {attn_ms * 1e3:.1f} us/launch, {achieved:.0f} GB/s; eager step {eager_ms:.3f} ms; "
         f"step {step_gbs:.0f} GB/s of algorithmic traffic")
 
     cpu = None
@@ -217,17 +228,17 @@ def main() -> int:
                          f"{sm.bits_summary()['bpw']:.3f} bpw group-64 weights, "
                          f"{a.act} activations, {a.kv} KV"),
             "segments": B, "ctx": ctx, "timing": "hip-graph" if graph is not None else "eager",
-            "streams": groups,
+            "streams": groups, "persistent": bool(a.persistent),
             "eager_ms_per_step": round(eager_ms, 4),
         },
         "roofline": {
-            "kernel": "attn_mfma_kernel (decode attention)",
+            "kernel": kname,
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic("attn"),
+            "traffic": read_traffic("layers" if a.persistent else "attn"),
             "bytes_per_launch": int(attn_bytes),
             "us_per_launch": round(attn_ms * 1e3, 2),
         },

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define ALTXS_ABI_VERSION 3
+#define ALTXS_ABI_VERSION 4
 
 enum {
   ALTXS_OK = 0,
@@ -246,10 +246,36 @@ typedef struct AltxsStepDesc {
    * bit-identical to the single-stream step.  NULL = one stream. */
   void *aux_stream;
   void **sync_events;
+  /* Persistent layer kernel (single stream, bf16 KV, W dividing 16): a plan
+   * built once by altxs_step_plan_build() for this descriptor's pointers and
+   * shapes -- plan_dev on the device, plan_host its host image, both
+   * altxs_step_plan_bytes() long.  Every slot of the step then runs in ONE
+   * launch: workgroups take tasks (a GEMM column tile or an attention
+   * (row, kv-head) pair of one 16-row tile) in dependency order, so one row
+   * tile's projections and MLP run while other tiles' attention streams the
+   * KV cache.  Bit-identical to the per-stage launches.  In this mode
+   * attn_events 0 and 1 bracket the layer kernel.  NULL = per-stage launches. */
+  void *plan_dev;
+  const void *plan_host;
+  int64_t plan_bytes;
 } AltxsStepDesc;
 
 /* Workspace bytes altxs_step needs for this descriptor (host-only). */
 int64_t altxs_step_workspace_bytes(const AltxsStepDesc *d);
+
+/* Bytes of the persistent-kernel plan for this descriptor (host-only; <0 on error). */
+int64_t altxs_step_plan_bytes(const AltxsStepDesc *d);
+
+/*
+ * Build the persistent-kernel plan for d (its plan fields are ignored): the
+ * per-slot weight pointers, parameters and workspace layout, written to
+ * plan_host and copied to plan_dev on `stream` (the call waits for the copy).
+ * A step whose descriptor no longer matches the plan fails with ALTXS_ERR_ARG.
+ * The reference keeps the same stacked per-layer tables for its persistent
+ * decode kernel (src/xsa_ttt/persistent_step.py:452-588).
+ */
+int32_t altxs_step_plan_build(const AltxsStepDesc *d, void *plan_host, void *plan_dev,
+                              int64_t bytes, altxs_stream_t stream);
 
 /*
  * One W-token step for B independent segments: embedding (+smear), every slot
