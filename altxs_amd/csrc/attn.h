@@ -97,7 +97,10 @@ __device__ __forceinline__ void split_parts(const float (&x)[8], bf16x8 (&out)[N
 }
 
 // One (query row r, kv head g) of the bf16-cache attention: ATT_WAVES waves.
-template <int G, int NP, int YBF16>
+// PF = 1: each wave keeps its next tile's loads in flight while it computes the
+// current one (two register buffers), for launches with one workgroup per CU;
+// the arithmetic, and so the result, is the same for PF = 0 and 1.
+template <int G, int NP, int YBF16, int PF = 0>
 __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, MergeLds<G>& sm) {
   static_assert(TILE == 64, "the MFMA tiling below assumes 64-key tiles");
   const int b = r / a.W, t = r % a.W;
@@ -129,14 +132,15 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int T = wave; T < ntiles; T += ATT_WAVES) {
+  auto load = [&](u32x4 (&kr)[8], u32x4 (&vr)[8], int T) {
     const u32x4* kt = (const u32x4*)(kb + (int64_t)T * (TILE * HD)) + lane;
     const u32x4* vt = (const u32x4*)(vb + (int64_t)T * (TILE * HD)) + lane;
-    u32x4 kr[8], vr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) kr[i] = __builtin_nontemporal_load(kt + 64 * i);
 #pragma unroll
     for (int i = 0; i < 8; ++i) vr[i] = __builtin_nontemporal_load(vt + 64 * i);
+  };
+  auto process = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8], int T) {
     // scores: S[blk] row 4*lg + i = key 16*blk + 4*lg + i, column col
     f32x4 S[4];
 #pragma unroll
@@ -198,6 +202,26 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
         for (int k = 0; k < NP; ++k)
           acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[k], vop, acc[nb], 0, 0, 0);
       }
+    }
+  };
+
+  if constexpr (PF == 0) {
+    for (int T = wave; T < ntiles; T += ATT_WAVES) {
+      u32x4 kr[8], vr[8];
+      load(kr, vr, T);
+      process(kr, vr, T);
+    }
+  } else {
+    // two buffers: A holds tiles wave + 2j*W, B tiles wave + (2j+1)*W
+    u32x4 ka[8], va[8], kb2[8], vb2[8];
+    int T = wave;
+    if (T < ntiles) load(ka, va, T);
+    for (; T < ntiles; T += 2 * ATT_WAVES) {
+      const int T1 = T + ATT_WAVES, T2 = T + 2 * ATT_WAVES;
+      if (T1 < ntiles) load(kb2, vb2, T1);
+      process(ka, va, T);
+      if (T2 < ntiles) load(ka, va, T2);
+      if (T1 < ntiles) process(kb2, vb2, T1);
     }
   }
   // l: this lane's keys only; add the four lane groups (fixed butterfly).

@@ -39,24 +39,30 @@ struct PersistArgs {
   float eps, gate_scale;
   int nrt;               // 16-row tiles
   int n_task[N_ST];      // tasks of each stage per (slot, row tile)
-  int per_unit, ntasks;  // per (slot, row tile); total
   const int32_t* pos;
   char* kv;              // slot 0 of the group's first segment
   int64_t slot_kv_bytes;
   const float *rope_cos, *rope_sin;
   WS w;
-  int* ticket;
   int* done;             // completed tasks of (slot s, row tile m, stage st) at
                          // done[(s * nrt + m) * ctr_stride + st]
   int ctr_stride;
   int32_t* err;
+  // Roles: the first ng workgroups to start take GEMM tasks from one queue,
+  // the others attention tasks from a second queue.
+  // GEMM queue: blocks b = s' * nrt + m of gblock tickets holding O, UP, DOWN
+  // of (s' - 1, m) then QKV of (s', m), for s' = 0 .. n_slots (entries of
+  // slots outside [0, n_slots) are skipped).  Attention queue: (slot, row
+  // tile)-major, 16 * Hkv tasks each.
+  int ng, gblock, n_gtask, n_atask;
+  int *role_ctr, *gticket, *aticket;
 };
 
 // Launch the persistent layer kernel on the arguments at dev_args (a device
 // copy of `a`, which the host side reads for the launch shape): act_bf16
 // selects the A operand mode, ks_o the K-split of the out-projection and
 // MLP-up GEMMs (K = D), ks_d that of MLP-down (K = F).  grid <= 0: as many
-// workgroups as can be resident.
+// workgroups as can be resident (all of them must be; more than ng).
 hipError_t launch_persist(const PersistArgs& a, const PersistArgs* dev_args, int act_bf16, int ks_o,
                           int ks_d, int grid, hipStream_t s);
 

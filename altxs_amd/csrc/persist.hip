@@ -1,18 +1,16 @@
 // Persistent layer kernel: every slot of the step for every 16-row tile of a
 // segment group in one launch.
 //
-// Work items ("tasks") are numbered in a topological order: for each slot s and
-// row tile m, the QKV column tiles, the attention (row, kv head) pairs, then the
-// O, UP and DOWN column tiles.  A workgroup takes the next number from an
-// atomic ticket, waits (bounded spin) until the stage it reads from is complete
-// for its row tile, runs the task with the same device code the per-stage
-// kernels use, publishes its stores (release fence) and bumps the completion
-// counter of (s, m, stage).  Dependencies always point to smaller numbers and
-// numbers are taken in increasing order by running workgroups, so the smallest
-// unfinished task can always run: there is no deadlock whatever the residency.
-// Row tiles progress independently, so one tile's projections and MLP run while
-// other tiles' attention streams the KV cache -- the launch gaps and pipeline
-// bubbles of 5 kernels per slot are gone, and no GEMM work is duplicated.
+// Work items ("tasks"): for each slot s and 16-row tile m, the QKV column
+// tiles, the attention (row, kv head) pairs, then the O, UP and DOWN column
+// tiles.  One workgroup per CU; the first `ng` workgroups to start are GEMM
+// workers and take QKV/O/UP/DOWN tasks from one queue, the others stream
+// attention tasks from a second queue.  A task waits (bounded spin) until the
+// stage it reads is complete for its row tile, runs the same device code as the
+// per-stage kernels, publishes its stores (one agent-scope release per
+// workgroup) and bumps the completion counter of (s, m, stage).  Row tiles
+// progress independently, so one tile's projections and MLP run while other
+// tiles' attention streams the KV cache.
 //
 // Results are bit-identical to the per-stage kernels: each task is the same
 // tile computation, and every reduction order depends only on the tile shape.
@@ -27,10 +25,27 @@ using namespace altxs_sk;
 namespace {
 
 constexpr int kThreads = 256;
+
+// Tuning switches (compile time).  MINW: waves per SIMD the register budget
+// is sized for (1: the full register file, one workgroup per CU, no spills).
+// ATT_PF: attention tasks keep the next tile's loads in flight.
+#ifndef ALTXS_PERSIST_MINW
+#define ALTXS_PERSIST_MINW 1
+#endif
+#ifndef ALTXS_PERSIST_ATT_PF
+#define ALTXS_PERSIST_ATT_PF 1
+#endif
 // A wait gives up after ~1 s of the 100 MHz wall clock (a step takes about a
 // millisecond) and flags ALTXS_EDEV_SPIN; every other wait then sees the flag
 // and returns at once, so the grid drains quickly with invalid results.
 constexpr uint64_t kSpinTicks = 100000000ull;
+
+#ifdef ALTXS_PERSIST_PROF
+// Experiment hook (not part of the library build): per ticket the wall clock at
+// task start, at the end of its dependency wait, at its end, and the stage.
+__device__ uint64_t g_prof[1 << 17];
+__shared__ uint64_t s_prof_wait;
+#endif
 
 // Wait until *ctr >= target (thread 0 polls), then make the producers' stores
 // visible to every thread of the workgroup.
@@ -48,9 +63,12 @@ __device__ __forceinline__ void wait_ctr(const int* ctr, int target, int32_t* er
         }
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the barrier extends it to every wave
+#ifdef ALTXS_PERSIST_PROF
+    s_prof_wait = (uint64_t)wall_clock64();
+#endif
   }
   __syncthreads();
-  __threadfence();
 }
 
 struct CtrWait {
@@ -129,7 +147,8 @@ struct Tasks {
     p.gate = (a.flags & ALTXS_F_SPARSE_GATE) ? a.w.GATE : nullptr;
     p.use_xsa = uni(P.use_xsa); p.y = a.w.Y; p.err = a.err;
     constexpr int NP = AM == A_BF16 ? 1 : 3;
-    altxs_attn::attn_mfma_task<G, NP, AM == A_BF16 ? 1 : 0>(p, r, g, *(MergeLds<G>*)smem);
+    altxs_attn::attn_mfma_task<G, NP, AM == A_BF16 ? 1 : 0, ALTXS_PERSIST_ATT_PF>(
+        p, r, g, *(MergeLds<G>*)smem);
   }
 
   __device__ __forceinline__ void attn(int s, int m, int k) const {
@@ -198,43 +217,78 @@ struct Tasks {
   }
 };
 
+// Role-split schedule: GEMM workers and attention streamers (see PersistArgs).
+// Each queue is consumed in an order consistent with one topological order of
+// all tasks, so the smallest unfinished task always has a running worker of
+// its role or is next in its queue: no deadlock while both roles have a
+// resident workgroup (grid <= resident capacity; waits are bounded anyway).
 template <int AM, int G, int KSO, int KSD>
-__global__ __launch_bounds__(kThreads, 2) void layers_kernel(const PersistArgs* __restrict__ pa) {
+__global__ __launch_bounds__(kThreads, ALTXS_PERSIST_MINW) void roles_kernel(const PersistArgs* __restrict__ pa) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int s_task;
-  const PersistArgs& a = *pa;  // in device memory: fields are scalar loads, nothing spills
+  const PersistArgs& a = *pa;
   const Tasks<AM, G> T{a, smem};
-  // Thread 0 takes tickets; the ticket is read back with readfirstlane so that
-  // it, and everything derived from it (slot, stage, column tile), is a scalar
-  // and every loop and branch below that contains a barrier is uniform.  The
-  // loop has exactly one thread-0 region (publish + next ticket): two such
-  // regions around the back edge get merged by the compiler into a lane-split
-  // loop in which lanes other than thread 0 re-enter the body with the old
-  // ticket while lane 0 waits for them, which never ends.
-  if (threadIdx.x == 0) s_task = atomicAdd(a.ticket, 1);
+  if (threadIdx.x == 0) s_task = atomicAdd(a.role_ctr, 1);
+  __syncthreads();
+  const bool gemm = __builtin_amdgcn_readfirstlane(s_task) < a.ng;
+  __syncthreads();
+  int* const q = gemm ? a.gticket : a.aticket;
+  const int nq = gemm ? a.n_gtask : a.n_atask;
+  if (threadIdx.x == 0) s_task = atomicAdd(q, 1);
   __syncthreads();
   int t = __builtin_amdgcn_readfirstlane(s_task);
-  while (t < a.ntasks) {
-    const int u = t / a.per_unit;
-    int k = t - u * a.per_unit;
-    const int s = u / a.nrt, m = u - s * a.nrt;
-    int st = 0;
-    while (st < N_ST - 1 && k >= a.n_task[st]) {
-      k -= a.n_task[st];
-      ++st;
+  const int nO = a.n_task[ST_O], nU = a.n_task[ST_UP], nD = a.n_task[ST_DOWN];
+  while (t < nq) {
+    int s, m, st, k;
+    bool valid = true;
+    if (gemm) {
+      const int b = t / a.gblock;
+      k = t - b * a.gblock;
+      const int sp = b / a.nrt;
+      m = b - sp * a.nrt;
+      if (k < nO) { st = ST_O; s = sp - 1; }
+      else if (k < nO + nU) { st = ST_UP; s = sp - 1; k -= nO; }
+      else if (k < nO + nU + nD) { st = ST_DOWN; s = sp - 1; k -= nO + nU; }
+      else { st = ST_QKV; s = sp; k -= nO + nU + nD; }
+      valid = st == ST_QKV ? s < a.n_slots : s >= 0;
+    } else {
+      const int u = t / a.n_task[ST_ATT];
+      k = t - u * a.n_task[ST_ATT];
+      s = u / a.nrt;
+      m = u - s * a.nrt;
+      st = ST_ATT;
     }
-    switch (st) {
-      case ST_QKV: T.qkv(s, m, k); break;
-      case ST_ATT: T.attn(s, m, k); break;
-      case ST_O: T.template o<KSO>(s, m, k); break;
-      case ST_UP: T.template up<KSO>(s, m, k); break;
-      default: T.template down<KSD>(s, m, k); break;
+#ifdef ALTXS_PERSIST_PROF
+    uint64_t prof_t0 = 0;
+    if (threadIdx.x == 0) prof_t0 = s_prof_wait = (uint64_t)wall_clock64();
+#endif
+    if (valid) {
+      switch (st) {
+        case ST_QKV: T.qkv(s, m, k); break;
+        case ST_ATT: T.attn(s, m, k); break;
+        case ST_O: T.template o<KSO>(s, m, k); break;
+        case ST_UP: T.template up<KSO>(s, m, k); break;
+        default: T.template down<KSD>(s, m, k); break;
+      }
     }
-    __threadfence();  // publish this task's stores before counting it
-    __syncthreads();  // every wave is done with the task (and with s_task)
+    __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's stores reached L2
+    __syncthreads();
     if (threadIdx.x == 0) {
-      atomicAdd(a.done + (int64_t)u * a.ctr_stride + st, 1);
-      s_task = atomicAdd(a.ticket, 1);
+#ifdef ALTXS_PERSIST_PROF
+      const int slot = gemm ? t : a.n_gtask + t;
+      if (valid && slot < (1 << 15)) {
+        g_prof[4 * slot] = prof_t0;
+        g_prof[4 * slot + 1] = s_prof_wait;
+        g_prof[4 * slot + 2] = (uint64_t)wall_clock64();
+        g_prof[4 * slot + 3] = (uint64_t)st | ((uint64_t)s << 8) | ((uint64_t)m << 16) |
+                               ((uint64_t)blockIdx.x << 24);
+      }
+#endif
+      if (valid) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        atomicAdd(a.done + ((int64_t)s * a.nrt + m) * a.ctr_stride + st, 1);
+      }
+      s_task = atomicAdd(q, 1);
     }
     __syncthreads();
     t = __builtin_amdgcn_readfirstlane(s_task);
@@ -253,7 +307,7 @@ size_t lds_bytes(const PersistArgs& a) {
 
 template <int AM, int G, int KSO, int KSD>
 hipError_t launch_t(const PersistArgs& a, const PersistArgs* dev_args, int grid, hipStream_t s) {
-  auto kfn = layers_kernel<AM, G, KSO, KSD>;
+  auto kfn = roles_kernel<AM, G, KSO, KSD>;
   const size_t lds = lds_bytes<AM, G, KSO, KSD>(a);
   static int resident = 0;  // workgroups that fit on the device at once (per instantiation)
   static size_t configured = 0;
@@ -274,9 +328,10 @@ hipError_t launch_t(const PersistArgs& a, const PersistArgs* dev_args, int grid,
       return e;
     resident = (per_cu > 0 ? per_cu : 1) * cus;
   }
+  // every workgroup resident at once, and at least one of each role
   int g = grid > 0 ? grid : resident;
-  if (g > a.ntasks) g = a.ntasks;
-  if (g < 1) g = 1;
+  if (g > resident) g = resident;
+  if (g <= a.ng || a.ng < 1) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL(kfn, dim3(g), dim3(kThreads), lds, s, dev_args);
   return hipGetLastError();
 }
@@ -307,3 +362,9 @@ hipError_t launch_persist(const PersistArgs& a, const PersistArgs* dev_args, int
 }
 
 }  // namespace altxs_sk
+
+#ifdef ALTXS_PERSIST_PROF
+extern "C" int altxs_prof_read(void* dst, int64_t n_u64) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_prof), (size_t)n_u64 * 8, 0, hipMemcpyDeviceToHost);
+}
+#endif

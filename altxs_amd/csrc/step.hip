@@ -20,6 +20,7 @@
 // 1293-1355, _apply_decoder_skip 1275-1291, _embed_tokens_window 1559-1579,
 // _project_logits/_apply_asym_softcap 1463-1500, _static_extend_body
 // 1649-1781.
+#include <stdlib.h>
 #include <string.h>
 
 #include <vector>
@@ -44,9 +45,21 @@ constexpr int kLmHeadColWgs = 0;
 // Preferred K-splits of the 4-wave GEMM stages (QKV and the LM head use
 // (NB, KS) = (4, 1): one 64-column head tile per task).
 constexpr int kKsO = 2, kKsUp = 2, kKsDown = 4;
-// Sync area layout (ints): ticket at 0, counters of (slot s, row tile m) at
-// kTicketPad + (s * nrt + m) * kCtrStride + stage.
+// Sync area layout (ints): persistent-kernel role counter at 0, GEMM-queue
+// and attention-queue tickets at 16 and 32 (one 64-byte line each), counters
+// of (slot s, row tile m) at kTicketPad + (s * nrt + m) * kCtrStride + stage.
 constexpr int kTicketPad = 64, kCtrStride = 16;
+// Persistent kernel: workgroups that run the GEMM chain; the rest stream
+// attention (ALTXS_PERSIST_NG overrides, for tuning).
+int persist_gemm_workers() {
+  static int ng = -1;
+  if (ng < 0) {
+    const char* e = getenv("ALTXS_PERSIST_NG");
+    ng = e ? atoi(e) : 96;
+    if (ng < 1) ng = 1;
+  }
+  return ng;
+}
 static_assert(N_ST <= kCtrStride, "counter group too small");
 
 int64_t carve(const AltxsStepDesc* d, int nb, WS* w, char* base) {
@@ -68,8 +81,8 @@ int64_t carve(const AltxsStepDesc* d, int nb, WS* w, char* base) {
   char* y = take(Rp * D * 4);
   char* hb = take(Rp * (int64_t)d->F * 4);
   char* stats = take(Rp * (int64_t)(d->V / 64 + 1) * 8);
-  // persistent-kernel counters: the ticket, then one 64-byte group of
-  // completion counters per (slot, row tile)
+  // persistent-kernel counters: role counter and queue tickets, then one
+  // 64-byte group of completion counters per (slot, row tile)
   const int nsync = kTicketPad + (int)(n * (Rp / 16)) * kCtrStride;
   char* sync = take(nsync * 4);
   if (w) {
@@ -414,17 +427,20 @@ void fill_plan(const AltxsStepDesc* d, const Group& G, char* host, const char* d
   a.n_task[ST_O] = (d->D + ncol_o - 1) / ncol_o;
   a.n_task[ST_UP] = (d->F + ncol_o - 1) / ncol_o;
   a.n_task[ST_DOWN] = (d->D + ncol_d - 1) / ncol_d;
-  a.per_unit = 0;
-  for (int st = 0; st < N_ST; ++st) a.per_unit += a.n_task[st];
-  a.ntasks = a.per_unit * a.n_slots * a.nrt;
   a.pos = G.pos; a.kv = G.kv;
   a.slot_kv_bytes = (int64_t)d->B * 2 * d->Hkv * d->max_len * HD * 2;
   a.rope_cos = d->rope_cos; a.rope_sin = d->rope_sin;
   put_ws(a.w, G.w);
-  a.ticket = G.w.SYNC;
   a.done = G.w.SYNC + kTicketPad;
   a.ctr_stride = kCtrStride;
   a.err = d->err;
+  a.ng = persist_gemm_workers();
+  a.gblock = a.n_task[ST_O] + a.n_task[ST_UP] + a.n_task[ST_DOWN] + a.n_task[ST_QKV];
+  a.n_gtask = a.gblock * (a.n_slots + 1) * a.nrt;
+  a.n_atask = a.n_task[ST_ATT] * a.n_slots * a.nrt;
+  a.role_ctr = G.w.SYNC;
+  a.gticket = G.w.SYNC + 16;
+  a.aticket = G.w.SYNC + 32;
   for (int s = 0; s < d->n_slots; ++s) {
     const AltxsSlot& S = d->slots[s];
     const AltxsLayer& L = d->layers[S.layer];

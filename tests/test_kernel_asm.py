@@ -40,4 +40,4 @@ def test_no_divergent_loop_around_barriers(src, tmp_path):
     bad = {k: v for k, v in rep.items() if v}
     assert not bad, f"divergent loops holding barriers: {bad}"
     if src == "persist.hip":
-        assert sum("layers_kernel" in k for k in rep) == 36  # every (act, G, KS_o, KS_d) variant
+        assert sum("roles_kernel" in k for k in rep) == 36  # every (act, G, KS_o, KS_d) variant
