@@ -30,12 +30,16 @@
 
 using namespace altxs_attn;
 
+#ifndef ALTXS_ATT_PF
+#define ALTXS_ATT_PF 0  // 1: each wave keeps its next tile's loads in flight
+#endif
+
 namespace {
 
 template <int G, int NP, int YBF16>
 __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
-  attn_mfma_task<G, NP, YBF16>(a, blockIdx.x / a.Hkv, blockIdx.x % a.Hkv, sm);
+  attn_mfma_task<G, NP, YBF16, ALTXS_ATT_PF>(a, blockIdx.x / a.Hkv, blockIdx.x % a.Hkv, sm);
 }
 
 // ---------------------------------------------------------------------------

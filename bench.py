@@ -15,8 +15,13 @@ bytes.  Weights are seeded N(0, 0.02^2) then quantised; tokens are Zipf(1.1).
 
 The line also carries:
 * ``roofline``: the decode-attention kernel (the dominant one), algorithmic
-  bytes per launch / its mean launch duration, timed with HIP events recorded
-  on the step's stream around every attention launch of the timed steps;
+  bytes per launch / its mean launch duration, timed with HIP events on the
+  step's stream around 20 back-to-back launches over slot 0's cache (the same
+  kernel and launch shape as in the step); ``us_per_launch_in_step`` is the
+  mean of events recorded around every attention launch inside the timed
+  steps, which also includes each launch's gap after the preceding kernel;
+  ``traffic`` comes from profiles/traffic_attn.txt (rocprofv3 FETCH_SIZE +
+  WRITE_SIZE, scaled by a plain copy of known size);
 * ``step_roofline``: algorithmic bytes of the whole step / step time;
 * ``cpu_baseline``: the CPU oracle (op-for-op fp32 PyTorch restatement of the
   reference eager step, B=1 per segment as the reference runs) timed on this
@@ -51,6 +56,44 @@ def read_traffic(kernel: str):
         if line.startswith("traffic_bytes_per_launch"):
             return float(line.split("=")[1].split()[0])
     return None
+
+
+def attn_kernel_ms(model, st, reps: int = 20) -> float:
+    """Mean duration of the decode-attention kernel: HIP events around ``reps``
+    back-to-back launches on the step's stream, over slot 0's cache and
+    positions with the step's launch configuration (XSA on, bf16 operands)."""
+    import ctypes
+
+    import torch
+
+    from altxs_amd import _lib
+
+    cfg = model.cfg
+    B, H, Hkv, max_len = st.batch, cfg.num_heads, cfg.num_kv_heads, st.max_len
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn(B, H, 64, generator=g, device="cuda")
+    y = torch.empty(B, H * 64, dtype=torch.bfloat16 if model.act_bf16 else torch.float32, device="cuda")
+    kv0 = st.kv[0]
+    a = _lib.AttnArgs()
+    a.B, a.W, a.H, a.Hkv, a.head_dim, a.max_len = B, 1, H, Hkv, 64, max_len
+    a.kv_bf16, a.y_bf16 = int(model.kv_bf16), int(model.act_bf16)
+    esz = kv0.element_size()
+    a.q, a.k = q.data_ptr(), kv0.data_ptr()
+    a.v = kv0.data_ptr() + Hkv * max_len * 64 * esz
+    a.kv_seg_stride = 2 * Hkv * max_len * 64
+    a.pos, a.gate, a.use_xsa = st.pos.data_ptr(), None, 1
+    a.flags = _lib.ATTN_OPS_BF16 if model.act_bf16 else 0
+    a.y, a.err = y.data_ptr(), st.err.data_ptr()
+    L, stream = _lib.load(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(L.altxs_decode_attn(ctypes.byref(a), stream), "altxs_decode_attn")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        L.altxs_decode_attn(ctypes.byref(a), stream)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def cpu_baseline(sm, ctx: int, seconds: float, seed: int = 0) -> dict:
@@ -100,6 +143,9 @@ def main() -> int:
     ap.add_argument("--persistent", action="store_true",
                     help="run every slot in one persistent launch (tasks in dependency order)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB five times (the known-size "
+                         "reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE), then exit")
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
 
@@ -111,6 +157,16 @@ def main() -> int:
 
     import numpy as np
     import torch
+
+    if a.copy_calibration > 0:
+        n = a.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+        return 0
 
     from altxs_amd import hiprt, synth
     from altxs_amd.config import make_config
@@ -167,6 +223,9 @@ def main() -> int:
     log(f"timed {a.steps} steps ({'graph' if graph is not None else 'eager'}): {ms:.3f} ms/step")
 
     # ---- dominant kernel: HIP events around every attention launch ----------
+    # The K instrumented steps are captured into one graph (distinct events per
+    # step) and replayed once, so the events see the graph's launch spacing;
+    # if capture is unavailable they run eagerly.
     n_slots = model.n_slots
     per_step = 2 * n_slots * groups
     ev = hiprt.EventArray(per_step * a.steps)
@@ -178,6 +237,20 @@ def main() -> int:
     s1.record()
     torch.cuda.synchronize()
     eager_ms = s0.elapsed_time(s1) / a.steps
+    event_timing = "eager"
+    if graph is not None:
+        try:
+            g2 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g2):
+                for k in range(a.steps):
+                    model.step(st, attn_events=ev.ptr + k * per_step * 8)
+            torch.cuda.synchronize()
+            g2.replay()
+            torch.cuda.synchronize()
+            event_timing = "hip-graph"
+        except Exception as exc:  # noqa: BLE001
+            log(f"instrumented graph failed ({exc!r}); using the eager event times")
+            torch.cuda.synchronize()
     kvb = 2 if a.kv == "bf16" else 4
     ab = synth.algorithmic_step_bytes(sm, B, ctx, kv_bytes=kvb)
     ybytes = 2 if a.act == "bf16" else 4
@@ -195,7 +268,12 @@ def main() -> int:
                       + B * cfg.num_heads * 4) / groups
         kname = "attn_mfma_kernel (decode attention)"
     ev.close()
-    attn_ms = float(np.mean(durs))
+    in_step_ms = float(np.mean(durs))  # events around each launch inside the step (incl. launch gaps)
+    if a.persistent or groups > 1 or a.kv != "bf16":
+        attn_ms = in_step_ms
+    else:
+        attn_ms = attn_kernel_ms(model, st)
+        st.check_errors()
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
     step_gbs = ab["total"] / (ms * 1e-3) / 1e9
     log(f"{kname.split(' ')[0]}: {attn_ms * 1e3:.1f} us/launch, {achieved:.0f} GB/s; eager step {eager_ms:.3f} ms; "
@@ -229,7 +307,7 @@ def main() -> int:
                          f"{a.act} activations, {a.kv} KV"),
             "segments": B, "ctx": ctx, "timing": "hip-graph" if graph is not None else "eager",
             "streams": groups, "persistent": bool(a.persistent),
-            "eager_ms_per_step": round(eager_ms, 4),
+            "eager_ms_per_step": round(eager_ms, 4), "kernel_event_timing": event_timing,
         },
         "roofline": {
             "kernel": kname,
@@ -241,6 +319,7 @@ def main() -> int:
             "traffic": read_traffic("layers" if a.persistent else "attn"),
             "bytes_per_launch": int(attn_bytes),
             "us_per_launch": round(attn_ms * 1e3, 2),
+            "us_per_launch_in_step": round(in_step_ms * 1e3, 2),
         },
         "step_roofline": {
             "algorithmic_bytes": int(ab["total"]),
