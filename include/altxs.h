@@ -4,8 +4,9 @@
  *
  * All pointers are device pointers unless stated otherwise; sizes are element
  * counts.  Every entry point enqueues work on `stream` (a hipStream_t passed as
- * void*; NULL = the legacy default stream), never synchronises, never
- * allocates, and returns ALTXS_OK (0) or a negative ALTXS_ERR_* code.  The
+ * void*; NULL = the legacy default stream), never allocates, never synchronises
+ * (except the set-up call altxs_step_plan_build, which waits for its copy),
+ * and returns ALTXS_OK (0) or a negative ALTXS_ERR_* code.  The
  * message for the last failure on the calling thread is altxs_last_error().
  * Runtime values that live in device memory (positions, token ids) cannot be
  * checked on the host; kernels skip out-of-range accesses and OR a code into
