@@ -12,7 +12,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libaltxs_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MAX_LAYERS = 32
 MAX_SLOTS = 64
@@ -76,16 +76,16 @@ class Layer(ctypes.Structure):
                 ("mlp_scale", ctypes.c_void_p), ("q_gain", ctypes.c_void_p),
                 ("attn_gate_w", ctypes.c_void_p), ("par_resid", ctypes.c_void_p),
                 ("par_post", ctypes.c_void_p),
-                ("lora_q_a", ctypes.c_void_p), ("lora_q_b", ctypes.c_void_p),
-                ("lora_v_a", ctypes.c_void_p), ("lora_v_b", ctypes.c_void_p),
-                ("lora_scale", ctypes.c_float), ("ln_scale", ctypes.c_float),
+                ("ln_scale", ctypes.c_float),
                 ("use_xsa", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class Slot(ctypes.Structure):
     _fields_ = [("layer", ctypes.c_int32), ("kind", ctypes.c_int32),
                 ("skip_idx", ctypes.c_int32), ("skip_src", ctypes.c_int32),
-                ("first_parallel", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("first_parallel", ctypes.c_int32), ("lora_scale", ctypes.c_float),
+                ("lora_q_a", ctypes.c_void_p), ("lora_q_b", ctypes.c_void_p),
+                ("lora_v_a", ctypes.c_void_p), ("lora_v_b", ctypes.c_void_p)]
 
 
 class StepDesc(ctypes.Structure):

@@ -28,6 +28,10 @@ struct SlotPlan {
   // the following slot (inputs formed by this slot's DOWN); has_next == 0: last slot
   int has_next, next_par, next_skip_src, next_skip_self;
   const float *next_mix, *next_skip_w, *next_skip_g;
+  // unmerged q/v LoRA of the slot (lora_rank 0: none)
+  const uint16_t *lqa, *lqb, *lva, *lvb;
+  float lora_s;
+  int lora_rank;
 };
 
 enum : int { ST_QKV = 0, ST_ATT = 1, ST_O = 2, ST_UP = 3, ST_DOWN = 4, N_ST = 5 };

@@ -130,6 +130,12 @@ struct Tasks {
     epi.Hkv = a.Hkv; epi.W = a.W; epi.max_len = a.max_len; epi.rd = a.rd; epi.pos = a.pos;
     epi.cosb = a.rope_cos; epi.sinb = a.rope_sin; epi.q_gain = uni(P.q_gain); epi.eps = a.eps;
     epi.err = a.err;
+    epi.rank = uni(P.lora_rank);
+    if (epi.rank > 0) {
+      epi.lqa = uni(P.lqa); epi.lqb = uni(P.lqb); epi.lva = uni(P.lva); epi.lvb = uni(P.lvb);
+      epi.lora_s = uni(P.lora_s);
+    }
+    epi.D = a.D; epi.a_f32 = AM == A_F32 ? 1 : 0;
     const CtrWait wt{s > 0 ? ctr(s - 1, m, ST_DOWN) : nullptr, a.n_task[ST_DOWN], a.err};
     gemm_task<0, AM, 4, 1>(wq, a.R, 16 * m, nt, 1 << 30, ADirect{nullptr, 0}, pro, epi, smem, 0,
                            wt);

@@ -146,7 +146,8 @@ int validate(const AltxsStepDesc* d) {
   ALTXS_REQUIRE(d->rope_dims >= 8 && d->rope_dims <= HD && d->rope_dims % 8 == 0,
                 "altxs_step: rope_dims=%d", d->rope_dims);
   ALTXS_REQUIRE(d->gate_window >= 0 && d->gate_window <= d->D, "altxs_step: gate_window");
-  ALTXS_REQUIRE(d->lora_rank == 0, "altxs_step: LoRA is not built in this version");
+  ALTXS_REQUIRE(d->lora_rank >= 0 && d->lora_rank <= 16, "altxs_step: lora_rank=%d not in [0, 16]",
+                d->lora_rank);
   ALTXS_REQUIRE(d->tokens && d->pos && d->prev_raw && d->cand_raw && d->kv && d->ws && d->logits &&
                     d->rope_cos && d->rope_sin && d->err,
                 "altxs_step: null state/output pointer");
@@ -182,6 +183,14 @@ int validate(const AltxsStepDesc* d) {
     if (S.kind == ALTXS_SLOT_PAR)
       ALTXS_REQUIRE(d->layers[S.layer].par_resid && d->layers[S.layer].par_post,
                     "altxs_step: slot %d parallel lambdas missing", s);
+    const int nl = (S.lora_q_a != nullptr) + (S.lora_q_b != nullptr) + (S.lora_v_a != nullptr) +
+                   (S.lora_v_b != nullptr);
+    ALTXS_REQUIRE(nl == 0 || (nl == 4 && d->lora_rank > 0),
+                  "altxs_step: slot %d LoRA needs all four matrices and lora_rank > 0", s);
+    if (nl)
+      ALTXS_REQUIRE(((uintptr_t)S.lora_q_a & 15) == 0 && ((uintptr_t)S.lora_v_a & 15) == 0 &&
+                        ((uintptr_t)S.lora_q_b & 1) == 0 && ((uintptr_t)S.lora_v_b & 1) == 0,
+                    "altxs_step: slot %d LoRA A must be 16-byte aligned", s);
   }
   return ALTXS_OK;
 }
@@ -265,6 +274,11 @@ struct StepRun {
     epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = G.pos;
     epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
     epi.err = d->err;
+    if (S.lora_q_a) {
+      epi.lqa = S.lora_q_a; epi.lqb = S.lora_q_b; epi.lva = S.lora_v_a; epi.lvb = S.lora_v_b;
+      epi.lora_s = S.lora_scale; epi.rank = d->lora_rank;
+    }
+    epi.D = d->D; epi.a_f32 = AM == A_F32 ? 1 : 0;
     return launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
                                       pro, epi, 0, st);
   }
@@ -451,6 +465,10 @@ void fill_plan(const AltxsStepDesc* d, const Group& G, char* host, const char* d
     P.par_post = L.par_post; P.ln_scale = L.ln_scale; P.use_xsa = L.use_xsa;
     P.par = S.kind == ALTXS_SLOT_PAR ? 1 : 0;
     P.first_parallel = S.first_parallel;
+    if (S.lora_q_a) {
+      P.lqa = S.lora_q_a; P.lqb = S.lora_q_b; P.lva = S.lora_v_a; P.lvb = S.lora_v_b;
+      P.lora_s = S.lora_scale; P.lora_rank = d->lora_rank;
+    }
     P.has_next = s + 1 < d->n_slots ? 1 : 0;
     if (P.has_next) {
       const AltxsSlot& S1 = d->slots[s + 1];

@@ -332,6 +332,11 @@ struct EpiQKV {
   const float* q_gain;
   float eps;
   int32_t* err;
+  // Unmerged LoRA of the slot (ttt_lora.py:53-55): q/v += s * (n A^T) B^T,
+  // n = the normalised input tile staged in LDS (bf16 or fp32: a_f32), D = K.
+  const uint16_t *lqa = nullptr, *lqb = nullptr, *lva = nullptr, *lvb = nullptr;
+  float lora_s = 0.f;
+  int rank = 0, D = 0, a_f32 = 0;
   template <class Cfg> struct Pre {
     static constexpr int TPR = Cfg::THREADS / 16, CPT = 64 / TPR;
     int p;
@@ -358,8 +363,60 @@ struct EpiQKV {
     }
     return o;
   }
+  // t = n A^T for the 16 rows (one 16x16 MFMA tile over K = D, operands in
+  // fp16: bf16 inputs convert exactly, fp32 inputs as two fp16 parts; A is
+  // fp16), then v[c] += s * sum_j t[row][j] B[col][j] in fp32, j < rank <= 16.
+  template <class Cfg, int CPT>
+  __device__ void lora_add(float (&v)[CPT], const void* As, int kind, int head, int row,
+                           int c0) const {
+    __shared__ float lt[16][17];
+    const uint16_t* A = kind == 0 ? lqa : lva;
+    const uint16_t* Bm = kind == 0 ? lqb : lvb;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (wave == 0) {
+      const int r = lane & 15, kq = 8 * (lane >> 4);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < D / 32; ++s) {
+        const int k = 32 * s + kq;
+        f16x8 a0, a1, b;
+        if (a_f32) {
+          const float* x = (const float*)As + r * lds_stride(D, A_F32) + k;
+          const f32x4 lo = *(const f32x4*)x, hi = *(const f32x4*)(x + 4);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float f = i < 4 ? lo[i] : hi[i - 4];
+            a0[i] = (_Float16)f;
+            a1[i] = (_Float16)(f - (float)a0[i]);
+          }
+        } else {
+          const u32x4 raw = *(const u32x4*)((const uint16_t*)As + r * lds_stride(D, A_BF16) + k);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            a0[2 * i] = (_Float16)bf16_lo(raw[i]);
+            a0[2 * i + 1] = (_Float16)bf16_hi(raw[i]);
+          }
+        }
+        if (r < rank) b = __builtin_bit_cast(f16x8, *(const u32x4*)(A + (int64_t)r * D + k));
+        else b = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, acc, 0, 0, 0);
+        if (a_f32) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lt[4 * (lane >> 4) + i][lane & 15] = acc[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const uint16_t* brow = Bm + (int64_t)(head * HD + c0 + i) * rank;
+      float d = 0.f;
+      for (int j = 0; j < rank; ++j) d += lt[row][j] * __half2float(__ushort_as_half(brow[j]));
+      v[i] += lora_s * d;
+    }
+  }
+
   template <class Cfg, class P>
-  __device__ void apply(const float* C, const P& pre, const void*, int m0, int n0, int R, int) const {
+  __device__ void apply(const float* C, const P& pre, const void* As, int m0, int n0, int R,
+                        int) const {
     constexpr int TPR = P::TPR, CPT = P::CPT;
     const int row = threadIdx.x / TPR, li = threadIdx.x % TPR, c0 = li * CPT;
     const int r = m0 + row;
@@ -369,6 +426,7 @@ struct EpiQKV {
     float v[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) v[i] = C[row * Cfg::CS + c0 + i];
+    if (rank > 0 && kind != 1) lora_add<Cfg, CPT>(v, As, kind, head, row, c0);
     if (kind < 2) {
       float ss = 0.f;
 #pragma unroll

@@ -173,7 +173,9 @@ class StepModel:
             n, k = p.shape
             self.qt[name] = _lib.QTensor(codes.data_ptr(), scales.data_ptr(), n, k, p.bits, 0)
         sm = synth.small
-        self.small = {k: _dev(v, dev) for k, v in sm.items()}
+        self.small = {k: _dev(v, dev) for k, v in sm.items() if "_loras." not in k}
+        # LoRA matrices in fp16 (the values are fp16-exact), as the C-ABI reads them
+        self.lora = {k: _dev(v, dev, torch.float16) for k, v in sm.items() if "_loras." in k}
         self.synth = synth
         self._cos_cache: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         self._disabled = False
@@ -200,7 +202,8 @@ class StepModel:
         d.B, d.W, d.D, d.H, d.Hkv = st.batch, st.win, cfg.model_dim, cfg.num_heads, cfg.num_kv_heads
         d.head_dim, d.F, d.V = cfg.head_dim, cfg.hidden_dim, cfg.vocab_size
         d.n_layers, d.n_slots, d.max_len = cfg.num_layers, self.n_slots, st.max_len
-        d.gate_window, d.rope_dims, d.lora_rank = cfg.gate_window, cfg.rope_dims_eff, 0
+        d.gate_window, d.rope_dims = cfg.gate_window, cfg.rope_dims_eff
+        d.lora_rank = cfg.lora_rank if self.lora else 0
         d.act_bf16, d.kv_bf16 = int(self.act_bf16), int(self.kv_bf16)
         f = flags
         if cfg.smear_gate_enabled:
@@ -232,13 +235,18 @@ class StepModel:
             ly.attn_gate_w = g.data_ptr() if g is not None else None
             ly.par_resid = sm["parallel_resid_lambdas"][i].data_ptr()
             ly.par_post = sm["parallel_post_lambdas"][i].data_ptr()
-            ly.lora_scale = 0.0
             ly.ln_scale = float(1.0 / np.sqrt(i + 1)) if cfg.ln_scale else 1.0
             ly.use_xsa = int(cfg.xsa_last_n > 0 and i >= L - cfg.xsa_last_n)
         for s, sl in enumerate(self.slots):
             o = d.slots[s]
             o.layer, o.kind, o.skip_idx = sl["layer"], sl["kind"], sl["skip_idx"]
             o.skip_src, o.first_parallel = sl["skip_src"], sl["first_parallel"]
+            if self.lora:
+                o.lora_scale = cfg.lora_alpha / cfg.lora_rank
+                o.lora_q_a = self.lora[f"q_loras.{s}.A"].data_ptr()
+                o.lora_q_b = self.lora[f"q_loras.{s}.B"].data_ptr()
+                o.lora_v_a = self.lora[f"v_loras.{s}.A"].data_ptr()
+                o.lora_v_b = self.lora[f"v_loras.{s}.B"].data_ptr()
         d.emb = self.qt["emb"]
         d.skip_weights = sm["skip_weights"].data_ptr()
         d.skip_gates = sm["skip_gates"].data_ptr() if "skip_gates" in sm else None

@@ -131,6 +131,17 @@ def make_model(cfg: AltxsConfig, *, seed: int = WEIGHT_SEED, std: float = 0.02,
         small[f"blocks.{i}.attn.q_gain"] = cfg.qk_gain_init + noise(H, scale=0.3)
         if cfg.sparse_attn_gate_enabled:
             small[f"blocks.{i}.attn.attn_gate_w"] = noise(H, gw, scale=0.3)
+    if cfg.lora_rank > 0:
+        # per-slot q/v adapters (TTTLoRA.q_loras/v_loras, ttt_lora.py:64-120), fp16
+        # values N(0, 0.01^2) for A and B (BASELINE cfg5; the reference starts B at 0)
+        lrng = np.random.default_rng(seed + 2)
+        r = cfg.lora_rank
+        for sl in range(len(enc) + len(dec)):
+            for kind, n_out in (("q", d), ("v", kvd)):
+                a = lrng.standard_normal((r, d)) * 0.01
+                b = lrng.standard_normal((n_out, r)) * 0.01
+                small[f"{kind}_loras.{sl}.A"] = a.astype(np.float16).astype(np.float32)
+                small[f"{kind}_loras.{sl}.B"] = b.astype(np.float16).astype(np.float32)
     return SynthModel(cfg, packed, small)
 
 

@@ -316,7 +316,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic("layers" if a.persistent else "attn"),
+            # measured for the default workload only (cfg3, 64 segments, ctx 2048)
+            "traffic": (read_traffic("layers" if a.persistent else "attn")
+                        if (a.profile, B, ctx, a.act, a.kv) == ("cfg3", 64, 2048, "bf16", "bf16") else None),
             "bytes_per_launch": int(attn_bytes),
             "us_per_launch": round(attn_ms * 1e3, 2),
             "us_per_launch_in_step": round(in_step_ms * 1e3, 2),

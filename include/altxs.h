@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define ALTXS_ABI_VERSION 4
+#define ALTXS_ABI_VERSION 5
 
 enum {
   ALTXS_OK = 0,
@@ -186,11 +186,6 @@ typedef struct AltxsLayer {
   const float *attn_gate_w;  /* [H, gate_window] or NULL */
   const float *par_resid;    /* [2] parallel_resid_lambdas[layer] or NULL */
   const float *par_post;     /* [2, 2] parallel_post_lambdas[layer] or NULL */
-  const uint16_t *lora_q_a;  /* LoRA (fp16) A [rank, D], B [H*hd, rank]; NULL = off */
-  const uint16_t *lora_q_b;
-  const uint16_t *lora_v_a;  /* A [rank, D], B [Hkv*hd, rank] */
-  const uint16_t *lora_v_b;
-  float lora_scale;
   float ln_scale;            /* 1/sqrt(layer+1) with ln_scale, else 1 */
   int32_t use_xsa;
   int32_t reserved;
@@ -202,7 +197,15 @@ typedef struct AltxsSlot {
   int32_t skip_idx;        /* decoder skip weight row, -1 = none */
   int32_t skip_src;        /* slot whose output is popped, -1 = none */
   int32_t first_parallel;  /* first parallel slot: both lanes start from x */
-  int32_t reserved;
+  /* Unmerged LoRA on this slot's q and v projections (rank = desc.lora_rank,
+   * 1..16; all four NULL = none): q += s * (n A_q^T) B_q^T, v likewise, added
+   * to the projection before QK-RMSNorm/RoPE (ttt_lora.py:53-55, 143-151;
+   * per slot as the reference's q_loras[slot]).  fp16, row-major. */
+  float lora_scale;          /* s = alpha/rank (or alpha/sqrt(rank) for rsLoRA) */
+  const uint16_t *lora_q_a;  /* [rank, D] */
+  const uint16_t *lora_q_b;  /* [H*head_dim, rank] */
+  const uint16_t *lora_v_a;  /* [rank, D] */
+  const uint16_t *lora_v_b;  /* [Hkv*head_dim, rank] */
 } AltxsSlot;
 
 typedef struct AltxsStepDesc {

@@ -12,7 +12,9 @@ tests run (XSA_AC_FUSED=0): ``GPT.static_extend`` (src/xsa_ttt/model.py:
   1275-1291 / _final_parallel_hidden 1357-1362;
 * CausalSelfAttention.forward 770-871 (QK-RMSNorm, RoPE 130-206 incl. YaRN,
   q_gain, _static_window_attention 550-585, XSA 760-768, sparse gate 854-862);
-* MLP 874-882; _project_logits + _apply_asym_softcap 1463-1500.
+* MLP 874-882; _project_logits + _apply_asym_softcap 1463-1500;
+* unmerged q/v LoRA per slot, when the config has a LoRA rank: LinearLoRA
+  (src/xsa_ttt/ttt_lora.py:22-55) as _block_with_lora adds it (143-151).
 
 Pinning: against logits written by the reference GPT itself on the same
 weights and tokens (tests/golden/model_*.npz from tests/golden/make_golden.py);
@@ -115,6 +117,9 @@ class OracleModel:
         self.n_skip = min(len(self.enc), len(self.dec))
         self.max_len = int(max_len)
         self.cos, self.sin = rotary_table(cfg, self.max_len)
+        # unmerged q/v LoRA per slot (ttt_lora.py:22-55, 143-151): scale alpha/rank
+        self.lora_rank = int(getattr(cfg, "lora_rank", 0) or 0)
+        self.lora_scale = float(cfg.lora_alpha) / self.lora_rank if self.lora_rank else 0.0
 
     # ---- helpers ----------------------------------------------------------
     def _r(self, x: torch.Tensor) -> torch.Tensor:
@@ -165,14 +170,25 @@ class OracleModel:
         return c * torch.tanh(lg / c)
 
     # ---- attention ----------------------------------------------------------
-    def _qkv(self, i: int, n: torch.Tensor, positions: torch.Tensor):
-        """Projections + QK-RMSNorm + RoPE + q_gain (model.py:783-812). n [T, D]."""
+    def _lora(self, kind: str, slot: int, x: torch.Tensor) -> torch.Tensor:
+        """LinearLoRA.forward (ttt_lora.py:53-55): (x @ A.T @ B.T) * scale."""
+        a, b = self.sd[f"{kind}_loras.{slot}.A"], self.sd[f"{kind}_loras.{slot}.B"]
+        return (x @ a.T @ b.T) * self.lora_scale
+
+    def _qkv(self, i: int, n: torch.Tensor, positions: torch.Tensor, slot: int = -1):
+        """Projections (+ the slot's q/v LoRA, _block_with_lora ttt_lora.py:143-151)
+        + QK-RMSNorm + RoPE + q_gain (model.py:783-812). n [T, D]."""
         q_w, k_w, v_w, _, _, _ = self._bank(i)
         T = n.shape[0]
         nr = self._r(n)
-        q = F.linear(nr, q_w).reshape(T, self.H, self.hd)
+        q = F.linear(nr, q_w)
+        v = F.linear(nr, v_w)
+        if self.lora_rank and slot >= 0:
+            q = q + self._lora("q", slot, nr)
+            v = v + self._lora("v", slot, nr)
+        q = q.reshape(T, self.H, self.hd)
         k = F.linear(nr, k_w).reshape(T, self.Hkv, self.hd)
-        v = F.linear(nr, v_w).reshape(T, self.Hkv, self.hd)
+        v = v.reshape(T, self.Hkv, self.hd)
         q = _rms(q)
         k = _rms(k)
         cos, sin = self.cos[positions], self.sin[positions]
@@ -215,7 +231,7 @@ class OracleModel:
     def _attn_static(self, i: int, slot: int, st: OracleState, n: torch.Tensor):
         T = n.shape[0]
         pos = torch.arange(st.pos, st.pos + T)
-        q, k, v = self._qkv(i, n, pos)
+        q, k, v = self._qkv(i, n, pos, slot)
         k, v = self._r(k), self._r(v)  # cache storage rounding (bf16 mode)
         q = self._r(q)  # bf16 score operand (split_attn.py:86-93 rounds q to bf16)
         st.k[slot][st.pos:st.pos + T] = k
@@ -306,8 +322,11 @@ class OracleModel:
         x0 = x
         pos = torch.arange(T)
 
+        slot_ctr = [0]
+
         def attn(i, n):
-            q, k, v = self._qkv(i, n, pos)
+            q, k, v = self._qkv(i, n, pos, slot_ctr[0])
+            slot_ctr[0] += 1
             k, v = self._r(k), self._r(v)
             y = self._attend(q, k, v, pos + 1)
             return self._post_attn(i, y, v, n)

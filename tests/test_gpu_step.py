@@ -26,7 +26,12 @@ CASES = {
     # profile: (B segments, T steps, weight std, softcap)
     "tiny": (3, 12, 0.08, (2.0, 1.5)),     # every motif feature, large activations
     "cfg1": (2, 16, 0.02, (30.0, 24.0)),   # BASELINE cfg1 weights (std 0.02)
+    # the same with unmerged per-slot q/v LoRA (rank 8 exercises rank < 16)
+    "tiny_lora": (3, 12, 0.08, (2.0, 1.5)),
+    "cfg1_lora": (2, 16, 0.02, (30.0, 24.0)),
 }
+LORA = {"tiny_lora": ("tiny", dict(lora_rank=8, lora_alpha=12.0)),
+        "cfg1_lora": ("cfg1", dict(lora_rank=16, lora_alpha=16.0))}
 _MODELS: dict = {}
 
 
@@ -40,7 +45,8 @@ def _synth(profile):
         from altxs_amd.config import make_config
 
         B, T, std, cap = CASES[profile]
-        cfg = make_config(profile)
+        base, over = LORA.get(profile, (profile, {}))
+        cfg = make_config(base, **over)
         _MODELS[profile] = synth.make_model(cfg, std=std, softcap=cap)
     return _MODELS[profile]
 
@@ -88,7 +94,7 @@ def _gpu_decode(profile, act, B=None, W=1, kv=None):
     return torch.cat(lg, 1).numpy(), torch.cat(cm, 1).numpy().astype(np.int64), model, st
 
 
-@pytest.mark.parametrize("profile", ["tiny", "cfg1"])
+@pytest.mark.parametrize("profile", ["tiny", "cfg1", "tiny_lora", "cfg1_lora"])
 def test_step_fp32_matches_oracle(profile):
     _log(f"step fp32 {profile}")
     got, _, _, _ = _gpu_decode(profile, "fp32")
@@ -106,7 +112,8 @@ def test_step_fp32_act_bf16_kv_meets_tolerance():
     assert err < LOGIT_TOL, err
 
 
-@pytest.mark.parametrize("profile,mean_tol,max_tol", [("tiny", 3e-3, 6e-2), ("cfg1", 5e-4, 1e-2)])
+@pytest.mark.parametrize("profile,mean_tol,max_tol", [("tiny", 3e-3, 6e-2), ("cfg1", 5e-4, 1e-2),
+                                                      ("cfg1_lora", 5e-4, 1e-2)])
 def test_step_bf16_matches_oracle_emulation(profile, mean_tol, max_tol):
     _log(f"step bf16 {profile}")
     got, _, _, _ = _gpu_decode(profile, "bf16")
@@ -128,6 +135,23 @@ def test_cdf_bit_identical_decode_encode_batch(act):
     assert np.array_equal(cmb[0], cm1[0])
     _, cmr, _, _ = _gpu_decode(profile, act, W=1)  # rerun
     assert np.array_equal(cmr, cm1)
+
+
+@pytest.mark.parametrize("act", ["fp32", "bf16"])
+def test_lora_cdf_bit_identical_decode_encode(act):
+    """With per-slot LoRA on, decode rows, encode windows and a smaller batch
+    still give the same integer tables."""
+    profile = "tiny_lora"
+    _log(f"lora lockstep {act}")
+    lg1, cm1, _, _ = _gpu_decode(profile, act, W=1)
+    lg4, cm4, _, _ = _gpu_decode(profile, act, W=4)
+    assert np.array_equal(cm1, cm4)
+    assert np.array_equal(lg1, lg4)
+    _, cmb, _, _ = _gpu_decode(profile, act, B=1, W=1)
+    assert np.array_equal(cmb[0], cm1[0])
+    # and the adapters change the result (the test would pass vacuously otherwise)
+    lg0, _, _, _ = _gpu_decode("tiny", act, W=1)
+    assert np.abs(lg0 - lg1).max() > 1e-3
 
 
 def test_bits_per_symbol_within_tenth_percent():

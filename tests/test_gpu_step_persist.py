@@ -31,8 +31,10 @@ def _synth(profile):
         from altxs_amd.config import make_config
 
         std, cap = {"tiny": (0.08, (2.0, 1.5)), "cfg1": (0.02, (30.0, 24.0)),
-                    "cfg3": (0.02, (30.0, 24.0))}[profile]
-        _MODELS[profile] = synth.make_model(make_config(profile), std=std, softcap=cap)
+                    "cfg3": (0.02, (30.0, 24.0)), "tiny_lora": (0.08, (2.0, 1.5))}[profile]
+        cfg = (make_config("tiny", lora_rank=8, lora_alpha=12.0) if profile == "tiny_lora"
+               else make_config(profile))
+        _MODELS[profile] = synth.make_model(cfg, std=std, softcap=cap)
     return _MODELS[profile]
 
 
@@ -59,6 +61,8 @@ def _run_steps(sm, act, W, toks, persistent, max_len=256):
     ("tiny", "fp32", 1, 3, 8),
     ("cfg1", "bf16", 1, 2, 12),
     ("cfg1", "bf16", 2, 5, 8),
+    ("tiny_lora", "bf16", 1, 3, 8),
+    ("tiny_lora", "fp32", 2, 3, 8),
 ])
 def test_persistent_bit_identical(profile, act, W, B, T):
     from altxs_amd import synth

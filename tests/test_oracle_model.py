@@ -148,3 +148,35 @@ def test_bf16_emulation_is_close_to_fp32():
     b = OracleModel(cfg, sm.state_dict(), max_len=256, act="bf16").decode_rows(toks)
     d = (a - b).abs().max().item()
     assert 0 < d < 0.1
+
+
+def test_lora_unmerged_equals_merged():
+    """Unmerged per-slot q/v LoRA (x @ A.T @ B.T * alpha/r, ttt_lora.py:53-55,
+    added to the q and v projections, 143-151) equals the dense model whose q
+    and v rows are W + (alpha/r) B @ A.  One slot per layer (no depth loops),
+    so each adapter folds into its own layer.  Moving the adapter to k, using
+    the wrong scale or A/B the wrong way round all fail this check."""
+    from oracle.model_ref import iter_indices
+
+    cfg = make_config("tiny", num_loops=0, lora_rank=8, lora_alpha=12.0)
+    sm = synth.make_model(cfg, std=0.08, softcap=(2.0, 1.5))
+    sd = sm.state_dict()
+    toks = synth.zipf_tokens(cfg.vocab_size, (10,), seed=3)
+    got = OracleModel(cfg, sd, max_len=256).decode_rows(toks)
+    enc, dec = iter_indices(cfg)
+    layers = list(enc) + list(dec)
+    assert sorted(layers) == list(range(cfg.num_layers))
+    merged = {k: np.array(v, copy=True) for k, v in sd.items() if "_loras." not in k}
+    s = cfg.lora_alpha / cfg.lora_rank
+    n = cfg.num_layers
+    for slot, layer in enumerate(layers):
+        dq = s * sd[f"q_loras.{slot}.B"].astype(np.float64) @ sd[f"q_loras.{slot}.A"].astype(np.float64)
+        dv = s * sd[f"v_loras.{slot}.B"].astype(np.float64) @ sd[f"v_loras.{slot}.A"].astype(np.float64)
+        merged["qo_bank"][layer] += dq.astype(np.float32)
+        merged["kv_bank"][n + layer] += dv.astype(np.float32)
+    want = OracleModel(make_config("tiny", num_loops=0), merged, max_len=256).decode_rows(toks)
+    err = (got - want).abs().max().item()
+    assert err < 1e-4, err
+    base = OracleModel(make_config("tiny", num_loops=0), sd, max_len=256).decode_rows(toks)
+    assert (got - base).abs().max().item() > 1e-2  # the adapters matter at this scale
+
