@@ -29,6 +29,7 @@ F_FINAL_ATTN = 1 << 6
 F_FINAL_MLP = 1 << 7
 CDF_RENORM = 1
 ATTN_OPS_BF16 = 1
+ATTN_ROWS = 2
 KV_TILE = 64
 
 SLOT_SEQ, SLOT_PAR = 0, 1

@@ -243,4 +243,195 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   });
 }
 
+// ---------------------------------------------------------------------------
+// bf16 cache, windows (W > 1): 16*NG consecutive query rows of one segment and
+// one query head per workgroup, so each K/V tile is read once for all of them.
+// Every query column performs exactly the decode task's arithmetic: the same
+// MFMA operand placement for its scores and P x V, tile T on wave T mod 4, the
+// same online softmax and the same wave-order merge.  Tiles past a query's
+// own last key are fully masked for it; they leave its running state
+// unchanged (alpha = 1, P = 0, and a wave that has seen no key keeps
+// m = -inf), so a window row gives the bits of the decode row.
+// ---------------------------------------------------------------------------
+
+struct WinLds {
+  float m[ATT_WAVES][16];
+  float l[ATT_WAVES][16];
+  float acc[ATT_WAVES][16][HD];
+};
+
+template <int NG, int NP, int YBF16>
+__device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, int t0, WinLds& sm) {
+  static_assert(TILE == 64, "the MFMA tiling below assumes 64-key tiles");
+  const int G = a.H / a.Hkv, g = h / G;
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const int lg = lane >> 4, col = lane & 15;
+  const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
+  const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
+  const int base = a.pos[b];
+  // this lane's query column in each group: window index t, position p (-1: inactive)
+  int pc[NG];
+  bf16x8 qop[NG][2][NP];
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const int t = t0 + 16 * gi + col;
+    int p = -1;
+    if (t < a.W) {
+      p = base + t;
+      if (p < 0 || p >= a.max_len) {
+        flag_err(a.err, ALTXS_EDEV_POS);
+        p = p < 0 ? 0 : a.max_len - 1;
+      }
+    }
+    pc[gi] = p;
+    const float* qh = a.q + ((int64_t)(b * a.W + (t < a.W ? t : 0)) * a.H + h) * HD;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float x[8];
+      if (t < a.W) {
+        const f32x4 lo = *(const f32x4*)(qh + 32 * ks + 8 * lg);
+        const f32x4 hi = *(const f32x4*)(qh + 32 * ks + 8 * lg + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { x[i] = lo[i] * 0.125f; x[4 + i] = hi[i] * 0.125f; }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = 0.f;
+      }
+      split_parts<NP>(x, qop[gi][ks]);
+    }
+  }
+  // keys to visit: up to the last active query of the workgroup (uniform)
+  const int t_last = (t0 + 16 * NG < a.W ? t0 + 16 * NG : a.W) - 1;
+  int p_last = base + t_last;
+  p_last = p_last < 0 ? 0 : (p_last >= a.max_len ? a.max_len - 1 : p_last);
+  const int ntiles = (p_last + TILE) / TILE;
+
+  float m_run[NG], l_part[NG];
+  f32x4 acc[NG][4];
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    m_run[gi] = -INFINITY;
+    l_part[gi] = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc[gi][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int T = wave; T < ntiles; T += ATT_WAVES) {
+    const u32x4* kt = (const u32x4*)(kb + (int64_t)T * (TILE * HD)) + lane;
+    const u32x4* vt = (const u32x4*)(vb + (int64_t)T * (TILE * HD)) + lane;
+    u32x4 kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = __builtin_nontemporal_load(kt + 64 * i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vr[i] = __builtin_nontemporal_load(vt + 64 * i);
+    const int k0 = T * TILE;
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      f32x4 S[4];
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        S[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const bf16x8 kop = __builtin_bit_cast(bf16x8, kr[2 * blk + ks]);
+#pragma unroll
+          for (int k = 0; k < NP; ++k)
+            S[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[gi][ks][k], S[blk], 0, 0, 0);
+        }
+      }
+      float mt = -INFINITY;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (k0 + 16 * blk + 4 * lg + i > pc[gi]) S[blk][i] = -INFINITY;
+          mt = fmaxf(mt, S[blk][i]);
+        }
+      mt = rows_max(mt);
+      const float m_new = fmaxf(m_run[gi], mt);
+      const bool none = m_new == -INFINITY;  // no key of this query seen yet
+      const float alpha = none ? 1.f : __expf(m_run[gi] - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          S[blk][i] = none ? 0.f : __expf(S[blk][i] - m_new);
+          ps += S[blk][i];
+        }
+      l_part[gi] = l_part[gi] * alpha + ps;
+      m_run[gi] = m_new;
+      // acc row 4*lg + i is query column 4*lg + i: its alpha lives on that lane
+      float al[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lg + i, WAVE);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[gi][nb][i] *= al[i];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float pv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { pv[i] = S[2 * s][i]; pv[4 + i] = S[2 * s + 1][i]; }
+        bf16x8 pop[NP];
+        split_parts<NP>(pv, pop);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          const bf16x8 vop = __builtin_bit_cast(bf16x8, vr[4 * s + nb]);
+#pragma unroll
+          for (int k = 0; k < NP; ++k)
+            acc[gi][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[k], vop, acc[gi][nb], 0, 0, 0);
+        }
+      }
+    }
+  }
+  // merge and store, one group of 16 queries at a time (wave w: queries w, w+4, ...)
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const float lsum = rows_sum(l_part[gi]);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm.acc[wave][4 * lg + i][16 * nb + col] = acc[gi][nb][i];
+    if (lane < 16) {
+      sm.m[wave][lane] = m_run[gi];
+      sm.l[wave][lane] = lsum;
+    }
+    __syncthreads();
+    for (int q = wave; q < 16; q += ATT_WAVES) {
+      const int t = t0 + 16 * gi + q;
+      if (t >= a.W) continue;
+      const int r = b * a.W + t;
+      int p = base + t;
+      p = p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p);
+      const int d = lane;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, sm.m[w][q]);
+      float Ls = 0.f, Y = 0.f;
+#pragma unroll
+      for (int w = 0; w < ATT_WAVES; ++w) {
+        const float mw = sm.m[w][q];
+        if (mw == -INFINITY) continue;
+        const float f = __expf(mw - M);
+        Ls += sm.l[w][q] * f;
+        Y += sm.acc[w][q][d] * f;
+      }
+      float y = Y / Ls;
+      if (a.use_xsa) {
+        const float vv = bf16_to_f32(vb[(int64_t)(p / TILE) * (TILE * HD) + kv_tile_v(p % TILE, d)]);
+        const float nrm = sqrtf(wave_sum(vv * vv));
+        const float vn = vv / fmaxf(nrm, 1e-12f);
+        const float dot = wave_sum(y * vn);
+        y = y - dot * vn;
+      }
+      if (a.gate) y *= a.gate[(int64_t)r * a.H + h];
+      const int64_t o = ((int64_t)r * a.H + h) * HD + d;
+      if (YBF16) ((uint16_t*)a.y)[o] = f32_to_bf16(y);
+      else ((float*)a.y)[o] = y;
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace altxs_attn

@@ -42,6 +42,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   attn_mfma_task<G, NP, YBF16, ALTXS_ATT_PF>(a, blockIdx.x / a.Hkv, blockIdx.x % a.Hkv, sm);
 }
 
+// Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
+// per workgroup; grid = B x H x ceil(W / (16*NG)).
+template <int NG, int NP, int YBF16>
+__global__ __launch_bounds__(ATT_THREADS) void attn_window_kernel(AttnP a) {
+  __shared__ WinLds sm;
+  const int nqb = (a.W + 16 * NG - 1) / (16 * NG);
+  const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
+  attn_window_task<NG, NP, YBF16>(a, bh / a.H, bh % a.H, qb * 16 * NG, sm);
+}
+
 // ---------------------------------------------------------------------------
 // fp32 cache: VALU kernel on the natural [key][64] layout.
 // ---------------------------------------------------------------------------
@@ -154,10 +164,28 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
 }
 
 template <int YBF16>
-hipError_t launch_y(const AttnP& p, int group, bool kv_bf16, bool ops_bf16, hipStream_t s) {
+hipError_t launch_y(const AttnP& p, int group, bool kv_bf16, bool ops_bf16, bool rows_only,
+                    hipStream_t s) {
   dim3 grid((unsigned)(p.B * p.W * p.Hkv)), block(ATT_THREADS);
 #define ATT_GO(K) \
   do { hipLaunchKernelGGL(K, grid, block, 0, s, p); return hipGetLastError(); } while (0)
+  if (kv_bf16 && p.W > 1 && !rows_only) {
+    const int ng = p.W <= 16 ? 1 : (p.W <= 32 ? 2 : 4);
+    const int nqb = (p.W + 16 * ng - 1) / (16 * ng);
+    dim3 wgrid((unsigned)((int64_t)p.B * p.H * nqb));
+#define WIN_GO(K) \
+  do { hipLaunchKernelGGL(K, wgrid, block, 0, s, p); return hipGetLastError(); } while (0)
+    if (ops_bf16) {
+      if (ng == 1) WIN_GO((attn_window_kernel<1, 1, YBF16>));
+      if (ng == 2) WIN_GO((attn_window_kernel<2, 1, YBF16>));
+      WIN_GO((attn_window_kernel<4, 1, YBF16>));
+    } else {
+      if (ng == 1) WIN_GO((attn_window_kernel<1, 3, YBF16>));
+      if (ng == 2) WIN_GO((attn_window_kernel<2, 3, YBF16>));
+      WIN_GO((attn_window_kernel<4, 3, YBF16>));
+    }
+#undef WIN_GO
+  }
   if (kv_bf16) {
     if (ops_bf16) {
       if (group == 1) ATT_GO((attn_mfma_kernel<1, 1, YBF16>));
@@ -186,8 +214,9 @@ hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s) {
   p.pos = a.pos; p.gate = a.gate; p.use_xsa = a.use_xsa; p.y = a.y; p.err = a.err;
   const int group = a.H / a.Hkv;
   const bool ops_bf16 = (a.flags & ALTXS_ATTN_OPS_BF16) != 0;
-  return a.y_bf16 ? launch_y<1>(p, group, a.kv_bf16 != 0, ops_bf16, s)
-                  : launch_y<0>(p, group, a.kv_bf16 != 0, ops_bf16, s);
+  const bool rows_only = (a.flags & ALTXS_ATTN_ROWS) != 0;
+  return a.y_bf16 ? launch_y<1>(p, group, a.kv_bf16 != 0, ops_bf16, rows_only, s)
+                  : launch_y<0>(p, group, a.kv_bf16 != 0, ops_bf16, rows_only, s);
 }
 
 extern "C" int32_t altxs_decode_attn(const AltxsAttnArgs* a, altxs_stream_t stream) {
@@ -203,8 +232,8 @@ extern "C" int32_t altxs_decode_attn(const AltxsAttnArgs* a, altxs_stream_t stre
                 "altxs_decode_attn: max_len=%d must be a positive multiple of %d", a->max_len, TILE);
   ALTXS_REQUIRE(a->kv_seg_stride >= (int64_t)a->Hkv * a->max_len * HD,
                 "altxs_decode_attn: kv_seg_stride too small");
-  ALTXS_REQUIRE((a->flags & ~ALTXS_ATTN_OPS_BF16) == 0, "altxs_decode_attn: unknown flags 0x%x",
-                a->flags);
+  ALTXS_REQUIRE((a->flags & ~(ALTXS_ATTN_OPS_BF16 | ALTXS_ATTN_ROWS)) == 0,
+                "altxs_decode_attn: unknown flags 0x%x", a->flags);
   ALTXS_REQUIRE(((uintptr_t)a->k & 15) == 0 && ((uintptr_t)a->v & 15) == 0 && ((uintptr_t)a->q & 15) == 0,
                 "altxs_decode_attn: q, k and v must be 16-byte aligned");
   ALTXS_CHECK_HIP(altxs_launch_attn(*a, (hipStream_t)stream));

@@ -127,6 +127,82 @@ def cpu_baseline(sm, ctx: int, seconds: float, seed: int = 0) -> dict:
                       f"{el:.1f} s, torch threads={cores})"}
 
 
+def window_bench(a) -> int:
+    """--window W > 1: one step scores W tokens of each of B segments from position 0
+    (the prefill-style chunk scoring of BASELINE cfg4: causal attention over the
+    chunk, MFMA GEMMs, one CDF per token).  MFMA-bound, so ``roofline`` is in
+    TFLOP/s against the dense bf16 peak."""
+    import numpy as np
+    import torch
+
+    from altxs_amd import synth
+    from altxs_amd.config import make_config
+    from altxs_amd.model import StepModel
+
+    B, W = a.segments, a.window
+    max_len = (W + 255) // 256 * 256
+    cfg = make_config(a.profile)
+    sm = synth.make_model(cfg)
+    model = StepModel(sm, act=a.act, kv=a.kv)
+    st = model.make_static_state(max_len, win=W, batch=B, want_probs=False, want_cdf=True)
+    st.pos.zero_()
+    st.token.copy_(torch.from_numpy(synth.zipf_tokens(cfg.vocab_size, (B, W)).astype(np.int32)))
+    for _ in range(a.warmup):
+        model.step(st)
+    torch.cuda.synchronize()
+    st.check_errors()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model.step(st)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(a.steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / a.steps
+    st.check_errors()
+    R = B * W
+    body = sum(p.codes.size for n, p in sm.packed.items() if n != "emb")
+    n_slots = model.n_slots
+    attn = 4 * 64 * (W * (W + 1) // 2) * cfg.num_heads * B * n_slots
+    flops = 2 * R * body + 2 * R * cfg.vocab_size * cfg.model_dim + attn
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak = 2500.0 if a.act == "bf16" else 157.3
+    log(f"window W={W} x {B} segments: {ms:.3f} ms/step, {R / (ms * 1e-3) / 1e6:.2f} M sym/s, "
+        f"{tflops:.0f} TFLOP/s")
+    cpu = None
+    if not a.no_cpu:
+        from oracle.model_ref import OracleModel
+
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        om = OracleModel(cfg, sm.state_dict(), act="fp32", max_len=max_len)
+        ids = synth.zipf_tokens(cfg.vocab_size, (W,), seed=3)
+        t0 = time.perf_counter()
+        om.forward_logits(ids)
+        el = time.perf_counter() - t0
+        cpu = {"value": W / el, "unit": "sym/s", "cores": cores, "kind": "port",
+               "sample": f"one segment of {W} tokens, fp32 oracle full causal forward, {el:.1f} s"}
+    out = {
+        "metric": f"scored symbols/sec, {a.profile} chunk scoring {B} segments x {W} tokens",
+        "value": round(R / (ms * 1e-3), 1), "unit": "sym/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": a.kv if a.act == a.kv else f"{a.act}-act/{a.kv}-kv", "data": "synthetic",
+        "config": {"workload": f"{a.profile} window scoring: {B} segments x {W} tokens from position 0",
+                   "segments": B, "window": W, "timing": "hip-graph"},
+        "roofline": {"kernel": "whole step (MFMA GEMMs + window attention)", "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": None, "flops": int(flops)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -140,6 +216,9 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--streams", type=int, default=1, choices=[1, 2],
                     help="2: two segment groups on two streams, attention launches alternating")
+    ap.add_argument("--window", type=int, default=1, metavar="W",
+                    help="W > 1: score W-token windows from position 0 (prefill-style "
+                         "chunk scoring, cfg4 = --profile cfg4 --window 2048); value = B*W / step")
     ap.add_argument("--persistent", action="store_true",
                     help="run every slot in one persistent launch (tasks in dependency order)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -158,6 +237,8 @@ def main() -> int:
     import numpy as np
     import torch
 
+    if a.window > 1:
+        return window_bench(a)
     if a.copy_calibration > 0:
         n = a.copy_calibration << 20
         src = torch.ones(n, dtype=torch.uint8, device="cuda")

@@ -128,12 +128,19 @@ int32_t altxs_qgemm_stream(const AltxsQTensor *w, int64_t count, int64_t codes_s
                                  bf16 for the MFMA products (the reference's
                                  tl.dot arithmetic, split_attn.py:86-141);
                                  0 = fp32-faithful (3-part bf16 splits) */
+#define ALTXS_ATTN_ROWS 2     /* bf16 cache, W > 1: one workgroup per row (the
+                                 decode kernel) instead of the window kernel,
+                                 which serves up to 64 rows of a segment per
+                                 K/V read; both give the same bits */
 
 /*
  * Decode attention over a KV cache.  For row r = b*W + t the query sits at
  * position p = pos[b] + t and attends to keys [0, p] of segment b.  Keys are
  * scanned in fixed 64-key tiles (tile T by wave T % waves) and the per-wave
- * partials merged in wave order, so a row's result does not depend on B or W.
+ * partials merged in wave order, so a row's result does not depend on B or W
+ * (windows of a bf16 cache run up to 64 rows per workgroup with the same
+ * per-row arithmetic; prefill_cache/_sdpa_with_past, model.py:679-700,
+ * 1821-1947, is such a window starting at position 0).
  * Replaces run_split_attn (split_attn.py:341-425) and the eager
  * _static_window_attention (model.py:550-585).
  */

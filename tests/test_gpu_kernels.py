@@ -228,6 +228,30 @@ def test_decode_attention_bf16_operands(H, Hkv):
     assert (y32.cpu().double() - ref32).abs().max().item() < 2e-5
 
 
+@pytest.mark.parametrize("H,Hkv,W", [(8, 8, 2), (8, 8, 16), (8, 8, 17), (8, 2, 33), (4, 1, 64),
+                                     (8, 8, 100), (4, 4, 257)])
+def test_window_kernel_bit_identical_to_rows(H, Hkv, W):
+    """The window kernel (up to 64 rows of a segment per K/V read) gives every
+    row the bits of the one-row decode kernel: ragged last blocks, GQA, XSA,
+    the sparse gate, windows starting at 0 (prefill) and ending at max_len."""
+    from altxs_amd import ops
+
+    _log(f"window kernel H={H} Hkv={Hkv} W={W}")
+    B, L = 3, 512
+    gen = torch.Generator().manual_seed(W * 10 + H + Hkv)
+    k = torch.randn(B, Hkv, L, 64, generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn(B, Hkv, L, 64, generator=gen).to(torch.bfloat16).to(DEV)
+    q = (torch.randn(B * W, H, 64, generator=gen) * 3).to(DEV)
+    gate = torch.rand(B * W, H, generator=gen).to(DEV)
+    pos = torch.tensor([0, 61, L - W], dtype=torch.int32, device=DEV)
+    for ob in (False, True):
+        for yb in (False, True):
+            got = ops.decode_attn(q, k, v, pos, W=W, gate=gate, use_xsa=True, ops_bf16=ob, y_bf16=yb)
+            want = ops.decode_attn(q, k, v, pos, W=W, gate=gate, use_xsa=True, ops_bf16=ob, y_bf16=yb,
+                                   rows=True)
+            assert torch.equal(got, want), (ob, yb)
+
+
 def test_decode_attention_window_equals_rows():
     """Row at position p computes the same bits as W=1 and inside a W=4 window."""
     from altxs_amd import ops
