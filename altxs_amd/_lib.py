@@ -47,6 +47,11 @@ EXPORTS = (
     "altxs_step_plan_bytes",
     "altxs_step_plan_build",
     "altxs_step",
+    "altxs_range_init",
+    "altxs_range_encode",
+    "altxs_range_finish",
+    "altxs_range_seed",
+    "altxs_range_decode",
 )
 
 
@@ -160,6 +165,16 @@ def load(path: str | None = None):
     L.altxs_step_plan_build.argtypes = [ctypes.POINTER(StepDesc), p, p, i64, p]
     L.altxs_step.restype = i32
     L.altxs_step.argtypes = [ctypes.POINTER(StepDesc), p]
+    L.altxs_range_init.restype = i32
+    L.altxs_range_init.argtypes = [p, i32, p]
+    L.altxs_range_encode.restype = i32
+    L.altxs_range_encode.argtypes = [p, i32, i32, p, p, i32, p, i64, p]
+    L.altxs_range_finish.restype = i32
+    L.altxs_range_finish.argtypes = [p, i32, p, i64, p]
+    L.altxs_range_seed.restype = i32
+    L.altxs_range_seed.argtypes = [p, i32, p, i64, p, p]
+    L.altxs_range_decode.restype = i32
+    L.altxs_range_decode.argtypes = [p, i32, p, i32, p, i64, p, i64, p]
     v = L.altxs_abi_version()
     if v != ABI_VERSION:
         raise AltxsLibraryError(f"{path}: ABI version {v} != {ABI_VERSION}")
@@ -171,3 +186,10 @@ def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load().altxs_last_error().decode(errors="replace")
         raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+class CoderState(ctypes.Structure):
+    """AltxsCoderState (include/altxs.h): one range-coder stream."""
+    _fields_ = [("low", ctypes.c_uint64), ("high", ctypes.c_uint64), ("pending", ctypes.c_uint64),
+                ("value", ctypes.c_uint64), ("nbits", ctypes.c_int64), ("nbytes", ctypes.c_int64),
+                ("partial", ctypes.c_uint32), ("err", ctypes.c_int32)]

@@ -302,6 +302,52 @@ int32_t altxs_step_plan_build(const AltxsStepDesc *d, void *plan_host, void *pla
  */
 int32_t altxs_step(const AltxsStepDesc *d, altxs_stream_t stream);
 
+/*
+ * Range coder (the 32-bit Witten-Neal-Cleary coder with E3 bits of
+ * arithmetic_coder_lm.py:90-288; replaces GpuRangeCoder, gpu_ac.py:397-479,
+ * and its one-thread kernels 84-218).  One stream per segment, state in device
+ * memory; the tables are the integer CDF rows altxs_step writes (cum[V+1],
+ * total = cum[V]).  Stream b's bytes live at buf + b*stride (MSB-first bits,
+ * the reference's _pack_bits layout); framing (<u64 len><bytes> per segment,
+ * incremental.py:1721-1722) is host work on the returned lengths.
+ */
+typedef struct AltxsCoderState {
+  uint64_t low, high;
+  uint64_t pending;  /* encoder: E3 bits owed */
+  uint64_t value;    /* decoder: code value */
+  int64_t nbits;     /* encoder: bits written; decoder: bits read */
+  int64_t nbytes;    /* after altxs_range_finish: the stream's length; decoder: input length */
+  uint32_t partial;  /* encoder: bits of the unfinished byte */
+  int32_t err;       /* 1: output buffer full, 2: symbol or table invalid */
+} AltxsCoderState;
+
+/* Encoder start state for n streams. */
+int32_t altxs_range_init(AltxsCoderState *st, int32_t n, altxs_stream_t stream);
+
+/* Encode W symbols per stream: stream b codes syms[b*W + t] with table row
+ * b*W + t of cum ([n*W, V+1] uint32), t = 0 .. W-1 in order (a decode row
+ * is W = 1, an encode window W > 1).  Replaces encode_symbol (gpu_ac.py:431). */
+int32_t altxs_range_encode(AltxsCoderState *st, int32_t n, int32_t W, const int32_t *syms,
+                           const uint32_t *cum, int32_t V, uint8_t *buf, int64_t stride,
+                           altxs_stream_t stream);
+
+/* Flush every stream (final bits, last partial byte); st[b].nbytes = length.
+ * Replaces finish (gpu_ac.py:443). */
+int32_t altxs_range_finish(AltxsCoderState *st, int32_t n, uint8_t *buf, int64_t stride,
+                           altxs_stream_t stream);
+
+/* Decoder start: read the first 32 bits of each stream (nbytes[b] = its
+ * length; bits past it read as 0).  Replaces begin_decode (gpu_ac.py:448). */
+int32_t altxs_range_seed(AltxsCoderState *st, int32_t n, const uint8_t *buf, int64_t stride,
+                         const int64_t *nbytes, altxs_stream_t stream);
+
+/* Decode one symbol per stream from table row b of cum ([n, V+1]) and write
+ * it to out[b*out_stride] -- e.g. the next step's token buffer, so decoding
+ * needs no host round trip.  Replaces decode_symbol (gpu_ac.py:466). */
+int32_t altxs_range_decode(AltxsCoderState *st, int32_t n, const uint32_t *cum, int32_t V,
+                           const uint8_t *buf, int64_t stride, int32_t *out, int64_t out_stride,
+                           altxs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,9 @@ def test_bad_arguments_return_errors_without_gpu():
     d.abi_version = 999
     assert L.altxs_step(ctypes.byref(d), None) == -1
     assert b"abi_version" in L.altxs_last_error()
+    assert L.altxs_range_encode(None, 1, 1, None, None, 256, None, 64, None) == -1
+    assert b"altxs_range_encode" in L.altxs_last_error()
+    assert L.altxs_range_decode(None, 1, None, 1, None, 64, None, 1, None) == -1
 
 
 def test_struct_layout_matches_header(tmp_path):
@@ -57,6 +60,8 @@ int main(void) {{
          sizeof(AltxsSlot), sizeof(AltxsStepDesc));
   printf("%zu %zu %zu %zu\\n", offsetof(AltxsStepDesc, layers), offsetof(AltxsStepDesc, emb),
          offsetof(AltxsStepDesc, tokens), offsetof(AltxsStepDesc, err));
+  printf("%zu %zu %zu\\n", sizeof(AltxsCoderState), offsetof(AltxsCoderState, nbytes),
+         offsetof(AltxsCoderState, err));
   return 0;
 }}
 """)
@@ -67,5 +72,6 @@ int main(void) {{
     py = [ctypes.sizeof(_lib.QTensor), ctypes.sizeof(_lib.AttnArgs), ctypes.sizeof(_lib.Layer),
           ctypes.sizeof(_lib.Slot), ctypes.sizeof(_lib.StepDesc),
           _lib.StepDesc.layers.offset, _lib.StepDesc.emb.offset, _lib.StepDesc.tokens.offset,
-          _lib.StepDesc.err.offset]
+          _lib.StepDesc.err.offset, ctypes.sizeof(_lib.CoderState), _lib.CoderState.nbytes.offset,
+          _lib.CoderState.err.offset]
     assert c_sizes == py
