@@ -238,6 +238,66 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_chunk_kernel(const float* __re
   }
 }
 
+// Same tables, one workgroup per row: for launches with many rows (encode
+// windows) the chunk kernel's recount of the counts before each chunk is pure
+// overhead.  Thread t owns elements [t*EPT, t*EPT + EPT); M and S are formed
+// exactly as in cdf_chunk_kernel (same threads, same tiles, same order) and p,
+// the counts and their exact integer prefix sums follow, so every table is
+// bit-identical to the chunk kernel's.
+template <int EPT>
+__global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __restrict__ logits,
+                                                              const float2* __restrict__ stats,
+                                                              int V, float* __restrict__ probs,
+                                                              uint32_t* __restrict__ cum) {
+  static_assert(EPT % 4 == 0, "whole 16-byte vectors per thread");
+  __shared__ float red[CH_WAVES];
+  __shared__ uint32_t wred[CH_WAVES];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int base = t * EPT;
+  const bool mine = base < V;  // V % EPT == 0 (host check)
+  const float* x = logits + row * (int64_t)V;
+  f32x4 v[EPT / 4];
+#pragma unroll
+  for (int k = 0; k < EPT / 4; ++k)
+    v[k] = mine ? __builtin_nontemporal_load((const f32x4*)(x + base) + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+  const int ntile = V / 64;
+  const float2* st = stats + row * (int64_t)ntile;
+  float mt = -INFINITY;
+  for (int i = t; i < ntile; i += CH_THREADS) mt = fmaxf(mt, st[i].x);
+  const float M = block_max_n(mt, red);
+  float sp = 0.f;
+  for (int i = t; i < ntile; i += CH_THREADS) {
+    const float2 q = st[i];
+    sp += q.y * __expf(q.x - M);
+  }
+  const float S = block_sum_n(sp, red);
+  const float iS = 1.f / S;
+  uint32_t f[EPT];
+  uint32_t tot = 0;
+#pragma unroll
+  for (int k = 0; k < EPT / 4; ++k) {
+    f32x4 p;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      p[e] = __expf(v[k][e] - M) * iS;
+      f[4 * k + e] = mine ? scale_count(p[e]) : 0u;
+      tot += f[4 * k + e];
+    }
+    if (probs && mine) *((f32x4*)(probs + row * (int64_t)V + base) + k) = p;
+  }
+  uint32_t run = block_excl_scan(tot, wred);
+  uint32_t* co = cum + row * (int64_t)(V + 1);
+  if (t == 0) co[0] = 0u;
+  if (mine) {
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {  // co + 1 is only 4-byte aligned: scalar stores
+      run += f[k];
+      co[base + k + 1] = run;
+    }
+  }
+}
+
 template <bool FROM_LOGITS>
 hipError_t launch_cdf(const float* in, int64_t rows, int V, int flags, float* probs,
                       uint32_t* cum, hipStream_t s) {
@@ -267,6 +327,19 @@ hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int6
                                   float* probs, uint32_t* cum, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   if (V % 64) return hipErrorInvalidValue;
+  if (rows >= 1024 && V >= 4096 && V <= 16 * CH_THREADS && V % (4 * CH_THREADS) == 0) {
+    // many rows: one workgroup per row (bit-identical tables, no recount)
+    if (V <= 4 * CH_THREADS)
+      hipLaunchKernelGGL(cdf_row_kernel<4>, dim3((unsigned)rows), dim3(CH_THREADS), 0, s, logits,
+                         stats, V, probs, cum);
+    else if (V <= 8 * CH_THREADS)
+      hipLaunchKernelGGL(cdf_row_kernel<8>, dim3((unsigned)rows), dim3(CH_THREADS), 0, s, logits,
+                         stats, V, probs, cum);
+    else
+      hipLaunchKernelGGL(cdf_row_kernel<16>, dim3((unsigned)rows), dim3(CH_THREADS), 0, s, logits,
+                         stats, V, probs, cum);
+    return hipGetLastError();
+  }
   const int chunk = V < 2048 ? V : 2048;
   if (V % chunk) return hipErrorInvalidValue;
   dim3 grid((unsigned)(V / chunk), (unsigned)rows), block(CH_THREADS);

@@ -154,6 +154,36 @@ def test_lora_cdf_bit_identical_decode_encode(act):
     assert np.abs(lg0 - lg1).max() > 1e-3
 
 
+@pytest.mark.parametrize("act", ["bf16", "fp32"])
+def test_long_window_bit_identical_to_rows(act):
+    """A 512-token window per segment (1024 rows: the launch shapes of chunk
+    scoring, e.g. one workgroup per CDF row) gives the logits and tables of
+    512 decode rows."""
+    from altxs_amd.model import StepModel
+
+    _log(f"long window vs rows {act}")
+    sm = _synth("cfg1")
+    B, T = 2, 512
+    toks = np.random.default_rng(5).integers(0, sm.cfg.vocab_size, (B, T))
+    model = StepModel(sm, act=act)
+    st = model.make_static_state(T, win=T, batch=B, want_probs=True)
+    st.token.copy_(torch.from_numpy(toks.astype(np.int32)))
+    model.step(st)
+    lg_w = st.logits.view(B, T, -1).cpu().numpy()
+    cm_w = st.cum.view(B, T, -1).cpu().numpy()
+    pr_w = st.probs.view(B, T, -1).cpu().numpy()
+    st.check_errors()
+    st1 = model.make_static_state(T, win=1, batch=B, want_probs=True)
+    for t in range(T):
+        st1.token.copy_(torch.from_numpy(toks[:, t:t + 1].astype(np.int32)))
+        model.step(st1, commit=True)
+        if t % 64 == 0 or t == T - 1:
+            assert np.array_equal(st1.cum.cpu().numpy(), cm_w[:, t]), t
+            assert np.array_equal(st1.logits.cpu().numpy(), lg_w[:, t]), t
+            assert np.array_equal(st1.probs.cpu().numpy(), pr_w[:, t]), t
+    st1.check_errors()
+
+
 def test_bits_per_symbol_within_tenth_percent():
     from oracle import coder
     from oracle.model_ref import softmax_probs
