@@ -559,4 +559,254 @@ hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect&
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile variant for launches with many rows (encode windows, chunk
+// scoring).  The 16-row tasks above decode every weight block once per 16
+// rows, which makes thousands of row tiles VALU-bound on the code unpacking.
+// Here a workgroup owns BIG_M = 128 rows x BIG_N = 128 columns: the A rows
+// (bf16, already normalised by norm_rows_kernel where the stage has a
+// prologue) pass through LDS one 256-wide k-block at a time, and each wave
+// decodes its two 16-column weight blocks once per k-step and applies them
+// to all eight 16-row blocks.
+//
+// Bit-identical to gemm_task for the same (NB, KS): every 16x16 output block
+// sees the same MFMA sequence (k-steps in order, one group of two k-steps per
+// fp16 scale, acc += scale * t), each K-slice of K/KS starts from zero, the
+// slices are added in slice order, and the epilogue runs on 16 x (16*NB)
+// tiles laid out exactly as gemm_task leaves them in LDS.
+// ---------------------------------------------------------------------------
+constexpr int BIG_M = 128, BIG_N = 128, BIG_AST = 256 + 8;  // A k-block LDS row stride (elements)
+
+template <int NB, int KS>
+__host__ __device__ constexpr size_t big_lds_bytes() {
+  using Cfg = TileCfg<NB, KS>;
+  const size_t a = (size_t)BIG_M * BIG_AST * 2;
+  const size_t c = (size_t)(BIG_M / 16) * (BIG_N / Cfg::NCOL) * 16 * Cfg::CS * 4;
+  return a > c ? a : c;
+}
+
+template <int BITS, int NB, int KS, class Epi>
+// One workgroup per CU: the 8 x 2 accumulator blocks per wave, their K-slice
+// totals and the next k-block's A rows in flight need the whole register file.
+__global__ __launch_bounds__(256, 1) void gemm_big_kernel(QT w, int R, const uint16_t* __restrict__ A,
+                                                          Epi epi) {
+  using Cfg = TileCfg<NB, KS>;
+  static_assert(Cfg::THREADS == 256, "the epilogues run on four waves");
+  constexpr int MB = BIG_M / 16, NSUB = BIG_N / Cfg::NCOL;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  uint16_t* As = (uint16_t*)smem;
+  float* Cs = (float*)smem;  // reused for the output tiles after the K loop
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id.  Here the A
+  // rows are the large operand (the weights of a stage are a few hundred KB),
+  // so every column tile of a row tile goes to one XCD, consecutively: the
+  // 128 rows then enter that XCD's L2 once for all column tiles.
+  int cx = blockIdx.x, ry = blockIdx.y;
+  if (gridDim.y % 8 == 0) {
+    const int bid = blockIdx.x + gridDim.x * blockIdx.y;
+    const int j = bid / 8;
+    ry = bid % 8 + 8 * (j / gridDim.x);
+    cx = j % gridDim.x;
+  }
+  const int m0 = ry * BIG_M, n0 = cx * BIG_N;
+  const int KB = w.K >> 8, KBS = KB / KS;
+  const int nb0 = (n0 >> 4) + 2 * wave;  // this wave's two 16-column weight blocks
+
+  f32x4 acc[MB][2], tot[MB][2];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = tot[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  Blk<BITS, A_BF16, false> wb[2], wn[2];
+  load_w(wb[0], w, nb0, 0, lane);
+  load_w(wb[1], w, nb0 + 1, 0, lane);
+
+  // A rows m0.. of a k-block: 16-byte chunks, 32 per row, 16 per thread; the
+  // next k-block's chunks are loaded into registers while this one computes
+  u32x4 av[16];
+  auto load_a_blk = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int r = c >> 5, k8 = (c & 31) * 8;
+      av[i] = (m0 + r < R) ? *(const u32x4*)(A + (int64_t)(m0 + r) * w.K + kb * 256 + k8)
+                           : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_a_blk = [&]() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      *(u32x4*)(As + (c >> 5) * BIG_AST + (c & 31) * 8) = av[i];
+    }
+  };
+  load_a_blk(0);
+  store_a_blk();
+  __syncthreads();
+
+  for (int kb = 0; kb < KB; ++kb) {
+    if (kb + 1 < KB) {  // next k-block's A rows and weights fly during this one's MFMAs
+      load_a_blk(kb + 1);
+      load_w(wn[0], w, nb0, kb + 1, lane);
+      load_w(wn[1], w, nb0 + 1, kb + 1, lane);
+    }
+    float scale[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      scale[j][0] = half_lo(wb[j].sc[0]); scale[j][1] = half_hi(wb[j].sc[0]);
+      scale[j][2] = half_lo(wb[j].sc[1]); scale[j][3] = half_hi(wb[j].sc[1]);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      bf16x8 bo[2][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+      // the 2*MB independent MFMA chains of the group first, then the scaled
+      // accumulation (the same per-block arithmetic as compute_blk; issuing the
+      // chains back to back keeps the matrix pipe busy instead of waiting on
+      // each chain's result)
+      // all of the group's A operands first (one LDS wait), then the MFMAs
+      u32x4 ar[2][MB];
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          ar[ss][mb] = *(const u32x4*)(As + (mb * 16 + (lane & 15)) * BIG_AST + 64 * g + 32 * ss +
+                                       8 * (lane >> 4));
+      f32x4 t[MB][2];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          t[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ar[0][mb]), bo[j][0],
+                                                             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          t[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ar[1][mb]), bo[j][1],
+                                                             t[mb][j], 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mb][j][i] += scale[j][g] * t[mb][j][i];
+    }
+    {  // (also for KS == 1: the compiler schedules the loop far worse without it)
+      if ((kb + 1) % KBS == 0) {  // end of a K-slice: add it to the slices before (in order)
+        const bool first = kb + 1 == KBS;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tot[mb][j][i] = first ? acc[mb][j][i] : tot[mb][j][i] + acc[mb][j][i];
+            acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+      }
+    }
+    __syncthreads();  // every wave is done with this k-block's A
+    if (kb + 1 < KB) {
+      store_a_blk();
+      __syncthreads();
+      wb[0] = wn[0];
+      wb[1] = wn[1];
+    }
+  }
+  // (the last barrier above also frees As for the output tiles)
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = 32 * wave + 16 * j + (lane & 15);  // column inside the workgroup tile
+      float* C = Cs + (size_t)(mb * NSUB + col / Cfg::NCOL) * 16 * Cfg::CS;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        C[(4 * (lane >> 4) + i) * Cfg::CS + col % Cfg::NCOL] = tot[mb][j][i];
+    }
+  __syncthreads();
+  for (int mb = 0; mb < MB; ++mb) {
+    const int r0 = m0 + 16 * mb;
+    if (r0 >= R) break;  // uniform
+    using P = decltype(epi.template prefetch<Cfg>(0, 0, 0, 0));
+    P pre[NSUB];
+#pragma unroll
+    for (int c = 0; c < NSUB; ++c) pre[c] = epi.template prefetch<Cfg>(r0, n0 + c * Cfg::NCOL, R, 0);
+#pragma unroll
+    for (int c = 0; c < NSUB; ++c)
+      epi.template apply<Cfg>(Cs + (size_t)(mb * NSUB + c) * 16 * Cfg::CS, pre[c], nullptr, r0,
+                              n0 + c * Cfg::NCOL, R, 0);
+  }
+}
+
+template <int BITS, int NB, int KS, class Epi>
+hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& epi, hipStream_t s) {
+  auto kfn = gemm_big_kernel<BITS, NB, KS, Epi>;
+  constexpr size_t lds = big_lds_bytes<NB, KS>();
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  dim3 grid((unsigned)(w.N / BIG_N), (unsigned)((R + BIG_M - 1) / BIG_M));
+  hipLaunchKernelGGL(kfn, grid, dim3(256), lds, s, w, R, A, epi);
+  return hipGetLastError();
+}
+
+// Usable for a tensor when its shape fits the tiling (else use gemm_task).
+inline bool big_gemm_fits(const QT& w) { return w.N % BIG_N == 0 && w.K % 256 == 0; }
+
+// (NB, KS) must be the 16-row path's choice for this tensor (pick_ks).
+template <int NB, int KS, class Epi>
+hipError_t launch_gemm_big(int bits, const QT& w, int R, const uint16_t* A, const Epi& epi,
+                           hipStream_t s) {
+  switch (bits) {
+    case 2: return launch_gemm_big_t<2, NB, KS>(w, R, A, epi, s);
+    case 3: return launch_gemm_big_t<3, NB, KS>(w, R, A, epi, s);
+    case 4: return launch_gemm_big_t<4, NB, KS>(w, R, A, epi, s);
+    case 6: return launch_gemm_big_t<6, NB, KS>(w, R, A, epi, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <class Epi>
+hipError_t launch_gemm_big4(int ks_max, int bits, const QT& w, int R, const uint16_t* A,
+                            const Epi& epi, hipStream_t s) {
+  switch (pick_ks(w.K, ks_max)) {
+    case 4: return launch_gemm_big<1, 4>(bits, w, R, A, epi, s);
+    case 2: return launch_gemm_big<2, 2>(bits, w, R, A, epi, s);
+    default: return launch_gemm_big<4, 1>(bits, w, R, A, epi, s);
+  }
+}
+
+// The prologue of a 16-row task, run on its own: rows [16*blockIdx.x, +16)
+// normalised exactly as gemm_task stages them (and the same side outputs,
+// e.g. sparse-gate logits), stored as bf16 rows of K for gemm_big_kernel.
+template <class Pro>
+__global__ __launch_bounds__(256) void norm_rows_kernel(Pro pro, int R, int K, uint16_t* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int m0 = blockIdx.x * 16;
+  pro.template stage<A_BF16, 256>(smem, smem + (size_t)16 * lds_stride(K, A_BF16) * 2, m0, R, K, 0, true);
+  __syncthreads();
+  const uint16_t* As = (const uint16_t*)smem;
+  const int n8 = K / 8;
+  for (int c = threadIdx.x; c < 16 * n8; c += 256) {
+    const int r = c / n8, k8 = (c % n8) * 8;
+    if (m0 + r < R) *(u32x4*)(out + (int64_t)(m0 + r) * K + k8) = *(const u32x4*)(As + r * lds_stride(K, A_BF16) + k8);
+  }
+}
+
+template <class Pro>
+hipError_t launch_norm_rows(const Pro& pro, int R, int K, uint16_t* out, hipStream_t s) {
+  const size_t lds = (size_t)16 * lds_stride(K, A_BF16) * 2 + Pro::kScratch;
+  hipLaunchKernelGGL(norm_rows_kernel<Pro>, dim3((unsigned)((R + 15) / 16)), dim3(256), lds, s, pro, R,
+                     K, out);
+  return hipGetLastError();
+}
+
 }  // namespace altxs

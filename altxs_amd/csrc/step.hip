@@ -42,6 +42,9 @@ int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 // LM head: workgroups per 16-row tile (0 = one per 64-column tile).
 constexpr int kLmHeadColWgs = 0;
+// Launches with at least this many rows use the 128 x 128 tile GEMMs
+// (gemm_big_kernel, bit-identical to the 16-row tasks); bf16 activations only.
+constexpr int kBigRows = 2048;
 // Preferred K-splits of the 4-wave GEMM stages (QKV and the LM head use
 // (NB, KS) = (4, 1): one 64-column head tile per task).
 constexpr int kKsO = 2, kKsUp = 2, kKsDown = 4;
@@ -279,8 +282,18 @@ struct StepRun {
       epi.lora_s = S.lora_scale; epi.rank = d->lora_rank;
     }
     epi.D = d->D; epi.a_f32 = AM == A_F32 ? 1 : 0;
+    if (big(R, L.qkv) && !S.lora_q_a) {  // normalised rows in Y (free until the attention)
+      hipError_t e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st);
+      if (e != hipSuccess) return e;
+      return launch_gemm_big<4, 1>(L.qkv.bits, qt_of(L.qkv), R, (const uint16_t*)w.Y, epi, st);
+    }
     return launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
                                       pro, epi, 0, st);
+  }
+
+  // The large-tile GEMMs apply (bf16 activations, many rows, a tileable shape).
+  bool big(int R, const AltxsQTensor& t) const {
+    return AM == A_BF16 && R >= kBigRows && big_gemm_fits(qt_of(t));
   }
 
   char* slot_kv(const Group& G, int s) const {
@@ -323,16 +336,22 @@ struct StepRun {
     hipError_t e;
     {  // out-projection + attention residual
       EpiO epi{base_s, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
-      if ((e = launch_gemm4<AM>(kKsO, L.o.bits, qt_of(L.o), R, ADirect{w.Y, 0}, ProNone{}, epi, 0,
-                                st)) != hipSuccess)
-        return e;
+      if (big(R, L.o))
+        e = launch_gemm_big4(kKsO, L.o.bits, qt_of(L.o), R, (const uint16_t*)w.Y, epi, st);
+      else
+        e = launch_gemm4<AM>(kKsO, L.o.bits, qt_of(L.o), R, ADirect{w.Y, 0}, ProNone{}, epi, 0, st);
+      if (e != hipSuccess) return e;
     }
     {  // MLP up + LeakyReLU(0.5)^2
       ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       EpiUp epi{w.HB, d->F, hb16};
-      if ((e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0,
-                                st)) != hipSuccess)
-        return e;
+      if (big(R, L.up)) {  // normalised rows in Y (the out-projection has read it)
+        if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
+        e = launch_gemm_big4(kKsUp, L.up.bits, qt_of(L.up), R, (const uint16_t*)w.Y, epi, st);
+      } else {
+        e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0, st);
+      }
+      if (e != hipSuccess) return e;
     }
     {  // MLP down + residual / lanes
       EpiDown epi;
@@ -355,9 +374,12 @@ struct StepRun {
         nx.parallel = par1 ? 1 : 0;
         nx.skip_self = S1.skip_src == s ? 1 : 0;
       }
-      if ((e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
-                                epi, 0, st)) != hipSuccess)
-        return e;
+      if (big(R, L.down))
+        e = launch_gemm_big4(kKsDown, L.down.bits, qt_of(L.down), R, (const uint16_t*)w.HB, epi, st);
+      else
+        e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
+                             epi, 0, st);
+      if (e != hipSuccess) return e;
     }
     return hipSuccess;
   }
@@ -375,9 +397,14 @@ struct StepRun {
       ProNorm pro{xf, fm == 1 ? w.X1 + n * Rp * D : nullptr, fm == 1 ? 1 : 0, 1.0f, d->norm_eps, d->D};
       EpiLogits epi{G.logits, fast_cdf ? w.STATS : nullptr, d->V,
                     (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap, d->softcap_pn};
-      if ((e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0},
-                                          pro, epi, kLmHeadColWgs, st)) != hipSuccess)
-        return e;
+      if (big(R, d->emb)) {
+        if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
+        e = launch_gemm_big<4, 1>(d->emb.bits, qt_of(d->emb), R, (const uint16_t*)w.Y, epi, st);
+      } else {
+        e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0},
+                                       pro, epi, kLmHeadColWgs, st);
+      }
+      if (e != hipSuccess) return e;
     }
     if (G.probs || G.cum) {
       if (fast_cdf && G.cum) {

@@ -156,14 +156,14 @@ def test_lora_cdf_bit_identical_decode_encode(act):
 
 @pytest.mark.parametrize("act", ["bf16", "fp32"])
 def test_long_window_bit_identical_to_rows(act):
-    """A 512-token window per segment (1024 rows: the launch shapes of chunk
-    scoring, e.g. one workgroup per CDF row) gives the logits and tables of
-    512 decode rows."""
+    """A 512-token window per segment (2048 rows: the launch shapes of chunk
+    scoring -- 128 x 128 GEMM tiles, one workgroup per CDF row) gives the
+    logits and tables of 512 decode rows."""
     from altxs_amd.model import StepModel
 
     _log(f"long window vs rows {act}")
     sm = _synth("cfg1")
-    B, T = 2, 512
+    B, T = 4, 512
     toks = np.random.default_rng(5).integers(0, sm.cfg.vocab_size, (B, T))
     model = StepModel(sm, act=act)
     st = model.make_static_state(T, win=T, batch=B, want_probs=True)
