@@ -203,6 +203,86 @@ def window_bench(a) -> int:
     return 0
 
 
+def coder_bench(a) -> int:
+    """--coder: the closed loop of compression on the cfg3 decode workload.
+    Compress = step + the range coder encoding each segment's next symbol with
+    the step's integer CDF; decompress = step + the decoder writing the decoded
+    symbol into the token buffer the next step reads (no host round trip).
+    Each is timed over K steps captured in one HIP graph; the coder kernels
+    alone are timed the same way (latency-bound: one lane per stream to
+    encode, one wave per stream to decode)."""
+    import numpy as np
+    import torch
+
+    from altxs_amd import synth
+    from altxs_amd.coder import RangeCoder
+    from altxs_amd.config import make_config
+    from altxs_amd.model import StepModel
+
+    B, ctx = a.segments, a.ctx
+    max_len = (ctx + 255) // 256 * 256
+    cfg = make_config(a.profile)
+    sm = synth.make_model(cfg)
+    model = StepModel(sm, act=a.act, kv=a.kv)
+    st = model.make_static_state(max_len, win=1, batch=B, want_probs=False, want_cdf=True)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    st.kv.normal_(generator=g)
+    st.pos.fill_(ctx - 1)
+    toks = torch.from_numpy(synth.zipf_tokens(cfg.vocab_size, (B, 1)).astype(np.int32)).cuda()
+    st.token.copy_(toks)
+    nxt = torch.from_numpy(synth.zipf_tokens(cfg.vocab_size, (B, 1), seed=7).astype(np.int32)).cuda()
+    K = a.steps
+    enc = RangeCoder(B, 64 + 8 * (K + a.warmup + 8))
+    dec = RangeCoder(B, 64 + 8 * (K + a.warmup + 8))
+    model.step(st)
+    torch.cuda.synchronize()
+    dec.begin_decode([bytes(16)] * B)
+
+    def timed(body) -> float:
+        for _ in range(a.warmup):
+            body()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(K):
+                body()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / K
+
+    step_ms = timed(lambda: model.step(st))
+    enc_ms = timed(lambda: enc.encode(st.cum, nxt))
+    dec_ms = timed(lambda: dec.decode(st.cum, st.token))
+    comp_ms = timed(lambda: (model.step(st), enc.encode(st.cum, nxt)))
+    dec.begin_decode([bytes(16)] * B)
+    decomp_ms = timed(lambda: (model.step(st), dec.decode(st.cum, st.token)))
+    st.check_errors()
+    enc.check()
+    dec.check()
+    log(f"step {step_ms * 1e3:.1f} us; encode {enc_ms * 1e3:.2f} us, decode {dec_ms * 1e3:.2f} us "
+        f"per call ({B} streams); compress {comp_ms * 1e3:.1f} us/step, decompress "
+        f"{decomp_ms * 1e3:.1f} us/step")
+    out = {
+        "metric": f"compressed symbols/sec, {a.profile} decode step + GPU range coder, {B} segments "
+                  f"ctx{ctx}",
+        "value": round(B / (comp_ms * 1e-3), 1), "unit": "sym/s", "n_gpus": 1, "steps": K,
+        "warmup": a.warmup, "ms_per_step": round(comp_ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": a.kv, "data": "synthetic",
+        "config": {"workload": f"{a.profile} compress: step + encode of one symbol per segment",
+                   "segments": B, "ctx": ctx, "timing": "hip-graph"},
+        "decompress": {"value": round(B / (decomp_ms * 1e-3), 1), "unit": "sym/s",
+                       "ms_per_step": round(decomp_ms, 4)},
+        "coder_us_per_call": {"encode": round(enc_ms * 1e3, 2), "decode": round(dec_ms * 1e3, 2),
+                              "step_alone": round(step_ms * 1e3, 1)},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,6 +299,9 @@ def main() -> int:
     ap.add_argument("--window", type=int, default=1, metavar="W",
                     help="W > 1: score W-token windows from position 0 (prefill-style "
                          "chunk scoring, cfg4 = --profile cfg4 --window 2048); value = B*W / step")
+    ap.add_argument("--coder", action="store_true",
+                    help="time compression (step + GPU range coder encode) and decompression "
+                         "(step + decode into the next step's token buffer) instead")
     ap.add_argument("--persistent", action="store_true",
                     help="run every slot in one persistent launch (tasks in dependency order)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -239,6 +322,8 @@ def main() -> int:
 
     if a.window > 1:
         return window_bench(a)
+    if a.coder:
+        return coder_bench(a)
     if a.copy_calibration > 0:
         n = a.copy_calibration << 20
         src = torch.ones(n, dtype=torch.uint8, device="cuda")
