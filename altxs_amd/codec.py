@@ -21,6 +21,11 @@ Device layout (``pack_tiled``), consumed by libaltxs_hip's MFMA GEMM:
   ``8*s + i`` at bit ``pb * (8*s + i)``) in ``8*pb`` bytes, lanes contiguous,
   so a block is ``512*b`` bytes and each lane's share is whole 16/8-byte words;
 * scales per block: 16 rows x 4 groups fp16, row-major (128 bytes).
+
+Dense weights (``bits = 16``, e.g. the reference's runtime banks, which are
+Init(seed) + the decoded delta in bf16) use the same block and lane order
+with each value stored as its bf16 bits (lane ``l``: 64 values, k-step ``s``
+in bytes 16s..16s+15), 8192 bytes per block and no scales.
 """
 
 from __future__ import annotations
@@ -124,6 +129,31 @@ def pack_tiled(codes: np.ndarray, scales: np.ndarray, bits: int) -> tuple[np.nda
     return packed, sc
 
 
+def bf16_bits(w: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns (uint16), round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(w, dtype=np.float32).view(np.uint32)
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)
+    nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    return np.where(nan, (u >> np.uint32(16)) | np.uint32(0x40), r).astype(np.uint16)
+
+
+def pack_dense_tiled(w: np.ndarray) -> np.ndarray:
+    """fp32 [N, K] -> the dense bf16 tiled bytes (module docstring)."""
+    n, k = w.shape
+    if n % BLOCK_N or k % BLOCK_K:
+        raise ValueError(f"tensor [{n}, {k}] must be a multiple of [{BLOCK_N}, {BLOCK_K}]")
+    vals = bf16_bits(w).reshape(-1)[_lane_order(n, k)]  # [blk, lane, 64]
+    return np.ascontiguousarray(vals).astype("<u2").view(np.uint8).reshape(-1)
+
+
+def unpack_dense_tiled(packed: np.ndarray, n: int, k: int) -> np.ndarray:
+    """Inverse of :func:`pack_dense_tiled`: fp32 [N, K] of the bf16 values."""
+    vals = np.ascontiguousarray(packed, dtype=np.uint8).view("<u2").astype(np.uint32)
+    out = np.zeros(n * k, dtype=np.uint32)
+    out[_lane_order(n, k).reshape(-1)] = vals
+    return (out << np.uint32(16)).view(np.float32).reshape(n, k)
+
+
 def unpack_tiled(packed: np.ndarray, scales_t: np.ndarray, n: int, k: int,
                  bits: int) -> tuple[np.ndarray, np.ndarray]:
     """Inverse of :func:`pack_tiled`."""
@@ -167,10 +197,16 @@ class PackedTensor:
         return int(self.tiled_scales.size * 2)
 
     def dense(self) -> np.ndarray:
+        if self.bits == 16:  # codes hold the bf16 bit patterns
+            return (self.codes.astype(np.uint32) << np.uint32(16)).view(np.float32)
         return dequantize_group64(self.codes, self.scales, self.bits)
 
     @classmethod
     def from_dense(cls, name: str, w: np.ndarray, bits: int) -> "PackedTensor":
+        if bits == 16:  # dense bf16 weights, no quantisation
+            n = w.shape[0]
+            return cls(name, 16, bf16_bits(w), np.zeros((n, 0), np.float16), pack_dense_tiled(w),
+                       np.zeros(0, np.float16))
         codes, scales = quantize_group64(w, bits)
         tiled, tsc = pack_tiled(codes, scales, bits)
         return cls(name, bits, codes, scales, tiled, tsc)

@@ -47,6 +47,9 @@ template <> struct Planes<2> { static constexpr int P0 = 2, P1 = 0; };
 template <> struct Planes<3> { static constexpr int P0 = 2, P1 = 1; };
 template <> struct Planes<4> { static constexpr int P0 = 4, P1 = 0; };
 template <> struct Planes<6> { static constexpr int P0 = 4, P1 = 2; };
+// BITS == 16: dense bf16 weights in the same tiled order (no codes, no scales):
+// a lane's 64 values of a block are 32 words, k-step s in words 4s..4s+3.
+template <> struct Planes<16> { static constexpr int P0 = 16, P1 = 0; };
 
 // A-operand modes
 enum AMode : int { A_F32 = 0, A_BF16 = 1, A_F16 = 2 };
@@ -146,6 +149,8 @@ __device__ __forceinline__ float code_center(int bits) {
 // (planes_to6 already applied).
 template <int BITS>
 __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
+  if constexpr (BITS == 16)
+    return __builtin_bit_cast(bf16x8, u32x4{p0[4 * s], p0[4 * s + 1], p0[4 * s + 2], p0[4 * s + 3]});
   const float center = code_center<BITS>(bits);
   uint32_t c[8];
   codes_step<BITS == 0 ? 6 : BITS>(p0, p1, s, c);
@@ -157,6 +162,7 @@ __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* 
 
 template <int BITS>
 __device__ __forceinline__ f16x8 b_op_f16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
+  static_assert(BITS != 16, "dense bf16 weights take bf16 or fp32 activations");
   const float center = code_center<BITS>(bits);
   uint32_t c[8];
   codes_step<BITS == 0 ? 6 : BITS>(p0, p1, s, c);
@@ -210,6 +216,15 @@ __device__ __forceinline__ void load_w(Blk<BITS, AM, ADIRECT>& b, const QT& w, i
     for (int i = 0; i < 4; ++i) { b.p0[i] = x[i]; b.p0[4 + i] = y[i]; b.p1[i] = z[i]; }
     const u32x2 sv = *(const u32x2*)(w.scales + bi * 64 + (lane & 15) * 4);
     b.sc[0] = sv[0]; b.sc[1] = sv[1];
+  } else if constexpr (BITS == 16) {
+    const u32x4* a0 = (const u32x4*)(w.codes + bi * (512 * 16)) + lane * 8;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const u32x4 x = a0[v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b.p0[4 * v + i] = x[i];
+    }
+    b.sc[0] = b.sc[1] = 0u;
   } else {
     constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
     const uint8_t* blk = w.codes + bi * (512 * BITS);
@@ -303,7 +318,8 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8& a0, bf16x8& 
 template <int BITS, int AM, bool ADIRECT>
 __device__ __forceinline__ void compute_blk(const Blk<BITS, AM, ADIRECT>& b, const void* As, int K,
                                             int kb, int lane, f32x4& acc, int bits = BITS) {
-  const float scale[4] = {half_lo(b.sc[0]), half_hi(b.sc[0]), half_lo(b.sc[1]), half_hi(b.sc[1])};
+  float scale[4] = {half_lo(b.sc[0]), half_hi(b.sc[0]), half_lo(b.sc[1]), half_hi(b.sc[1])};
+  if constexpr (BITS == 16) scale[0] = scale[1] = scale[2] = scale[3] = 1.f;  // dense: acc += t
   const int row = lane & 15;
   constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
   uint32_t q0[2 * P0], q1[P1 > 0 ? 2 * P1 : 1];
@@ -541,6 +557,10 @@ hipError_t launch_gemm_bits(int bits, const QT& w, int R, int batch, int64_t cod
     case 3: return launch_gemm<3, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
     case 4: return launch_gemm<4, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
     case 6: return launch_gemm<6, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+    case 16:
+      if constexpr (AM != A_F16)
+        return launch_gemm<16, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -762,7 +782,7 @@ hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& e
 }
 
 // Usable for a tensor when its shape fits the tiling (else use gemm_task).
-inline bool big_gemm_fits(const QT& w) { return w.N % BIG_N == 0 && w.K % 256 == 0; }
+inline bool big_gemm_fits(const QT& w) { return w.bits <= 6 && w.N % BIG_N == 0 && w.K % 256 == 0; }
 
 // (NB, KS) must be the 16-row path's choice for this tensor (pick_ks).
 template <int NB, int KS, class Epi>

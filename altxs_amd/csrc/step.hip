@@ -117,10 +117,11 @@ QT qt_of(const AltxsQTensor& t) {
 }
 
 int check_tensor(const AltxsQTensor& t, int64_t N, int64_t K, const char* what, int li) {
-  ALTXS_REQUIRE(t.codes && t.scales, "altxs_step: layer %d %s: null tensor", li, what);
+  const bool dense = t.bits == 16;  // bf16 values in the tiled order, no scales
+  ALTXS_REQUIRE(t.codes && (dense || t.scales), "altxs_step: layer %d %s: null tensor", li, what);
   ALTXS_REQUIRE(t.N == N && t.K == K, "altxs_step: layer %d %s: shape [%lld,%lld] != [%lld,%lld]",
                 li, what, (long long)t.N, (long long)t.K, (long long)N, (long long)K);
-  ALTXS_REQUIRE(t.bits == 2 || t.bits == 3 || t.bits == 4 || t.bits == 6,
+  ALTXS_REQUIRE(t.bits == 2 || t.bits == 3 || t.bits == 4 || t.bits == 6 || dense,
                 "altxs_step: layer %d %s: bits=%d", li, what, t.bits);
   ALTXS_REQUIRE(((uintptr_t)t.codes & 15) == 0 && ((uintptr_t)t.scales & 7) == 0,
                 "altxs_step: layer %d %s: misaligned", li, what);
@@ -428,6 +429,10 @@ struct StepRun {
 // ---- persistent layer kernel -------------------------------------------------
 
 bool persist_ok(const AltxsStepDesc* d) {
+  for (int l = 0; l < d->n_layers; ++l) {  // the layer kernel decodes packed widths only
+    const AltxsLayer& L = d->layers[l];
+    if (L.qkv.bits > 6 || L.o.bits > 6 || L.up.bits > 6 || L.down.bits > 6) return false;
+  }
   return d->kv_bf16 && 16 % d->W == 0 && !split_mode(d);
 }
 int64_t plan_slots_off() { return align_up((int64_t)sizeof(PersistArgs), 256); }

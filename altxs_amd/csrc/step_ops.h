@@ -58,8 +58,24 @@ __device__ void dequant_run(const QT& w, int n, int run, float (&out)[8]) {
   for (int i = 0; i < 8; ++i) out[i] = ((float)c[i] - center) * sc;
 }
 
+// Dense bf16 rows (bits 16): the 8 values of run `run` of row n, one 16-byte load.
+__device__ void dense_run(const QT& w, int n, int run, float (&out)[8]) {
+  const int KB = w.K >> 8;
+  const int k0 = 8 * run, kb = k0 >> 8, kk = k0 & 255;
+  const int s = kk >> 5, lg = (kk & 31) >> 3;
+  const int L = (n & 15) + 16 * lg;
+  const size_t bi = (size_t)(n >> 4) * KB + kb;
+  const u32x4 x = *((const u32x4*)(w.codes + bi * (512 * 16)) + L * 8 + s);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = bf16_lo(x[i]);
+    out[2 * i + 1] = bf16_hi(x[i]);
+  }
+}
+
 __device__ void dequant_run_bits(int bits, const QT& w, int n, int run, float (&out)[8]) {
   switch (bits) {
+    case 16: dense_run(w, n, run, out); break;
     case 2: dequant_run<2>(w, n, run, out); break;
     case 3: dequant_run<3>(w, n, run, out); break;
     case 4: dequant_run<4>(w, n, run, out); break;

@@ -91,12 +91,17 @@ class SynthModel:
 
 
 def make_model(cfg: AltxsConfig, *, seed: int = WEIGHT_SEED, std: float = 0.02,
-               softcap: tuple[float, float] | None = None) -> SynthModel:
+               softcap: tuple[float, float] | None = None, dense: bool = False) -> SynthModel:
+    """``dense``: every matrix kept as bf16 (the reference's runtime banks)
+    instead of the mixed-bit packing."""
     cfg.validate()
     rng = np.random.default_rng(seed)
     d, kvd, f = cfg.model_dim, cfg.kv_dim, cfg.hidden_dim
     names = tensor_list(cfg)
-    bits = allocate_bits([(nm, nn * kk) for nm, nn, kk in names], cfg.bpw_target)
+    if dense:
+        bits = {nm: 16 for nm, _, _ in names}
+    else:
+        bits = allocate_bits([(nm, nn * kk) for nm, nn, kk in names], cfg.bpw_target)
     packed = {}
     for nm, nn, kk in names:
         w = rng.standard_normal((nn, kk), dtype=np.float32) * np.float32(std)

@@ -146,3 +146,31 @@ def test_kv_tile_layout_roundtrip_and_operand_runs():
                     run = tv[1, 2, T, 8 * (64 * (4 * s + nb) + lane):][:8]
                     keys = [64 * T + 16 * (2 * s + j // 4) + 4 * g + j % 4 for j in range(8)]
                     assert np.array_equal(run, x[1, 2, keys, 16 * nb + c])
+
+
+def test_dense_bf16_tiled_layout():
+    """Dense bf16 weights: each value at the byte offset the layout states
+    (block (n//16, k//256), lane n%16 + 16*((k%32)//8), k-step (k%256)//32,
+    element k%8), as its round-to-nearest-even bf16 bits."""
+    import torch
+
+    from altxs_amd import codec
+
+    rng = np.random.default_rng(3)
+    n, k = 48, 768
+    w = (rng.standard_normal((n, k)) * 3).astype(np.float32)
+    w[0, :4] = [0.0, -0.0, 1e-40, 65504.0]
+    t = codec.pack_dense_tiled(w)
+    assert t.size == n * k * 2
+    want = torch.from_numpy(w).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    rows, cols = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
+    blk = (rows // 16) * (k // 256) + cols // 256
+    kk = cols % 256
+    lane = rows % 16 + 16 * ((kk % 32) // 8)
+    off = blk * 8192 + lane * 128 + (kk // 32) * 16 + (kk % 8) * 2
+    got = t[off].astype(np.uint16) | (t[off + 1].astype(np.uint16) << 8)
+    assert np.array_equal(got, want)
+    assert np.array_equal(codec.unpack_dense_tiled(t, n, k),
+                          torch.from_numpy(w).to(torch.bfloat16).float().numpy())
+    p = codec.PackedTensor.from_dense("w", w, 16)
+    assert p.bits == 16 and p.nbytes_scales == 0 and np.array_equal(p.dense(), codec.unpack_dense_tiled(t, n, k))

@@ -32,6 +32,10 @@ CASES = {
 }
 LORA = {"tiny_lora": ("tiny", dict(lora_rank=8, lora_alpha=12.0)),
         "cfg1_lora": ("cfg1", dict(lora_rank=16, lora_alpha=16.0))}
+# dense bf16 weights (bits 16: the reference's runtime banks); "large" is the
+# reference's default student (17 slots with loops, GQA, parallel lanes, V=256)
+CASES.update({"tiny_dense": (3, 12, 0.08, (2.0, 1.5)), "large_dense": (2, 10, 0.02, (30.0, 24.0))})
+DENSE = {"tiny_dense": "tiny", "large_dense": "large"}
 _MODELS: dict = {}
 
 
@@ -45,9 +49,9 @@ def _synth(profile):
         from altxs_amd.config import make_config
 
         B, T, std, cap = CASES[profile]
-        base, over = LORA.get(profile, (profile, {}))
+        base, over = LORA.get(profile, (DENSE.get(profile, profile), {}))
         cfg = make_config(base, **over)
-        _MODELS[profile] = synth.make_model(cfg, std=std, softcap=cap)
+        _MODELS[profile] = synth.make_model(cfg, std=std, softcap=cap, dense=profile in DENSE)
     return _MODELS[profile]
 
 
@@ -94,7 +98,8 @@ def _gpu_decode(profile, act, B=None, W=1, kv=None):
     return torch.cat(lg, 1).numpy(), torch.cat(cm, 1).numpy().astype(np.int64), model, st
 
 
-@pytest.mark.parametrize("profile", ["tiny", "cfg1", "tiny_lora", "cfg1_lora"])
+@pytest.mark.parametrize("profile", ["tiny", "cfg1", "tiny_lora", "cfg1_lora", "tiny_dense",
+                                     "large_dense"])
 def test_step_fp32_matches_oracle(profile):
     _log(f"step fp32 {profile}")
     got, _, _, _ = _gpu_decode(profile, "fp32")
@@ -113,7 +118,9 @@ def test_step_fp32_act_bf16_kv_meets_tolerance():
 
 
 @pytest.mark.parametrize("profile,mean_tol,max_tol", [("tiny", 3e-3, 6e-2), ("cfg1", 5e-4, 1e-2),
-                                                      ("cfg1_lora", 5e-4, 1e-2)])
+                                                      ("cfg1_lora", 5e-4, 1e-2),
+                                                      ("tiny_dense", 3e-3, 6e-2),
+                                                      ("large_dense", 5e-4, 1e-2)])
 def test_step_bf16_matches_oracle_emulation(profile, mean_tol, max_tol):
     _log(f"step bf16 {profile}")
     got, _, _, _ = _gpu_decode(profile, "bf16")
@@ -152,6 +159,20 @@ def test_lora_cdf_bit_identical_decode_encode(act):
     # and the adapters change the result (the test would pass vacuously otherwise)
     lg0, _, _, _ = _gpu_decode("tiny", act, W=1)
     assert np.abs(lg0 - lg1).max() > 1e-3
+
+
+@pytest.mark.parametrize("act", ["fp32", "bf16"])
+def test_dense_cdf_bit_identical_decode_encode(act):
+    """Dense bf16 weights on the student profile: decode rows, windows and a
+    smaller batch give the same tables."""
+    profile = "large_dense"
+    _log(f"dense lockstep {act}")
+    lg1, cm1, _, _ = _gpu_decode(profile, act, W=1)
+    lg5, cm5, _, _ = _gpu_decode(profile, act, W=5)
+    assert np.array_equal(cm1, cm5)
+    assert np.array_equal(lg1, lg5)
+    _, cmb, _, _ = _gpu_decode(profile, act, B=1, W=1)
+    assert np.array_equal(cmb[0], cm1[0])
 
 
 @pytest.mark.parametrize("act", ["bf16", "fp32"])
