@@ -52,6 +52,8 @@ EXPORTS = (
     "altxs_range_finish",
     "altxs_range_seed",
     "altxs_range_decode",
+    "altxs_codec_decode",
+    "altxs_pack_dense",
 )
 
 
@@ -175,6 +177,10 @@ def load(path: str | None = None):
     L.altxs_range_seed.argtypes = [p, i32, p, i64, p, p]
     L.altxs_range_decode.restype = i32
     L.altxs_range_decode.argtypes = [p, i32, p, i32, p, i64, p, i64, p]
+    L.altxs_codec_decode.restype = i32
+    L.altxs_codec_decode.argtypes = [ctypes.POINTER(CodecGroups), p, p, i64, i64, p, i64, i64, p, p]
+    L.altxs_pack_dense.restype = i32
+    L.altxs_pack_dense.argtypes = [p, p, i64, i64, i64, p, p]
     v = L.altxs_abi_version()
     if v != ABI_VERSION:
         raise AltxsLibraryError(f"{path}: ABI version {v} != {ABI_VERSION}")
@@ -193,3 +199,13 @@ class CoderState(ctypes.Structure):
     _fields_ = [("low", ctypes.c_uint64), ("high", ctypes.c_uint64), ("pending", ctypes.c_uint64),
                 ("value", ctypes.c_uint64), ("nbits", ctypes.c_int64), ("nbytes", ctypes.c_int64),
                 ("partial", ctypes.c_uint32), ("err", ctypes.c_int32)]
+
+
+CODEBOOK_MODES = {"lloyd": 0, "symmetric": 1, "shared": 2, "fp4": 3, "hybrid_fp4_symmetric": 4}
+
+
+class CodecGroups(ctypes.Structure):
+    """AltxsCodecGroups (include/altxs.h): the three width groups of one bank."""
+    _fields_ = [("packed", ctypes.c_void_p * 3), ("codebook", ctypes.c_void_p * 3),
+                ("shared", ctypes.c_void_p * 3), ("n_codes", ctypes.c_int64 * 3),
+                ("n_book", ctypes.c_int64 * 3), ("mode", ctypes.c_int32), ("reserved", ctypes.c_int32)]

@@ -181,12 +181,13 @@ class PackedTensor:
     bits: int
     codes: np.ndarray   # uint8 [N, K]
     scales: np.ndarray  # fp16 [N, K//64]
-    tiled: np.ndarray   # uint8 bytes
+    tiled: np.ndarray   # uint8 bytes (or a device tensor built there, see altxs_amd.shipped)
     tiled_scales: np.ndarray  # fp16
+    nk: tuple[int, int] | None = None  # the shape when `codes` is not kept on the host
 
     @property
     def shape(self) -> tuple[int, int]:
-        return tuple(self.codes.shape)  # type: ignore[return-value]
+        return self.nk if self.nk is not None else tuple(self.codes.shape)  # type: ignore[return-value]
 
     @property
     def nbytes_codes(self) -> int:

@@ -167,7 +167,10 @@ class StepModel:
         self._keep: list[torch.Tensor] = []
         self.qt: dict[str, _lib.QTensor] = {}
         for name, p in synth.packed.items():
-            codes = torch.from_numpy(np.ascontiguousarray(p.tiled)).to(dev)
+            if isinstance(p.tiled, torch.Tensor):  # tiles built on the device (shipped codec)
+                codes = p.tiled.to(dev)
+            else:
+                codes = torch.from_numpy(np.ascontiguousarray(p.tiled)).to(dev)
             scales = torch.from_numpy(np.ascontiguousarray(p.tiled_scales).view(np.int16)).to(dev)
             self._keep += [codes, scales]
             n, k = p.shape

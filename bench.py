@@ -299,6 +299,9 @@ def main() -> int:
     ap.add_argument("--window", type=int, default=1, metavar="W",
                     help="W > 1: score W-token windows from position 0 (prefill-style "
                          "chunk scoring, cfg4 = --profile cfg4 --window 2048); value = B*W / step")
+    ap.add_argument("--dense", action="store_true",
+                    help="dense bf16 weights (bits 16, the reference's runtime banks) instead of "
+                         "the mixed-bit packing")
     ap.add_argument("--coder", action="store_true",
                     help="time compression (step + GPU range coder encode) and decompression "
                          "(step + decode into the next step's token buffer) instead")
@@ -342,7 +345,7 @@ def main() -> int:
     max_len = (ctx + 255) // 256 * 256
     cfg = make_config(a.profile)
     t0 = time.time()
-    sm = synth.make_model(cfg)
+    sm = synth.make_model(cfg, dense=a.dense)
     log(f"model {a.profile}: {sm.bits_summary()['bpw']:.4f} bpw, built in {time.time() - t0:.1f}s")
     model = StepModel(sm, act=a.act, kv=a.kv)
     st = model.make_static_state(max_len, win=1, batch=B, want_probs=False, want_cdf=True,
@@ -469,8 +472,9 @@ def main() -> int:
             "workload": (f"{a.profile} decode step: {B} segments x 1 symbol, ctx {ctx}, "
                          f"{cfg.num_layers} layers d={cfg.model_dim} H={cfg.num_heads} "
                          f"FFN={cfg.hidden_dim} V={cfg.vocab_size}, "
-                         f"{sm.bits_summary()['bpw']:.3f} bpw group-64 weights, "
-                         f"{a.act} activations, {a.kv} KV"),
+                         + ("dense bf16 weights, " if a.dense else
+                            f"{sm.bits_summary()['bpw']:.3f} bpw group-64 weights, ")
+                         + f"{a.act} activations, {a.kv} KV"),
             "segments": B, "ctx": ctx, "timing": "hip-graph" if graph is not None else "eager",
             "streams": groups, "persistent": bool(a.persistent),
             "eager_ms_per_step": round(eager_ms, 4), "kernel_event_timing": event_timing,
@@ -484,7 +488,8 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             # measured for the default workload only (cfg3, 64 segments, ctx 2048)
             "traffic": (read_traffic("layers" if a.persistent else "attn")
-                        if (a.profile, B, ctx, a.act, a.kv) == ("cfg3", 64, 2048, "bf16", "bf16") else None),
+                        if (a.profile, B, ctx, a.act, a.kv, a.dense) == ("cfg3", 64, 2048, "bf16", "bf16", False)
+                        else None),
             "bytes_per_launch": int(attn_bytes),
             "us_per_launch": round(attn_ms * 1e3, 2),
             "us_per_launch_in_step": round(in_step_ms * 1e3, 2),

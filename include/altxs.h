@@ -348,6 +348,53 @@ int32_t altxs_range_decode(AltxsCoderState *st, int32_t n, const uint32_t *cum, 
                            const uint8_t *buf, int64_t stride, int32_t *out, int64_t out_stride,
                            altxs_stream_t stream);
 
+/* ---- the shipped per-channel codec (dense runtime banks) -------------------
+ *
+ * The reference ships weights as Init(seed) + a per-channel mixed-bit delta
+ * (src/hyperflow_distillation/mixed_bit_delta.py): every channel (a row, or
+ * a column of the o / down banks, of `width` values) has 0/2/3/4 bits; the
+ * codes of all channels of one width are packed together LSB first (3-bit:
+ * 8 codes per 3 bytes, little endian); each width has its own codebook. At
+ * runtime the banks are dense (model.py:1183-1245): in this library a dense
+ * tensor is an AltxsQTensor with bits = 16 (bf16 values in the MFMA-tiled
+ * order, no scales), which altxs_step accepts for every matrix. */
+enum {
+  ALTXS_CODEBOOK_LLOYD = 0,     /* codebook [n_b][2^b] fp16 levels per channel */
+  ALTXS_CODEBOOK_SYMMETRIC = 1, /* codebook [n_b] fp16 scale: (c - (2^b-1)/2) * s */
+  ALTXS_CODEBOOK_SHARED = 2,    /* shared [2^b] fp16 levels x codebook [n_b] fp16 scale */
+  ALTXS_CODEBOOK_FP4 = 3,       /* 4-bit codes as FP4 E2M1 x codebook [n_b] fp16 scale */
+  ALTXS_CODEBOOK_HYBRID = 4     /* 4-bit channels as FP4, 2/3-bit symmetric */
+};
+
+typedef struct AltxsCodecGroups {
+  const uint8_t *packed[3];    /* index b - 2 (b = 2, 3, 4): the width's packed codes */
+  const uint16_t *codebook[3]; /* fp16, per mode (above) */
+  const uint16_t *shared[3];   /* ALTXS_CODEBOOK_SHARED: [2^b] fp16 levels, else NULL */
+  int64_t n_codes[3];          /* codes held by packed[b - 2] (bounds every read) */
+  int64_t n_book[3];           /* fp16 entries of codebook[b - 2] */
+  int32_t mode;                /* ALTXS_CODEBOOK_* */
+  int32_t reserved;
+} AltxsCodecGroups;
+
+/* Decode channels j = 0 .. n_channels-1: channel j has bits[j] (0: a dead
+ * channel, all zero) and is the rank[j]-th channel of its width (its codes are
+ * codes rank*width .. +width of that width's stream); value i of channel j goes
+ * to out[j*stride_ch + i*stride_el] (fp32), so o / down channels can land as
+ * columns. Replaces dequantize_channels + _from_channels
+ * (mixed_bit_delta.py:116-229) for one bank part. A channel with a bad width,
+ * or whose codes or codebook entries lie past the given counts, is written as
+ * zeros and ORs 2 into *err (a caller-owned device int32). */
+int32_t altxs_codec_decode(const AltxsCodecGroups *g, const uint8_t *bits, const int32_t *rank,
+                           int64_t n_channels, int64_t width, float *out, int64_t stride_ch,
+                           int64_t stride_el, int32_t *err, altxs_stream_t stream);
+
+/* A dense bits = 16 tensor from fp32 rows: w = base + delta (base may be NULL;
+ * fp32 add as apply_delta_to, train_hyperflow.py:8-19), rounded to bf16 (to
+ * nearest even) and written in the MFMA-tiled order of AltxsQTensor (N % 16 ==
+ * 0, K % 256 == 0; row r of base/delta at r*ld). tiled: N*K*2 bytes. */
+int32_t altxs_pack_dense(const float *base, const float *delta, int64_t N, int64_t K, int64_t ld,
+                         void *tiled, altxs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,8 @@
 * :func:`symmetric_levels` restates ``_symmetric_levels`` (147-152).
 * :func:`dequantize_channels` restates ``dequantize_channels`` (172-229) for the
   lloyd, symmetric, shared and fp4 modes.
+* :func:`from_channels` restates ``_from_channels`` (116-144); pinned by a
+  hand-built 2-layer example (tests/test_codec.py).
 * :func:`dequant_group64` is the symmetric rule with 64-wide groups along K
   (the build's device format); pinned against the closed form on all codes.
 * :func:`unpack_tiled` reads the device layout back to (codes, scales); it is
@@ -80,6 +82,27 @@ def dequantize_channels(channel_bits, codebooks, packed, *, channel_width, mode=
         else:
             raise ValueError(f"unsupported mode {mode} for {b}-bit")
     return out
+
+
+def from_channels(name: str, channels: np.ndarray, shape, n_layers: int) -> np.ndarray:
+    """Decoded channels -> the bank tensor (``_from_channels``,
+    mixed_bit_delta.py:116-144): q/k/v/up/emb channels are rows; o and down
+    channels are columns (their banks store the transpose)."""
+    x = np.asarray(channels, dtype=np.float32)
+    L = int(n_layers)
+    if name == "qo_bank":
+        d = int(shape[-1])
+        q = x[:L * d].reshape(L, d, d)
+        o = x[L * d:].reshape(L, d, d).transpose(0, 2, 1)
+        return np.concatenate([q, o], axis=0)
+    if name == "kv_bank":
+        kv, d = int(shape[1]), int(shape[2])
+        return np.concatenate([x[:L * kv].reshape(L, kv, d), x[L * kv:].reshape(L, kv, d)], axis=0)
+    if name in ("mlp_up_bank", "tok_emb.weight"):
+        return x.reshape(shape)
+    if name == "mlp_down_bank":
+        return x.reshape(shape[0], shape[2], shape[1]).transpose(0, 2, 1)
+    raise KeyError(name)
 
 
 def dequant_group64(codes: np.ndarray, scales: np.ndarray, bits: int) -> np.ndarray:

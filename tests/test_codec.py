@@ -174,3 +174,68 @@ def test_dense_bf16_tiled_layout():
                           torch.from_numpy(w).to(torch.bfloat16).float().numpy())
     p = codec.PackedTensor.from_dense("w", w, 16)
     assert p.bits == 16 and p.nbytes_scales == 0 and np.array_equal(p.dense(), codec.unpack_dense_tiled(t, n, k))
+
+
+def test_from_channels_hand_built():
+    """_from_channels (mixed_bit_delta.py:116-144) on a 2-layer, d=2 example
+    written out by hand: q/k/v/up rows are channels, o/down columns are."""
+    x = np.arange(16, dtype=np.float32).reshape(8, 2)  # channel c holds (2c, 2c+1)
+    qo = codec_ref.from_channels("qo_bank", x, [4, 2, 2], 2)
+    assert np.array_equal(qo[0], [[0, 1], [2, 3]]) and np.array_equal(qo[1], [[4, 5], [6, 7]])
+    # o of layer 0 is channels 4, 5 as columns: o0[i][c] = channel(4 + c)[i]
+    assert np.array_equal(qo[2], [[8, 10], [9, 11]]) and np.array_equal(qo[3], [[12, 14], [13, 15]])
+    kv = codec_ref.from_channels("kv_bank", x[:4], [4, 1, 2], 2)
+    assert np.array_equal(kv[:, 0], [[0, 1], [2, 3], [4, 5], [6, 7]])
+    down = codec_ref.from_channels("mlp_down_bank", x[:8], [2, 2, 4], 2)  # [L, d=2, F=4]
+    assert np.array_equal(down[0], [[0, 2, 4, 6], [1, 3, 5, 7]])
+    up = codec_ref.from_channels("mlp_up_bank", x[:8], [2, 4, 2], 2)
+    assert np.array_equal(up[1], [[8, 9], [10, 11], [12, 13], [14, 15]])
+
+
+def test_bank_parts_place_channels_like_from_channels():
+    """altxs_amd.shipped.bank_parts (where the device decoder writes each
+    channel) equals from_channels followed by the split into this build's
+    per-layer tensors."""
+    from altxs_amd import shipped
+    from altxs_amd.config import make_config
+
+    cfg = make_config("tiny")
+    L, d, kvd, F, V = cfg.num_layers, cfg.model_dim, cfg.kv_dim, cfg.hidden_dim, cfg.vocab_size
+    shapes = {"tok_emb.weight": [V, d], "qo_bank": [2 * L, d, d], "kv_bank": [2 * L, kvd, d],
+              "mlp_up_bank": [L, F, d], "mlp_down_bank": [L, d, F]}
+    rng = np.random.default_rng(0)
+    bank = {n: rng.standard_normal((int(np.prod(s)) // d, d)).astype(np.float32) for n, s in shapes.items()}
+    dst = {n: np.zeros(a * b, np.float32) for n, (a, b) in shipped.tensor_shapes(cfg).items()}
+    for name, parts in shipped.bank_parts(cfg).items():
+        covered = 0
+        for p in parts:
+            for j in range(p.n):
+                idx = p.offset + j * p.stride_ch + np.arange(d) * p.stride_el
+                dst[p.dest][idx] = bank[name][p.c0 + j]
+            covered += p.n
+        assert covered == bank[name].shape[0]
+    full = {n: codec_ref.from_channels(n, bank[n], shapes[n], L) for n in shapes}
+    assert np.array_equal(dst["emb"].reshape(V, d), full["tok_emb.weight"])
+    for l in range(L):
+        qkv = np.concatenate([full["qo_bank"][l], full["kv_bank"][l], full["kv_bank"][L + l]])
+        assert np.array_equal(dst[f"l{l}.qkv"].reshape(qkv.shape), qkv)
+        assert np.array_equal(dst[f"l{l}.o"].reshape(d, d), full["qo_bank"][L + l])
+        assert np.array_equal(dst[f"l{l}.up"].reshape(F, d), full["mlp_up_bank"][l])
+        assert np.array_equal(dst[f"l{l}.down"].reshape(d, F), full["mlp_down_bank"][l])
+
+
+@pytest.mark.skipif(not os.path.exists("/root/reference/weights/mixed_da_bpw3.15_upb1.8.json"),
+                    reason="the reference asset is only in the build container")
+def test_shipped_layouts_match_bank_parts():
+    """The shipped student's layouts (channel counts, widths) are what the
+    device decoder's placement expects for its config."""
+    from altxs_amd import shipped
+
+    meta = json.load(open("/root/reference/weights/mixed_da_bpw3.15_upb1.8.json"))
+    cfg = shipped.config_from_meta(meta)
+    assert cfg.num_layers == meta["n_layers"] and cfg.vocab_size == 256
+    for name, parts in shipped.bank_parts(cfg).items():
+        lay = meta["layouts"][name]
+        assert lay["channel_width"] == cfg.model_dim
+        assert sum(p.n for p in parts) == lay["channels"]
+        assert sorted((p.c0, p.c0 + p.n) for p in parts)[-1][1] == lay["channels"]

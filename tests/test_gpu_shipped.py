@@ -1,0 +1,186 @@
+"""The shipped per-channel codec on the device (altxs_codec_decode,
+altxs_pack_dense) and the dense bf16 step it feeds.
+
+* decode: every codebook mode of the reference (lloyd, symmetric, shared,
+  fp4, hybrid) over random channel widths incl. dead channels, written as rows
+  and as columns, equals the oracle's ``dequantize_channels`` bit for bit;
+* pack: bf16(base + delta) in the tiled order equals the host packer's bytes;
+* end to end: a codec written in the reference's file format (json +
+  safetensors) for the "tiny" config, plus an Init state, decodes and packs on
+  the device, and the step on those weights matches the fp32 oracle run on
+  bf16(Init + delta).  (The reference's own asset is not on the GPU box; the
+  oracle decoder is pinned against it on the CPU.)
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """LSB-first packing of the reference format (3-bit: 8 codes per 3 bytes)."""
+    c = np.asarray(codes, dtype=np.uint32).reshape(-1)
+    per = 8 if bits == 3 else 8 // bits
+    nbytes = 3 if bits == 3 else 1
+    pad = (-c.size) % per
+    c = np.concatenate([c, np.zeros(pad, np.uint32)]).reshape(-1, per)
+    words = np.bitwise_or.reduce(c << (np.arange(per, dtype=np.uint32) * bits), axis=1)
+    return np.stack([(words >> (8 * i)) & 0xFF for i in range(nbytes)], axis=1).astype(np.uint8).reshape(-1)
+
+
+def random_bank(rng, n_ch: int, width: int, mode: str):
+    bits = rng.choice([0, 2, 3, 4], size=n_ch, p=[0.05, 0.3, 0.35, 0.3]).astype(np.uint8)
+    if mode == "fp4":
+        bits[bits > 0] = 4
+    packed, books, scales = {}, {}, {}
+    for b in (2, 3, 4):
+        n = int((bits == b).sum())
+        packed[b] = pack_codes(rng.integers(0, 1 << b, n * width), b)
+        if mode == "lloyd":
+            books[b] = (rng.standard_normal((n, 1 << b)) * 0.05).astype(np.float16)
+        elif mode == "shared":
+            books[b] = (rng.standard_normal(1 << b)).astype(np.float16)
+            scales[b] = (rng.random(n) * 0.05 + 0.001).astype(np.float16)
+        else:
+            books[b] = (rng.random((n, 1)) * 0.05 + 0.001).astype(np.float16)
+    return bits, packed, books, scales
+
+
+@pytest.mark.parametrize("mode", ["lloyd", "symmetric", "shared", "fp4", "hybrid_fp4_symmetric"])
+def test_codec_decode_matches_oracle(mode):
+    from altxs_amd import shipped
+    from oracle import codec_ref
+
+    _log(f"codec decode {mode}")
+    rng = np.random.default_rng(len(mode))
+    n_ch, width = 96, 512
+    bits, packed, books, scales = random_bank(rng, n_ch, width, mode)
+    for b in (2, 3, 4):  # the test packer inverts the oracle's unpacker
+        n = int((bits == b).sum())
+        assert codec_ref.unpack_codes(packed[b], b, n * width).size == n * width
+    want = codec_ref.dequantize_channels(bits, books, packed, channel_width=width, mode=mode,
+                                         scales=scales or None)
+    bank = shipped.DeviceBank(bits, packed, books, mode, scales or None, "cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rows = torch.full((n_ch * width,), 7.0, device="cuda")
+    bank.decode(shipped.Part(0, n_ch, "x", 0, width, 1), width, rows, err)
+    cols = torch.full((n_ch * width,), 7.0, device="cuda")
+    bank.decode(shipped.Part(0, n_ch, "x", 0, 1, n_ch), width, cols, err)
+    part = torch.full((40 * width + 3,), 7.0, device="cuda")  # a channel range at an offset
+    bank.decode(shipped.Part(50, 40, "x", 3, width, 1), width, part, err)
+    assert int(err.item()) == 0
+    assert np.array_equal(rows.cpu().numpy().reshape(n_ch, width), want)
+    assert np.array_equal(cols.cpu().numpy().reshape(width, n_ch), want.T)
+    assert np.array_equal(part.cpu().numpy()[3:].reshape(40, width), want[50:90])
+
+
+def test_codec_decode_flags_missing_codebook_rows():
+    from altxs_amd import shipped
+
+    _log("codec decode error flag")
+    rng = np.random.default_rng(1)
+    bits, packed, books, _ = random_bank(rng, 32, 512, "lloyd")
+    books[3] = books[3][:2]  # two channels' worth of levels only
+    bank = shipped.DeviceBank(bits, packed, books, "lloyd", None, "cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.zeros(32 * 512, device="cuda")
+    bank.decode(shipped.Part(0, 32, "x", 0, 512, 1), 512, out, err)
+    assert int(err.item()) == 2
+    rank3 = np.flatnonzero(bits == 3)
+    if rank3.size > 2:  # channels past the codebook are zero, the others decoded
+        assert not out.view(32, 512)[int(rank3[2])].any()
+
+
+def test_pack_dense_matches_host_packer():
+    from altxs_amd import codec, shipped
+
+    _log("pack dense")
+    rng = np.random.default_rng(2)
+    base = rng.standard_normal((48, 768)).astype(np.float32)
+    delta = (rng.standard_normal((48, 768)) * 1e-3).astype(np.float32)
+    got = shipped.pack_dense(torch.from_numpy(delta).cuda(), torch.from_numpy(base).cuda())
+    want = codec.pack_dense_tiled(base + delta)
+    assert np.array_equal(got.cpu().numpy(), want)
+    got0 = shipped.pack_dense(torch.from_numpy(delta).cuda())
+    assert np.array_equal(got0.cpu().numpy(), codec.pack_dense_tiled(delta))
+
+
+def test_shipped_codec_end_to_end(tmp_path):
+    from safetensors.numpy import save_file
+
+    from altxs_amd import codec, shipped, synth
+    from altxs_amd.config import make_config
+    from altxs_amd.model import StepModel
+    from oracle import codec_ref
+    from oracle.model_ref import OracleModel
+
+    _log("shipped codec end to end (tiny)")
+    cfg = make_config("tiny")
+    L, d, kvd, F, V = cfg.num_layers, cfg.model_dim, cfg.kv_dim, cfg.hidden_dim, cfg.vocab_size
+    shapes = {"tok_emb.weight": [V, d], "qo_bank": [2 * L, d, d], "kv_bank": [2 * L, kvd, d],
+              "mlp_up_bank": [L, F, d], "mlp_down_bank": [L, d, F]}
+    rng = np.random.default_rng(11)
+    sm0 = synth.make_model(cfg, std=0.08, softcap=(2.0, 1.5))
+    init = {n: (rng.standard_normal(s) * 0.06).astype(np.float32) for n, s in shapes.items()}
+    state, layouts = {}, {}
+    delta = {}
+    for name, shape in shapes.items():
+        n_ch = int(np.prod(shape)) // d
+        bits, packed, books, _ = random_bank(rng, n_ch, d, "lloyd")
+        state[f"bits/{name}"] = bits
+        for b in (2, 3, 4):
+            state[f"packed/{name}/b{b}"] = packed[b]
+            state[f"codebook/{name}/b{b}"] = books[b]
+        layouts[name] = {"shape": shape, "channels": n_ch, "channel_width": d, "fp16": False}
+        ch = codec_ref.dequantize_channels(bits, books, packed, channel_width=d, mode="lloyd")
+        delta[name] = codec_ref.from_channels(name, ch, shape, L)
+    small_names = sorted(sm0.small)
+    for n in small_names:
+        state[f"small/{n}"] = np.ascontiguousarray(sm0.small[n], dtype=np.float32)
+    cfg_meta = {f: getattr(cfg, f) for f in ("vocab_size", "num_layers", "xsa_last_n", "model_dim",
+                                              "num_heads", "num_kv_heads", "mlp_mult", "rope_dims",
+                                              "rope_yarn", "num_loops", "loop_start", "loop_end",
+                                              "parallel_start_layer", "block_size")}
+    meta = {"format": "hope_mixed_bit_delta", "format_version": 5, "seed": 1, "cfg": cfg_meta,
+            "codebook_mode": "lloyd", "n_layers": L, "layouts": layouts, "small_params": small_names}
+    stem = str(tmp_path / "codec")
+    save_file(state, stem + ".safetensors")
+    json.dump(meta, open(stem + ".json", "w"))
+
+    cfg2, weights, small = shipped.load_shipped(stem + ".safetensors", init)
+    assert cfg2 == cfg
+    model_sm = synth.SynthModel(cfg2, weights, {k: np.asarray(v) for k, v in small.items()})
+    # the oracle runs bf16(Init + delta), reassembled into reference banks
+    dense = {n: torch.from_numpy(init[n] + delta[n]).to(torch.bfloat16).float().numpy() for n in shapes}
+    sd = dict(sm0.small)
+    sd.update(dense)
+    for l in range(L):  # the device tiles hold exactly these values
+        qkv = np.concatenate([dense["qo_bank"][l], dense["kv_bank"][l], dense["kv_bank"][L + l]])
+        assert np.array_equal(weights[f"l{l}.qkv"].tiled.cpu().numpy(), codec.pack_dense_tiled(qkv))
+        assert np.array_equal(weights[f"l{l}.down"].tiled.cpu().numpy(),
+                              codec.pack_dense_tiled(dense["mlp_down_bank"][l]))
+    toks = synth.zipf_tokens(V, (2, 10), seed=4).astype(np.int32)
+    model = StepModel(model_sm, act="fp32")
+    st = model.make_static_state(256, win=1, batch=2)
+    got = []
+    for t in range(toks.shape[1]):
+        st.token.copy_(torch.from_numpy(toks[:, t:t + 1]))
+        model.step(st, commit=True)
+        got.append(st.logits.cpu().numpy().copy())
+    st.check_errors()
+    got = np.stack(got, 1)
+    om = OracleModel(cfg, sd, act="fp32", max_len=256)
+    want = np.stack([om.decode_rows(t).numpy() for t in toks.astype(np.int64)])
+    err = np.abs(got - want).max()
+    _log(f"max |dlogit| = {err:.3e}")
+    assert err < 2e-4, err
