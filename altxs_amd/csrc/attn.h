@@ -315,14 +315,16 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) acc[gi][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  for (int T = wave; T < ntiles; T += ATT_WAVES) {
+  // tile T of the K and V caches -> registers (one 16-byte load per lane each)
+  auto load_t = [&](u32x4 (&kr)[8], u32x4 (&vr)[8], int T) {
     const u32x4* kt = (const u32x4*)(kb + (int64_t)T * (TILE * HD)) + lane;
     const u32x4* vt = (const u32x4*)(vb + (int64_t)T * (TILE * HD)) + lane;
-    u32x4 kr[8], vr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) kr[i] = __builtin_nontemporal_load(kt + 64 * i);
 #pragma unroll
     for (int i = 0; i < 8; ++i) vr[i] = __builtin_nontemporal_load(vt + 64 * i);
+  };
+  auto tile = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8], int T) {
     const int k0 = T * TILE;
 #pragma unroll
     for (int gi = 0; gi < NG; ++gi) {
@@ -383,6 +385,21 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
             acc[gi][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[k], vop, acc[gi][nb], 0, 0, 0);
         }
       }
+    }
+  };
+  // Tiles T = wave, wave + 4, ... in order; the next tile's loads are in
+  // flight while the current one is computed (two register buffers), which
+  // at one wave per SIMD is the only latency hiding there is.
+  {
+    u32x4 ka[8], va[8], kn[8], vn[8];
+    int T = wave;
+    if (T < ntiles) load_t(ka, va, T);
+    for (; T < ntiles; T += 2 * ATT_WAVES) {
+      const int T1 = T + ATT_WAVES, T2 = T + 2 * ATT_WAVES;
+      if (T1 < ntiles) load_t(kn, vn, T1);
+      tile(ka, va, T);
+      if (T2 < ntiles) load_t(ka, va, T2);
+      if (T1 < ntiles) tile(kn, vn, T1);
     }
   }
   // merge and store, one group of 16 queries at a time (wave w: queries w, w+4, ...)

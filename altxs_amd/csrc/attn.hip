@@ -170,7 +170,10 @@ hipError_t launch_y(const AttnP& p, int group, bool kv_bf16, bool ops_bf16, bool
 #define ATT_GO(K) \
   do { hipLaunchKernelGGL(K, grid, block, 0, s, p); return hipGetLastError(); } while (0)
   if (kv_bf16 && p.W > 1 && !rows_only) {
-    const int ng = p.W <= 16 ? 1 : (p.W <= 32 ? 2 : 4);
+    // 32 query rows per workgroup for longer windows: the 64-row variant needs
+    // more than half the register file (one wave per SIMD) and measured slower
+    // (cfg4: 2.99 vs 2.77 ms per slot); the bits are the same either way
+    const int ng = p.W <= 16 ? 1 : 2;
     const int nqb = (p.W + 16 * ng - 1) / (16 * ng);
     dim3 wgrid((unsigned)((int64_t)p.B * p.H * nqb));
 #define WIN_GO(K) \
