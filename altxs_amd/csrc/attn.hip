@@ -39,7 +39,8 @@ namespace {
 template <int G, int NP, int YBF16>
 __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
-  attn_mfma_task<G, NP, YBF16, ALTXS_ATT_PF>(a, blockIdx.x / a.Hkv, blockIdx.x % a.Hkv, sm);
+  // GQA launches have G times fewer workgroups: keep two tiles per wave in flight
+  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : ALTXS_ATT_PF)>(a, blockIdx.x / a.Hkv, blockIdx.x % a.Hkv, sm);
 }
 
 // Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
