@@ -244,7 +244,12 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_chunk_kernel(const float* __re
 // exactly as in cdf_chunk_kernel (same threads, same tiles, same order) and p,
 // the counts and their exact integer prefix sums follow, so every table is
 // bit-identical to the chunk kernel's.
-template <int EPT>
+//
+// stats == NULL (launches whose LM head skipped them): the kernel forms each
+// 64-column tile's (max m_t, sum of exp(l - m_t)) itself, exactly as the LM
+// head epilogue does (one tile per wave, column c on lane c, wave_max and
+// wave_sum), from the row staged in LDS.
+template <int EPT, bool OWN_STATS>
 __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __restrict__ logits,
                                                               const float2* __restrict__ stats,
                                                               int V, float* __restrict__ probs,
@@ -252,6 +257,7 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __rest
   static_assert(EPT % 4 == 0, "whole 16-byte vectors per thread");
   __shared__ float red[CH_WAVES];
   __shared__ uint32_t wred[CH_WAVES];
+  extern __shared__ __attribute__((aligned(16))) float srow[];  // OWN_STATS: the row, then the stats
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x;
   const int base = t * EPT;
@@ -263,6 +269,23 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __rest
     v[k] = mine ? __builtin_nontemporal_load((const f32x4*)(x + base) + k) : f32x4{0.f, 0.f, 0.f, 0.f};
   const int ntile = V / 64;
   const float2* st = stats + row * (int64_t)ntile;
+  if constexpr (OWN_STATS) {
+    float2* sst = (float2*)(srow + V);
+    if (mine) {
+#pragma unroll
+      for (int k = 0; k < EPT / 4; ++k) *((f32x4*)(srow + base) + k) = v[k];
+    }
+    __syncthreads();
+    const int w = t / WAVE, l = t % WAVE;
+    for (int i = w; i < ntile; i += CH_WAVES) {  // uniform per wave
+      const float lv = srow[64 * i + l];
+      const float m = wave_max(lv);
+      const float e = wave_sum(lv == -INFINITY ? 0.f : __expf(lv - m));
+      if (l == 0) sst[i] = make_float2(m, e);
+    }
+    __syncthreads();
+    st = sst;
+  }
   float mt = -INFINITY;
   for (int i = t; i < ntile; i += CH_THREADS) mt = fmaxf(mt, st[i].x);
   const float M = block_max_n(mt, red);
@@ -323,23 +346,43 @@ hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, boo
                      : launch_cdf<false>(in, rows, V, flags, probs, cum, s);
 }
 
+bool altxs_cdf_rows_kernel(int64_t rows, int V) {
+  return rows >= 1024 && V >= 4096 && V <= 16 * CH_THREADS && V % (4 * CH_THREADS) == 0;
+}
+
 hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int64_t rows, int V,
                                   float* probs, uint32_t* cum, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   if (V % 64) return hipErrorInvalidValue;
-  if (rows >= 1024 && V >= 4096 && V <= 16 * CH_THREADS && V % (4 * CH_THREADS) == 0) {
-    // many rows: one workgroup per row (bit-identical tables, no recount)
-    if (V <= 4 * CH_THREADS)
-      hipLaunchKernelGGL(cdf_row_kernel<4>, dim3((unsigned)rows), dim3(CH_THREADS), 0, s, logits,
-                         stats, V, probs, cum);
-    else if (V <= 8 * CH_THREADS)
-      hipLaunchKernelGGL(cdf_row_kernel<8>, dim3((unsigned)rows), dim3(CH_THREADS), 0, s, logits,
-                         stats, V, probs, cum);
-    else
-      hipLaunchKernelGGL(cdf_row_kernel<16>, dim3((unsigned)rows), dim3(CH_THREADS), 0, s, logits,
-                         stats, V, probs, cum);
+  if (altxs_cdf_rows_kernel(rows, V)) {
+    // many rows: one workgroup per row (bit-identical tables, no recount); with
+    // stats == NULL it forms the tile statistics itself from the row in LDS
+    const size_t lds = stats ? 0 : (size_t)V * 4 + (size_t)(V / 64) * 8;
+#define ROW_GO(E)                                                                              \
+  do {                                                                                         \
+    if (stats)                                                                                 \
+      hipLaunchKernelGGL((cdf_row_kernel<E, false>), dim3((unsigned)rows), dim3(CH_THREADS), 0, \
+                         s, logits, stats, V, probs, cum);                                     \
+    else {                                                                                     \
+      static bool configured = false;                                                          \
+      if (!configured) {                                                                       \
+        hipError_t e = hipFuncSetAttribute((const void*)cdf_row_kernel<E, true>,               \
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,         \
+                                           (int)(16 * CH_THREADS * 4 + 16 * CH_THREADS / 8));  \
+        if (e != hipSuccess) return e;                                                         \
+        configured = true;                                                                     \
+      }                                                                                        \
+      hipLaunchKernelGGL((cdf_row_kernel<E, true>), dim3((unsigned)rows), dim3(CH_THREADS),    \
+                         lds, s, logits, stats, V, probs, cum);                                \
+    }                                                                                          \
+  } while (0)
+    if (V <= 4 * CH_THREADS) ROW_GO(4);
+    else if (V <= 8 * CH_THREADS) ROW_GO(8);
+    else ROW_GO(16);
+#undef ROW_GO
     return hipGetLastError();
   }
+  if (!stats) return hipErrorInvalidValue;
   const int chunk = V < 2048 ? V : 2048;
   if (V % chunk) return hipErrorInvalidValue;
   dim3 grid((unsigned)(V / chunk), (unsigned)rows), block(CH_THREADS);

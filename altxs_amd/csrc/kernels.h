@@ -8,6 +8,9 @@ hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, boo
 
 // Row-parallel softmax -> CDF from the LM head's per-64-column tile statistics
 // (no renormalisation); V % 64 == 0.
+// Whether altxs_launch_cdf_stats uses one workgroup per row for this shape
+// (it then also accepts stats == NULL and forms the tile statistics itself).
+bool altxs_cdf_rows_kernel(int64_t rows, int V);
 hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int64_t rows, int V,
                                   float* probs, uint32_t* cum, hipStream_t s);
 

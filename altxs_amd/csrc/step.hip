@@ -391,12 +391,16 @@ struct StepRun {
     const int R = G.nb * d->W;
     const int64_t Rp = align_up(R, 16), D = d->D;
     const bool fast_cdf = !(d->flags & ALTXS_F_RENORM) && d->V % 64 == 0;
+    bool own_stats = false;
     hipError_t e;
     {
       const int n = d->n_slots, fm = final_mode(d);
       const float* xf = (fm == 2 ? w.X1 : w.X0) + n * Rp * D;
       ProNorm pro{xf, fm == 1 ? w.X1 + n * Rp * D : nullptr, fm == 1 ? 1 : 0, 1.0f, d->norm_eps, d->D};
-      EpiLogits epi{G.logits, fast_cdf ? w.STATS : nullptr, d->V,
+      // with the large-tile head and the one-row-per-workgroup CDF, the CDF
+      // kernel forms the tile statistics itself (same arithmetic, off the GEMM)
+      own_stats = big(R, d->emb) && fast_cdf && G.cum && altxs_cdf_rows_kernel(R, d->V);
+      EpiLogits epi{G.logits, (fast_cdf && !own_stats) ? w.STATS : nullptr, d->V,
                     (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap, d->softcap_pn};
       if (big(R, d->emb)) {
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
@@ -409,7 +413,8 @@ struct StepRun {
     }
     if (G.probs || G.cum) {
       if (fast_cdf && G.cum) {
-        if ((e = altxs_launch_cdf_stats(G.logits, w.STATS, R, d->V, G.probs, G.cum, st)) != hipSuccess)
+        if ((e = altxs_launch_cdf_stats(G.logits, own_stats ? nullptr : w.STATS, R, d->V, G.probs,
+                                        G.cum, st)) != hipSuccess)
           return e;
       } else {
         const int fl = (d->flags & ALTXS_F_RENORM) ? ALTXS_CDF_RENORM : 0;
