@@ -433,9 +433,6 @@ __device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, i
   auto issue = [&](int nt) { issue_w(nt); issue_a(nt); };
   if (nt0 < ntiles) issue_w(nt0);
   wait();
-  // the first tile's epilogue inputs (positions, RoPE rows, residuals) are
-  // requested before the prologue, so their latency overlaps it
-  auto pre = epi.template prefetch<Cfg>(m0, nt0 * Cfg::NCOL, R, batch);
   if (nt0 < ntiles) issue_a(nt0);
   if constexpr (STAGE) {
     pro.template stage<AM, Cfg::THREADS>(As, scratch, m0, R, w.K, batch, nt0 == 0);
@@ -445,7 +442,7 @@ __device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, i
     const int n0 = nt * Cfg::NCOL;
     const int nb = nt * NB + nbi;
     const bool active = nb * 16 < w.N;
-    if (nt != nt0) pre = epi.template prefetch<Cfg>(m0, n0, R, batch);
+    const auto pre = epi.template prefetch<Cfg>(m0, n0, R, batch);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (active) {
       for (int kb = kb0; kb < kb1; kb += 2) {
