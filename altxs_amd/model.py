@@ -121,12 +121,22 @@ class StaticState:
         """[B, 2, Hkv, max_len, hd] view of one slot's cache."""
         return self.kv[slot]
 
-    def _desc(self, flags: int) -> _lib.StepDesc:
-        d = self._descs.get(flags)
+    def _desc(self, flags: int, width: int | None = None) -> _lib.StepDesc:
+        w = self.win if width is None else int(width)
+        d = self._descs.get((flags, w))
         if d is None:
             d = self.model._fill_desc(self, flags)
-            self._descs[flags] = d
+            if w != self.win:  # a narrower window over the same buffers (first B*w rows)
+                if not 1 <= w <= self.win or self.split or self.persistent:
+                    raise ValueError(f"width {w} not usable on this state")
+                d.W = w
+            self._descs[(flags, w)] = d
         return d
+
+    def tokens(self, width: int | None = None) -> torch.Tensor:
+        """The [B, width] token buffer a step of that width reads (a view)."""
+        w = self.win if width is None else int(width)
+        return self.token.view(-1)[:self.batch * w].view(self.batch, w)
 
     def commit_window(self) -> None:
         """pos += W; prev_raw = cand (K/V rows are already in place)."""
@@ -283,15 +293,18 @@ class StepModel:
 
     # ---- the step -------------------------------------------------------------
     def step(self, st: StaticState, *, commit: bool = False, renorm: bool = False,
-             attn_events: int | None = None) -> None:
+             attn_events: int | None = None, width: int | None = None) -> None:
         """Enqueue one step on the current stream.
 
         ``attn_events``: optional address of 2*n_slots hipEvent_t handles,
         recorded around each slot's attention launch (timing hook); with a
         persistent state, events 0 and 1 bracket the layer kernel.
+        ``width``: run a window of that many tokens (<= the state's W) over the
+        same buffers -- tokens in ``st.tokens(width)``, outputs in the first
+        B*width rows; a commit advances pos by width.
         """
         flags = (_lib.F_COMMIT if commit else 0) | (_lib.F_RENORM if renorm else 0)
-        d = st._desc(flags)
+        d = st._desc(flags, width)
         d.attn_events = attn_events
         rc = self.lib.altxs_step(ctypes.byref(d), ctypes.c_void_p(_stream_ptr(self.device)))
         _lib.check(rc, "altxs_step")
