@@ -471,23 +471,26 @@ struct EpiQKV {
     if (r >= R) return;
     const int p = pre.p;
     const bool pos_ok = p >= 0 && p < max_len;
-    if (kind == 0) {
-      float* qo = q + ((int64_t)r * H + head) * HD + c0;
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) qo[i] = v[i] * pre.gain;
+    static_assert(CPT == 4, "four consecutive columns per thread (16-byte q / K stores)");
+    if (kind == 0) {  // q row: 16-byte aligned (c0 % 4 == 0)
+      *(f32x4*)(q + ((int64_t)r * H + head) * HD + c0) =
+          f32x4{v[0] * pre.gain, v[1] * pre.gain, v[2] * pre.gain, v[3] * pre.gain};
     } else if (pos_ok) {
       const int b = r / W;
       const int64_t head_base = (((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len * HD;
       if (kv_bf16) {  // tiled operand layout (kv_tile_k / kv_tile_v)
         uint16_t* tile = (uint16_t*)kv + head_base + (int64_t)(p / ALTXS_KV_TILE) * (ALTXS_KV_TILE * HD);
         const int kt = p % ALTXS_KV_TILE;
+        if (kind == 1) {  // K: dims c0 .. c0+3 are adjacent in the tile (one 8-byte store)
+          *(u32x2*)(tile + kv_tile_k(kt, c0)) =
+              u32x2{(uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                    (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16)};
+        } else {
 #pragma unroll
-        for (int i = 0; i < CPT; ++i)
-          tile[kind == 1 ? kv_tile_k(kt, c0 + i) : kv_tile_v(kt, c0 + i)] = f32_to_bf16(v[i]);
+          for (int i = 0; i < CPT; ++i) tile[kv_tile_v(kt, c0 + i)] = f32_to_bf16(v[i]);
+        }
       } else {
-        float* row = (float*)kv + head_base + (int64_t)p * HD + c0;
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) row[i] = v[i];
+        *(f32x4*)((float*)kv + head_base + (int64_t)p * HD + c0) = f32x4{v[0], v[1], v[2], v[3]};
       }
     } else if (li == 0) {
       flag_err(err, ALTXS_EDEV_POS);
