@@ -46,6 +46,9 @@ def test_bad_arguments_return_errors_without_gpu():
     assert L.altxs_range_encode(None, 1, 1, None, None, 256, None, 64, None) == -1
     assert b"altxs_range_encode" in L.altxs_last_error()
     assert L.altxs_range_decode(None, 1, None, 1, None, 64, None, 1, None) == -1
+    assert L.altxs_codec_decode(None, None, None, 1, 512, None, 512, 1, None, None) == -1
+    assert L.altxs_pack_dense(None, None, 16, 256, 256, None, None) == -1
+    assert b"altxs_pack_dense" in L.altxs_last_error()
 
 
 def test_struct_layout_matches_header(tmp_path):
@@ -62,6 +65,8 @@ int main(void) {{
          offsetof(AltxsStepDesc, tokens), offsetof(AltxsStepDesc, err));
   printf("%zu %zu %zu\\n", sizeof(AltxsCoderState), offsetof(AltxsCoderState, nbytes),
          offsetof(AltxsCoderState, err));
+  printf("%zu %zu %zu\\n", sizeof(AltxsCodecGroups), offsetof(AltxsCodecGroups, n_codes),
+         offsetof(AltxsCodecGroups, mode));
   return 0;
 }}
 """)
@@ -73,5 +78,6 @@ int main(void) {{
           ctypes.sizeof(_lib.Slot), ctypes.sizeof(_lib.StepDesc),
           _lib.StepDesc.layers.offset, _lib.StepDesc.emb.offset, _lib.StepDesc.tokens.offset,
           _lib.StepDesc.err.offset, ctypes.sizeof(_lib.CoderState), _lib.CoderState.nbytes.offset,
-          _lib.CoderState.err.offset]
+          _lib.CoderState.err.offset, ctypes.sizeof(_lib.CodecGroups), _lib.CodecGroups.n_codes.offset,
+          _lib.CodecGroups.mode.offset]
     assert c_sizes == py
