@@ -257,7 +257,7 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __rest
   static_assert(EPT % 4 == 0, "whole 16-byte vectors per thread");
   __shared__ float red[CH_WAVES];
   __shared__ uint32_t wred[CH_WAVES];
-  extern __shared__ __attribute__((aligned(16))) float srow[];  // OWN_STATS: the row, then the stats
+  extern __shared__ __attribute__((aligned(16))) float srow[];  // [V] (+ [V/64] float2 stats)
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x;
   const int base = t * EPT;
@@ -310,15 +310,22 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __rest
     if (probs && mine) *((f32x4*)(probs + row * (int64_t)V + base) + k) = p;
   }
   uint32_t run = block_excl_scan(tot, wred);
-  uint32_t* co = cum + row * (int64_t)(V + 1);
-  if (t == 0) co[0] = 0u;
+  // The table goes out through LDS so that each store instruction writes 64
+  // consecutive words (a thread's own 16 values are 64 bytes apart from its
+  // neighbours', and co + 1 is only 4-byte aligned).
+  uint32_t* scum = (uint32_t*)srow;
+  __syncthreads();  // srow (OWN_STATS) is no longer read
   if (mine) {
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {  // co + 1 is only 4-byte aligned: scalar stores
+    for (int k = 0; k < EPT; ++k) {
       run += f[k];
-      co[base + k + 1] = run;
+      scum[base + k] = run;
     }
   }
+  __syncthreads();
+  uint32_t* co = cum + row * (int64_t)(V + 1);
+  if (t == 0) co[0] = 0u;
+  for (int i = t; i < V; i += CH_THREADS) co[i + 1] = scum[i];
 }
 
 template <bool FROM_LOGITS>
@@ -357,24 +364,27 @@ hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int6
   if (altxs_cdf_rows_kernel(rows, V)) {
     // many rows: one workgroup per row (bit-identical tables, no recount); with
     // stats == NULL it forms the tile statistics itself from the row in LDS
-    const size_t lds = stats ? 0 : (size_t)V * 4 + (size_t)(V / 64) * 8;
+    // dynamic LDS: the table staging (and, forming the statistics, the row and its stats)
+    const size_t lds = (size_t)V * 4 + (stats ? 0 : (size_t)(V / 64) * 8);
 #define ROW_GO(E)                                                                              \
   do {                                                                                         \
+    static bool configured = false;                                                            \
+    if (!configured) {                                                                         \
+      const int most = (int)(16 * CH_THREADS * 4 + 16 * CH_THREADS / 8);                       \
+      hipError_t e = hipFuncSetAttribute((const void*)cdf_row_kernel<E, true>,                 \
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, most);    \
+      if (e == hipSuccess)                                                                     \
+        e = hipFuncSetAttribute((const void*)cdf_row_kernel<E, false>,                         \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, most);             \
+      if (e != hipSuccess) return e;                                                           \
+      configured = true;                                                                       \
+    }                                                                                          \
     if (stats)                                                                                 \
-      hipLaunchKernelGGL((cdf_row_kernel<E, false>), dim3((unsigned)rows), dim3(CH_THREADS), 0, \
-                         s, logits, stats, V, probs, cum);                                     \
-    else {                                                                                     \
-      static bool configured = false;                                                          \
-      if (!configured) {                                                                       \
-        hipError_t e = hipFuncSetAttribute((const void*)cdf_row_kernel<E, true>,               \
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,         \
-                                           (int)(16 * CH_THREADS * 4 + 16 * CH_THREADS / 8));  \
-        if (e != hipSuccess) return e;                                                         \
-        configured = true;                                                                     \
-      }                                                                                        \
+      hipLaunchKernelGGL((cdf_row_kernel<E, false>), dim3((unsigned)rows), dim3(CH_THREADS),   \
+                         lds, s, logits, stats, V, probs, cum);                                \
+    else                                                                                       \
       hipLaunchKernelGGL((cdf_row_kernel<E, true>), dim3((unsigned)rows), dim3(CH_THREADS),    \
                          lds, s, logits, stats, V, probs, cum);                                \
-    }                                                                                          \
   } while (0)
     if (V <= 4 * CH_THREADS) ROW_GO(4);
     else if (V <= 8 * CH_THREADS) ROW_GO(8);

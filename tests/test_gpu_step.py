@@ -175,16 +175,17 @@ def test_dense_cdf_bit_identical_decode_encode(act):
     assert np.array_equal(cmb[0], cm1[0])
 
 
-@pytest.mark.parametrize("act", ["bf16", "fp32"])
-def test_long_window_bit_identical_to_rows(act):
-    """A 512-token window per segment (2048 rows: the launch shapes of chunk
-    scoring -- 128 x 128 GEMM tiles, one workgroup per CDF row) gives the
-    logits and tables of 512 decode rows."""
+@pytest.mark.parametrize("act,B", [("bf16", 4), ("fp32", 4), ("bf16", 2)])
+def test_long_window_bit_identical_to_rows(act, B):
+    """A 512-token window per segment gives the logits and tables of 512
+    decode rows: 2048 rows take the launch shapes of chunk scoring (128 x 128
+    GEMM tiles, one workgroup per CDF row forming its own tile statistics),
+    1024 rows the 16-row GEMMs with one workgroup per CDF row."""
     from altxs_amd.model import StepModel
 
-    _log(f"long window vs rows {act}")
+    _log(f"long window vs rows {act} B={B}")
     sm = _synth("cfg1")
-    B, T = 4, 512
+    T = 512
     toks = np.random.default_rng(5).integers(0, sm.cfg.vocab_size, (B, T))
     model = StepModel(sm, act=act)
     st = model.make_static_state(T, win=T, batch=B, want_probs=True)
