@@ -583,11 +583,14 @@ hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect&
 // Large-tile variant for launches with many rows (encode windows, chunk
 // scoring).  The 16-row tasks above decode every weight block once per 16
 // rows, which makes thousands of row tiles VALU-bound on the code unpacking.
-// Here a workgroup owns BIG_M = 128 rows x BIG_N = 128 columns: the A rows
+// Here a workgroup owns BIG_M = 64 rows x BIG_N = 128 columns: the A rows
 // (bf16, already normalised by norm_rows_kernel where the stage has a
 // prologue) pass through LDS one 256-wide k-block at a time, and each wave
 // decodes its two 16-column weight blocks once per k-step and applies them
-// to all eight 16-row blocks.
+// to all four 16-row blocks.  Two workgroups share a CU: the kernel is bound
+// by latency (weight decode, LDS reads, the scaled accumulation), and the
+// second workgroup's waves hide it; 128-row tiles at one workgroup per CU
+// ran 1.3-1.4x slower, 32-row tiles decode each weight block too often.
 //
 // Bit-identical to gemm_task for the same (NB, KS): every 16x16 output block
 // sees the same MFMA sequence (k-steps in order, one group of two k-steps per
@@ -595,7 +598,7 @@ hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect&
 // slices are added in slice order, and the epilogue runs on 16 x (16*NB)
 // tiles laid out exactly as gemm_task leaves them in LDS.
 // ---------------------------------------------------------------------------
-constexpr int BIG_M = 128, BIG_N = 128, BIG_AST = 256 + 8;  // A k-block LDS row stride (elements)
+constexpr int BIG_M = 64, BIG_N = 128, BIG_AST = 256 + 8;  // A k-block LDS row stride (elements)
 
 template <int NB, int KS>
 __host__ __device__ constexpr size_t big_lds_bytes() {
@@ -606,9 +609,10 @@ __host__ __device__ constexpr size_t big_lds_bytes() {
 }
 
 template <int BITS, int NB, int KS, class Epi>
-// One workgroup per CU: the 8 x 2 accumulator blocks per wave, their K-slice
-// totals and the next k-block's A rows in flight need the whole register file.
-__global__ __launch_bounds__(256, 1) void gemm_big_kernel(QT w, int R, const uint16_t* __restrict__ A,
+// Two workgroups per CU (at most 256 VGPRs a lane): the 4 x 2 accumulator
+// blocks per wave, their K-slice totals, the next k-block's weights and A rows
+// in flight.
+__global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uint16_t* __restrict__ A,
                                                           Epi epi) {
   using Cfg = TileCfg<NB, KS>;
   static_assert(Cfg::THREADS == 256, "the epilogues run on four waves");
@@ -620,7 +624,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(QT w, int R, const uin
   // Workgroups are dealt to the 8 XCDs round-robin by linear id.  Here the A
   // rows are the large operand (the weights of a stage are a few hundred KB),
   // so every column tile of a row tile goes to one XCD, consecutively: the
-  // 128 rows then enter that XCD's L2 once for all column tiles.
+  // tile's rows then enter that XCD's L2 once for all column tiles.
   int cx = blockIdx.x, ry = blockIdx.y;
   if (gridDim.y % 8 == 0) {
     const int bid = blockIdx.x + gridDim.x * blockIdx.y;
@@ -641,12 +645,13 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(QT w, int R, const uin
   load_w(wb[0], w, nb0, 0, lane);
   load_w(wb[1], w, nb0 + 1, 0, lane);
 
-  // A rows m0.. of a k-block: 16-byte chunks, 32 per row, 16 per thread; the
+  // A rows m0.. of a k-block: 16-byte chunks, 32 per row, ACH per thread; the
   // next k-block's chunks are loaded into registers while this one computes
-  u32x4 av[16];
+  constexpr int ACH = BIG_M * 32 / 256;
+  u32x4 av[ACH];
   auto load_a_blk = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < ACH; ++i) {
       const int c = threadIdx.x + 256 * i;
       const int r = c >> 5, k8 = (c & 31) * 8;
       av[i] = (m0 + r < R) ? *(const u32x4*)(A + (int64_t)(m0 + r) * w.K + kb * 256 + k8)
@@ -655,7 +660,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(QT w, int R, const uin
   };
   auto store_a_blk = [&]() {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < ACH; ++i) {
       const int c = threadIdx.x + 256 * i;
       *(u32x4*)(As + (c >> 5) * BIG_AST + (c & 31) * 8) = av[i];
     }
