@@ -315,14 +315,16 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) acc[gi][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // tile T of the K and V caches -> registers (one 16-byte load per lane each)
+  // tile T of the K and V caches -> registers (one 16-byte load per lane each).
+  // Ordinary (temporal) loads: every query block of this (segment, head) reads
+  // the same tiles, and they are meant to stay in L2 between the blocks.
   auto load_t = [&](u32x4 (&kr)[8], u32x4 (&vr)[8], int T) {
     const u32x4* kt = (const u32x4*)(kb + (int64_t)T * (TILE * HD)) + lane;
     const u32x4* vt = (const u32x4*)(vb + (int64_t)T * (TILE * HD)) + lane;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = __builtin_nontemporal_load(kt + 64 * i);
+    for (int i = 0; i < 8; ++i) kr[i] = kt[64 * i];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vr[i] = __builtin_nontemporal_load(vt + 64 * i);
+    for (int i = 0; i < 8; ++i) vr[i] = vt[64 * i];
   };
   auto tile = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8], int T) {
     const int k0 = T * TILE;
@@ -387,20 +389,14 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
       }
     }
   };
-  // Tiles T = wave, wave + 4, ... in order; the next tile's loads are in
-  // flight while the current one is computed (two register buffers), which
-  // at one wave per SIMD is the only latency hiding there is.
-  {
-    u32x4 ka[8], va[8], kn[8], vn[8];
-    int T = wave;
-    if (T < ntiles) load_t(ka, va, T);
-    for (; T < ntiles; T += 2 * ATT_WAVES) {
-      const int T1 = T + ATT_WAVES, T2 = T + 2 * ATT_WAVES;
-      if (T1 < ntiles) load_t(kn, vn, T1);
-      tile(ka, va, T);
-      if (T2 < ntiles) load_t(ka, va, T2);
-      if (T1 < ntiles) tile(kn, vn, T1);
-    }
+  // Tiles T = wave, wave + 4, ... in order, one tile in registers at a time:
+  // that keeps NG = 2 at 164 VGPRs, three waves per SIMD, whose interleaving
+  // hides the load latency far better than a second register buffer at one
+  // wave per SIMD (288 VGPRs; cfg4: 0.93 vs 2.1 ms per slot).
+  for (int T = wave; T < ntiles; T += ATT_WAVES) {
+    u32x4 kr[8], vr[8];
+    load_t(kr, vr, T);
+    tile(kr, vr, T);
   }
   // merge and store, one group of 16 queries at a time (wave w: queries w, w+4, ...)
 #pragma unroll

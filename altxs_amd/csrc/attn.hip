@@ -44,12 +44,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
 }
 
 // Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
-// per workgroup; grid = B x H x ceil(W / (16*NG)).
+// per workgroup; grid = B x H x ceil(W / (16*NG)).  At most 256 VGPRs, so at
+// least two waves share a SIMD (NG <= 2 takes 164: three).
 template <int NG, int NP, int YBF16>
-__global__ __launch_bounds__(ATT_THREADS) void attn_window_kernel(AttnP a) {
+__global__ __launch_bounds__(ATT_THREADS, 2) void attn_window_kernel(AttnP a) {
   __shared__ WinLds sm;
   const int nqb = (a.W + 16 * NG - 1) / (16 * NG);
-  const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id.  Every query
+  // block of a (segment, head) reads the same K/V tiles, so the blocks of one
+  // (segment, head) go to one XCD, consecutively, and its tiles stay in that
+  // XCD's L2 (a bijection of the ids when the grid is a multiple of 8).
+  int L = blockIdx.x;
+  if (gridDim.x % 8 == 0) L = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+  const int qb = L % nqb, bh = L / nqb;
   attn_window_task<NG, NP, YBF16>(a, bh / a.H, bh % a.H, qb * 16 * NG, sm);
 }
 
@@ -172,8 +179,8 @@ hipError_t launch_y(const AttnP& p, int group, bool kv_bf16, bool ops_bf16, bool
   do { hipLaunchKernelGGL(K, grid, block, 0, s, p); return hipGetLastError(); } while (0)
   if (kv_bf16 && p.W > 1 && !rows_only) {
     // 32 query rows per workgroup for longer windows: the 64-row variant needs
-    // more than half the register file (one wave per SIMD) and measured slower
-    // (cfg4: 2.99 vs 2.77 ms per slot); the bits are the same either way
+    // 253 VGPRs (two waves per SIMD) and measured slower (cfg4: 1.17 vs
+    // 0.93 ms per slot); the bits are the same either way
     const int ng = p.W <= 16 ? 1 : 2;
     const int nqb = (p.W + 16 * ng - 1) / (16 * ng);
     dim3 wgrid((unsigned)((int64_t)p.B * p.H * nqb));
