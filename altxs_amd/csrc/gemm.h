@@ -145,12 +145,63 @@ __device__ __forceinline__ float code_center(int bits) {
   else return 0.5f * (float)((1 << BITS) - 1);
 }
 
+// 2- and 3-bit codes by table: every value c - center is exact in bf16, so a
+// byte table of the bf16 bits, read with v_perm_b32, gives the operand with
+// the same bits as the conversion below at about half the VALU work.
+// lut_bytes<BITS>(hi, half): byte i = low (hi = 0) or high byte of
+// bf16(c - center) for c = 4 * half + i (folded to constants).
+template <int BITS>
+__device__ __forceinline__ uint32_t lut_bytes(int hi, int half) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v = (float)(4 * half + i) - 0.5f * (float)((1 << BITS) - 1);
+    const uint32_t b = __builtin_bit_cast(uint32_t, v) >> 16;  // exact: at most 3 mantissa bits
+    w |= ((hi ? b >> 8 : b) & 0xFFu) << (8 * i);
+  }
+  return w;
+}
+// 2-bit fields i = 0..3 (bits 2i, 2i+1 of x < 256) -> byte i
+__device__ __forceinline__ uint32_t spread2to8(uint32_t x) {
+  x = (x | (x << 12)) & 0x000F000Fu;
+  return (x | (x << 6)) & 0x03030303u;
+}
+// bits i = 0..3 of x < 16 -> bit 0 of byte i
+__device__ __forceinline__ uint32_t spread1to8(uint32_t x) {
+  x = (x | (x << 14)) & 0x00030003u;
+  return (x | (x << 7)) & 0x01010101u;
+}
+// Four codes (one per byte of c4) -> two words of bf16 pairs.
+template <int BITS>
+__device__ __forceinline__ void lut4(uint32_t c4, uint32_t& w01, uint32_t& w23) {
+  // v_perm_b32: byte selector k < 4 takes byte k of the second source, 4..7
+  // byte k - 4 of the first
+  const uint32_t lo = __builtin_amdgcn_perm(lut_bytes<BITS>(0, 1), lut_bytes<BITS>(0, 0), c4);
+  const uint32_t hi = __builtin_amdgcn_perm(lut_bytes<BITS>(1, 1), lut_bytes<BITS>(1, 0), c4);
+  w01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
+  w23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
+}
+
 // B operand of k-step s: codes - center.  BITS == 0 expects the 6-bit layout
 // (planes_to6 already applied).
 template <int BITS>
 __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
   if constexpr (BITS == 16)
     return __builtin_bit_cast(bf16x8, u32x4{p0[4 * s], p0[4 * s + 1], p0[4 * s + 2], p0[4 * s + 3]});
+  if constexpr (BITS == 2 || BITS == 3) {
+    static_assert(Planes<BITS>::P0 == 2, "2-bit low plane: k-step s is bits 16 (s & 1) + 2i of p0[s >> 1]");
+    const uint32_t f0 = (p0[s >> 1] >> (16 * (s & 1))) & 0xFFFFu;
+    uint32_t ca = spread2to8(f0 & 0xFFu), cb = spread2to8(f0 >> 8);
+    if constexpr (BITS == 3) {  // third bit: bit 8 (s & 3) + i of p1[s >> 2]
+      const uint32_t f1 = (p1[s >> 2] >> (8 * (s & 3))) & 0xFFu;
+      ca |= spread1to8(f1 & 0xFu) << 2;
+      cb |= spread1to8(f1 >> 4) << 2;
+    }
+    uint32_t r0, r1, r2, r3;
+    lut4<BITS>(ca, r0, r1);
+    lut4<BITS>(cb, r2, r3);
+    return __builtin_bit_cast(bf16x8, u32x4{r0, r1, r2, r3});
+  }
   const float center = code_center<BITS>(bits);
   uint32_t c[8];
   codes_step<BITS == 0 ? 6 : BITS>(p0, p1, s, c);
