@@ -182,6 +182,19 @@ __device__ __forceinline__ void lut4(uint32_t c4, uint32_t& w01, uint32_t& w23) 
   w23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
 }
 
+// (float) of byte M of x.  The compiler folds the byte masks of the 4-bit
+// path below into per-field extracts and then converts from byte 0 only; the
+// instruction itself reads any byte in place.
+template <int M>
+__device__ __forceinline__ float ubyte_f32(uint32_t x) {
+  float r;
+  if constexpr (M == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (M == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (M == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 // B operand of k-step s: codes - center.  BITS == 0 expects the 6-bit layout
 // (planes_to6 already applied).
 template <int BITS>
@@ -201,6 +214,23 @@ __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* 
     lut4<BITS>(ca, r0, r1);
     lut4<BITS>(cb, r2, r3);
     return __builtin_bit_cast(bf16x8, u32x4{r0, r1, r2, r3});
+  }
+  if constexpr (BITS == 4) {
+    // nibbles -> bytes: byte m of ca / cb holds code 2m / 2m + 1, which the
+    // byte conversions (v_cvt_f32_ubyte0..3) read in place; the arithmetic is
+    // the generic path's ((float)c - center, rounded to bf16)
+    const uint32_t w = p0[s];
+    const uint32_t ca = w & 0x0F0F0F0Fu, cb = (w >> 4) & 0x0F0F0F0Fu;
+    bf16x8 r;
+    r[0] = (__bf16)(ubyte_f32<0>(ca) - 7.5f);
+    r[1] = (__bf16)(ubyte_f32<0>(cb) - 7.5f);
+    r[2] = (__bf16)(ubyte_f32<1>(ca) - 7.5f);
+    r[3] = (__bf16)(ubyte_f32<1>(cb) - 7.5f);
+    r[4] = (__bf16)(ubyte_f32<2>(ca) - 7.5f);
+    r[5] = (__bf16)(ubyte_f32<2>(cb) - 7.5f);
+    r[6] = (__bf16)(ubyte_f32<3>(ca) - 7.5f);
+    r[7] = (__bf16)(ubyte_f32<3>(cb) - 7.5f);
+    return r;
   }
   const float center = code_center<BITS>(bits);
   uint32_t c[8];
