@@ -302,7 +302,7 @@ def main() -> int:
     ap.add_argument("--kv", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--streams", type=int, default=1, choices=[1, 2],
-                    help="2: two segment groups on two streams, attention launches alternating")
+                    help="2: two segment groups on two streams, the second chain started half a slot later")
     ap.add_argument("--window", type=int, default=1, metavar="W",
                     help="W > 1: score W-token windows from position 0 (prefill-style "
                          "chunk scoring, cfg4 = --profile cfg4 --window 2048); value = B*W / step")

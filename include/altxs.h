@@ -250,11 +250,12 @@ typedef struct AltxsStepDesc {
    * it: events 2s, 2s+1 for slot s (one group); (g*n_slots + s)*2 + {0,1} for
    * group g in split mode. */
   void **attn_events;
-  /* Split mode (B >= 2): a second stream and 2*n_slots + 2 caller-created
-   * events (hipEventDisableTiming).  Segments [0, ceil(B/2)) run on `stream`,
-   * the rest on aux_stream; their attention launches alternate so one group's
-   * projections and MLP overlap the other group's KV streaming.  Results are
-   * bit-identical to the single-stream step.  NULL = one stream. */
+  /* Split mode (B >= 2): a second stream and at least 2 caller-created
+   * events (hipEventDisableTiming; 2*n_slots + 2 are accepted).  Segments
+   * [0, ceil(B/2)) run on `stream`, the rest on aux_stream, each group's step
+   * one chain; the second starts after the first group's slot-0 QKV, so one
+   * group's projections and MLP overlap the other group's KV streaming.
+   * Results are bit-identical to the single-stream step.  NULL = one stream. */
   void *aux_stream;
   void **sync_events;
   /* Persistent layer kernel (single stream, bf16 KV, W dividing 16): a plan
