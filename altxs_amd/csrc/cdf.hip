@@ -238,94 +238,92 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_chunk_kernel(const float* __re
   }
 }
 
-// Same tables, one workgroup per row: for launches with many rows (encode
-// windows) the chunk kernel's recount of the counts before each chunk is pure
-// overhead.  Thread t owns elements [t*EPT, t*EPT + EPT); M and S are formed
-// exactly as in cdf_chunk_kernel (same threads, same tiles, same order) and p,
-// the counts and their exact integer prefix sums follow, so every table is
-// bit-identical to the chunk kernel's.
-//
-// stats == NULL (launches whose LM head skipped them): the kernel forms each
-// 64-column tile's (max m_t, sum of exp(l - m_t)) itself, exactly as the LM
-// head epilogue does (one tile per wave, column c on lane c, wave_max and
-// wave_sum), from the row staged in LDS.
-template <int EPT, bool OWN_STATS>
+// Inclusive scan over the 64 lanes of a wave (exact integers): DPP row shifts
+// inside each 16-lane row (a lane whose source is across the row edge reads
+// 0), then the totals of the rows before it.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += dpp_u<0x111>(v);  // row_shr:1
+  v += dpp_u<0x112>(v);  // row_shr:2
+  v += dpp_u<0x114>(v);  // row_shr:4
+  v += dpp_u<0x118>(v);  // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const int rw = (threadIdx.x % WAVE) >> 4;
+  return v + (rw > 0 ? r0 : 0u) + (rw > 1 ? r1 : 0u) + (rw > 2 ? r2 : 0u);
+}
+
+// One workgroup per row, the row in registers: wave w holds the 64-column
+// tiles w, w + 16, ... (TPW of them), column c of a tile on lane c -- the
+// layout of the LM-head epilogue's tile statistics, which (stats == NULL) the
+// kernel forms itself with the same wave_max / wave_sum.  M and S come from
+// the tile statistics exactly as in cdf_chunk_kernel; each count is the same
+// elementwise function of its logit; the table is the exact integer prefix
+// (in-tile wave scans plus the exclusive prefix of the tile totals), so the
+// tables equal the chunk kernel's.  Loads and stores are 64 consecutive words
+// per wave instruction; LDS holds only the tile statistics and totals.
+template <int TPW>
 __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __restrict__ logits,
                                                               const float2* __restrict__ stats,
                                                               int V, float* __restrict__ probs,
                                                               uint32_t* __restrict__ cum) {
-  static_assert(EPT % 4 == 0, "whole 16-byte vectors per thread");
+  constexpr int NT = CH_WAVES * TPW;  // tiles of the row (V / 64, host check)
+  static_assert(NT <= 4 * WAVE, "one wave forms the prefix of the tile totals");
   __shared__ float red[CH_WAVES];
-  __shared__ uint32_t wred[CH_WAVES];
-  extern __shared__ __attribute__((aligned(16))) float srow[];  // [V] (+ [V/64] float2 stats)
+  __shared__ float2 sst[NT];
+  __shared__ uint32_t tex[NT];
   const int64_t row = blockIdx.x;
-  const int t = threadIdx.x;
-  const int base = t * EPT;
-  const bool mine = base < V;  // V % EPT == 0 (host check)
+  const int t = threadIdx.x, w = t / WAVE, l = t % WAVE;
   const float* x = logits + row * (int64_t)V;
-  f32x4 v[EPT / 4];
+  float v[TPW];
 #pragma unroll
-  for (int k = 0; k < EPT / 4; ++k)
-    v[k] = mine ? __builtin_nontemporal_load((const f32x4*)(x + base) + k) : f32x4{0.f, 0.f, 0.f, 0.f};
-  const int ntile = V / 64;
-  const float2* st = stats + row * (int64_t)ntile;
-  if constexpr (OWN_STATS) {
-    float2* sst = (float2*)(srow + V);
-    if (mine) {
+  for (int j = 0; j < TPW; ++j) v[j] = __builtin_nontemporal_load(x + 64 * (w + CH_WAVES * j) + l);
+  const float2* st = stats ? stats + row * (int64_t)NT : sst;
+  if (!stats) {
 #pragma unroll
-      for (int k = 0; k < EPT / 4; ++k) *((f32x4*)(srow + base) + k) = v[k];
+    for (int j = 0; j < TPW; ++j) {
+      const float m = wave_max(v[j]);
+      const float e = wave_sum(v[j] == -INFINITY ? 0.f : __expf(v[j] - m));
+      if (l == 0) sst[w + CH_WAVES * j] = make_float2(m, e);
     }
     __syncthreads();
-    const int w = t / WAVE, l = t % WAVE;
-    for (int i = w; i < ntile; i += CH_WAVES) {  // uniform per wave
-      const float lv = srow[64 * i + l];
-      const float m = wave_max(lv);
-      const float e = wave_sum(lv == -INFINITY ? 0.f : __expf(lv - m));
-      if (l == 0) sst[i] = make_float2(m, e);
-    }
-    __syncthreads();
-    st = sst;
   }
   float mt = -INFINITY;
-  for (int i = t; i < ntile; i += CH_THREADS) mt = fmaxf(mt, st[i].x);
+  for (int i = t; i < NT; i += CH_THREADS) mt = fmaxf(mt, st[i].x);
   const float M = block_max_n(mt, red);
   float sp = 0.f;
-  for (int i = t; i < ntile; i += CH_THREADS) {
+  for (int i = t; i < NT; i += CH_THREADS) {
     const float2 q = st[i];
     sp += q.y * __expf(q.x - M);
   }
   const float S = block_sum_n(sp, red);
   const float iS = 1.f / S;
-  uint32_t f[EPT];
-  uint32_t tot = 0;
+  uint32_t inc[TPW];
 #pragma unroll
-  for (int k = 0; k < EPT / 4; ++k) {
-    f32x4 p;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      p[e] = __expf(v[k][e] - M) * iS;
-      f[4 * k + e] = mine ? scale_count(p[e]) : 0u;
-      tot += f[4 * k + e];
-    }
-    if (probs && mine) *((f32x4*)(probs + row * (int64_t)V + base) + k) = p;
+  for (int j = 0; j < TPW; ++j) {
+    const float p = __expf(v[j] - M) * iS;
+    if (probs) probs[row * (int64_t)V + 64 * (w + CH_WAVES * j) + l] = p;
+    inc[j] = wave_incl_scan_u32(scale_count(p));
+    if (l == WAVE - 1) tex[w + CH_WAVES * j] = inc[j];
   }
-  uint32_t run = block_excl_scan(tot, wred);
-  // The table goes out through LDS so that each store instruction writes 64
-  // consecutive words (a thread's own 16 values are 64 bytes apart from its
-  // neighbours', and co + 1 is only 4-byte aligned).
-  uint32_t* scum = (uint32_t*)srow;
-  __syncthreads();  // srow (OWN_STATS) is no longer read
-  if (mine) {
+  __syncthreads();
+  if (w == 0) {  // tile totals -> exclusive prefix, tiles 4l .. 4l+3 on lane l
+    uint32_t a[4];
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-      run += f[k];
-      scum[base + k] = run;
+    for (int k = 0; k < 4; ++k) a[k] = 4 * l + k < NT ? tex[4 * l + k] : 0u;
+    const uint32_t s4 = a[0] + a[1] + a[2] + a[3];
+    uint32_t run = wave_incl_scan_u32(s4) - s4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (4 * l + k < NT) tex[4 * l + k] = run;
+      run += a[k];
     }
   }
   __syncthreads();
   uint32_t* co = cum + row * (int64_t)(V + 1);
   if (t == 0) co[0] = 0u;
-  for (int i = t; i < V; i += CH_THREADS) co[i + 1] = scum[i];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) co[1 + 64 * (w + CH_WAVES * j) + l] = tex[w + CH_WAVES * j] + inc[j];
 }
 
 template <bool FROM_LOGITS>
@@ -363,33 +361,15 @@ hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int6
   if (V % 64) return hipErrorInvalidValue;
   if (altxs_cdf_rows_kernel(rows, V)) {
     // many rows: one workgroup per row (bit-identical tables, no recount); with
-    // stats == NULL it forms the tile statistics itself from the row in LDS
-    // dynamic LDS: the table staging (and, forming the statistics, the row and its stats)
-    const size_t lds = (size_t)V * 4 + (stats ? 0 : (size_t)(V / 64) * 8);
-#define ROW_GO(E)                                                                              \
-  do {                                                                                         \
-    static bool configured = false;                                                            \
-    if (!configured) {                                                                         \
-      const int most = (int)(16 * CH_THREADS * 4 + 16 * CH_THREADS / 8);                       \
-      hipError_t e = hipFuncSetAttribute((const void*)cdf_row_kernel<E, true>,                 \
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, most);    \
-      if (e == hipSuccess)                                                                     \
-        e = hipFuncSetAttribute((const void*)cdf_row_kernel<E, false>,                         \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, most);             \
-      if (e != hipSuccess) return e;                                                           \
-      configured = true;                                                                       \
-    }                                                                                          \
-    if (stats)                                                                                 \
-      hipLaunchKernelGGL((cdf_row_kernel<E, false>), dim3((unsigned)rows), dim3(CH_THREADS),   \
-                         lds, s, logits, stats, V, probs, cum);                                \
-    else                                                                                       \
-      hipLaunchKernelGGL((cdf_row_kernel<E, true>), dim3((unsigned)rows), dim3(CH_THREADS),    \
-                         lds, s, logits, stats, V, probs, cum);                                \
-  } while (0)
-    if (V <= 4 * CH_THREADS) ROW_GO(4);
-    else if (V <= 8 * CH_THREADS) ROW_GO(8);
-    else ROW_GO(16);
-#undef ROW_GO
+    // stats == NULL it forms the tile statistics itself
+    const dim3 grid((unsigned)rows), block(CH_THREADS);
+    switch (V / (64 * CH_WAVES)) {  // tiles per wave
+      case 4: hipLaunchKernelGGL(cdf_row_kernel<4>, grid, block, 0, s, logits, stats, V, probs, cum); break;
+      case 8: hipLaunchKernelGGL(cdf_row_kernel<8>, grid, block, 0, s, logits, stats, V, probs, cum); break;
+      case 12: hipLaunchKernelGGL(cdf_row_kernel<12>, grid, block, 0, s, logits, stats, V, probs, cum); break;
+      case 16: hipLaunchKernelGGL(cdf_row_kernel<16>, grid, block, 0, s, logits, stats, V, probs, cum); break;
+      default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
   }
   if (!stats) return hipErrorInvalidValue;
