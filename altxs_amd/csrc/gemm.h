@@ -681,6 +681,12 @@ hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect&
 // ---------------------------------------------------------------------------
 constexpr int BIG_M = 64, BIG_N = 128, BIG_AST = 256 + 8;  // A k-block LDS row stride (elements)
 
+// Epilogues that also offer strip<Cfg>(strip C tile, r0, n0, R) -- the same
+// per-element arithmetic over a 16 x BIG_N strip -- set kStrip.
+template <class E, class = void> struct epi_has_strip : std::false_type {};
+template <class E>
+struct epi_has_strip<E, std::void_t<decltype(E::kStrip)>> : std::integral_constant<bool, E::kStrip> {};
+
 template <int NB, int KS>
 __host__ __device__ constexpr size_t big_lds_bytes() {
   using Cfg = TileCfg<NB, KS>;
@@ -834,6 +840,14 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
         C[(4 * (lane >> 4) + i) * Cfg::CS + col % Cfg::NCOL] = tot[mb][j][i];
     }
   __syncthreads();
+  if constexpr (epi_has_strip<Epi>::value) {  // whole 16 x 128 strips, vector accesses
+    for (int mb = 0; mb < MB; ++mb) {
+      const int r0 = m0 + 16 * mb;
+      if (r0 >= R) break;  // uniform
+      epi.template strip<Cfg>(Cs + (size_t)mb * NSUB * 16 * Cfg::CS, r0, n0, R);
+    }
+    return;
+  }
   for (int mb = 0; mb < MB; ++mb) {
     const int r0 = m0 + 16 * mb;
     if (r0 >= R) break;  // uniform

@@ -319,17 +319,58 @@ struct NextIn {
     e.sg = skip_g ? skip_g[c] : 0.f;
     return e;
   }
-  __device__ void put(int64_t idx, float x, const El& e) const {
+  struct Out { float base, attn; };
+  __device__ Out calc(float x, const El& e) const {
     float bs = x;
     if (skip) {
       const float sc = e.sw * (skip_self ? x : e.sk);
       bs = skip_g ? lerp_t(sc, x, sigmoidf(e.sg)) : x + sc;
     }
     const float in = e.m0 * bs + e.m1 * e.x0;
-    base[idx] = parallel ? bs : in;
-    if (attn != base) attn[idx] = in;
+    return {parallel ? bs : in, in};
+  }
+  __device__ void put(int64_t idx, float x, const El& e) const {
+    const Out o = calc(x, e);
+    base[idx] = o.base;
+    if (attn != base) attn[idx] = o.attn;
   }
 };
+
+// ---- per-element arithmetic of the O / UP / DOWN epilogues -----------------
+// Shared by apply() (tiles of the 16-row tasks) and strip() (16 x 128 strips
+// of the large-tile kernel), so both paths compile to the same operations.
+__device__ __forceinline__ float o_el(float c, float sc, float base, int parallel) {
+  const float a = sc * c;
+  return parallel ? a : base + a;
+}
+__device__ __forceinline__ float up_el(float v) {
+  const float lr = v > 0.f ? v : 0.5f * v;
+  return lr * lr;
+}
+struct DownOut { float x, x1; };
+__device__ __forceinline__ DownOut down_el(float c, float sc, float xo, float l0, float l1, int parallel,
+                                           const float* pr, const float* pp) {
+  const float m = sc * c;
+  if (!parallel) return {xo + m, 0.f};
+  return {pr[0] * l0 + pp[0] * xo + pp[2] * m, pr[1] * l1 + pp[1] * xo + pp[3] * m};
+}
+
+// Strips (large-tile kernel, 256 threads): 16 rows x 128 columns, thread t
+// on row t / 16, columns 8 (t % 16) .. +8 -- one sub-tile of the LDS C layout
+// (16 x NCOL tiles, stride CS) -- with 16- and 32-byte vector accesses.
+template <class Cfg>
+__device__ __forceinline__ const float* strip_src(const float* Cst, int rr, int c8) {
+  return Cst + (size_t)(c8 / Cfg::NCOL) * 16 * Cfg::CS + rr * Cfg::CS + c8 % Cfg::NCOL;
+}
+__device__ __forceinline__ void ld8(float (&v)[8], const float* p) {
+  const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
+}
+__device__ __forceinline__ void st8(float* p, const float (&v)[8]) {
+  *(f32x4*)p = f32x4{v[0], v[1], v[2], v[3]};
+  *(f32x4*)(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
 
 // ---- epilogues --------------------------------------------------------------
 
@@ -530,9 +571,22 @@ struct EpiO {
       const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
       const int r = m0 + rr, c = n0 + cc;
       if (r >= R || c >= D) continue;
-      const float a = pre.sc[j] * C[rr * Cfg::CS + cc];
-      xout[(int64_t)r * D + c] = parallel ? a : pre.base[j] + a;
+      xout[(int64_t)r * D + c] = o_el(C[rr * Cfg::CS + cc], pre.sc[j], pre.base[j], parallel);
     }
+  }
+  static constexpr bool kStrip = true;
+  template <class Cfg>
+  __device__ void strip(const float* Cst, int r0, int n0, int R) const {
+    const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
+    if (r >= R) return;
+    const float* cs = strip_src<Cfg>(Cst, rr, c8);
+    const int64_t o = (int64_t)r * D + n0 + c8;
+    float sc[8], base[8], out[8];
+    ld8(sc, attn_scale + n0 + c8);
+    if (!parallel) ld8(base, xin + o);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = o_el(cs[i], sc[i], parallel ? 0.f : base[i], parallel);
+    st8(xout + o, out);
   }
 };
 
@@ -549,12 +603,30 @@ struct EpiUp {
       const int rr = EW<Cfg>::row(j), cc = EW<Cfg>::col(j);
       const int r = m0 + rr, c = n0 + cc;
       if (r >= R || c >= F) continue;
-      const float v = C[rr * Cfg::CS + cc];
-      const float lr = v > 0.f ? v : 0.5f * v;
-      const float o = lr * lr;
+      const float o = up_el(C[rr * Cfg::CS + cc]);
       const int64_t idx = (int64_t)r * F + c;
       if (hb16) ((uint16_t*)h)[idx] = f32_to_bf16(o);
       else ((float*)h)[idx] = o;
+    }
+  }
+  static constexpr bool kStrip = true;
+  template <class Cfg>
+  __device__ void strip(const float* Cst, int r0, int n0, int R) const {
+    const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
+    if (r >= R) return;
+    const float* cs = strip_src<Cfg>(Cst, rr, c8);
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = up_el(cs[i]);
+    const int64_t idx = (int64_t)r * F + n0 + c8;
+    if (hb16) {
+      u32x4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16(o[2 * i]) | ((uint32_t)f32_to_bf16(o[2 * i + 1]) << 16);
+      *(u32x4*)((uint16_t*)h + idx) = w;
+    } else {
+      st8((float*)h + idx, o);
     }
   }
 };
@@ -598,18 +670,57 @@ struct EpiDown {
       const int r = m0 + rr, c = n0 + cc;
       if (r >= R || c >= D) continue;
       const int64_t o = (int64_t)r * D + c;
-      const float m = pre.sc[j] * C[rr * Cfg::CS + cc];
-      float x;
-      if (!parallel) {
-        x = pre.xo[j] + m;
-        out0[o] = x;
-      } else {
-        const float a = pre.xo[j];
-        x = pr[0] * pre.l0[j] + pp[0] * a + pp[2] * m;
-        out0[o] = x;
-        out1[o] = pr[1] * pre.l1[j] + pp[1] * a + pp[3] * m;
+      const DownOut y = down_el(C[rr * Cfg::CS + cc], pre.sc[j], pre.xo[j], pre.l0[j], pre.l1[j],
+                                parallel, pr, pp);
+      out0[o] = y.x;
+      if (parallel) out1[o] = y.x1;
+      if (next.base) next.put(o, y.x, pre.nx[j]);
+    }
+  }
+  static constexpr bool kStrip = true;
+  template <class Cfg>
+  __device__ void strip(const float* Cst, int r0, int n0, int R) const {
+    const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
+    if (r >= R) return;
+    const float* cs = strip_src<Cfg>(Cst, rr, c8);
+    const int c = n0 + c8;
+    const int64_t o = (int64_t)r * D + c;
+    float sc[8], xo[8], l0[8], l1[8], x[8], x1[8];
+    ld8(sc, mlp_scale + c);
+    ld8(xo, xout + o);
+    if (parallel) {
+      ld8(l0, lane0 + o);
+      ld8(l1, lane1 + o);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l0[i] = l1[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const DownOut y = down_el(cs[i], sc[i], xo[i], l0[i], l1[i], parallel, pr, pp);
+      x[i] = y.x;
+      x1[i] = y.x1;
+    }
+    st8(out0 + o, x);
+    if (parallel) st8(out1 + o, x1);
+    if (next.base) {  // the next slot's inputs (NextIn::load / put, eight at a time)
+      float ex0[8], em0[8], em1[8], esk[8], esw[8], esg[8], ob[8], oa[8];
+      ld8(ex0, next.x0 + o);
+      ld8(em0, next.mix + c);
+      ld8(em1, next.mix + D + c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) esk[i] = esw[i] = esg[i] = 0.f;
+      if (next.skip && !next.skip_self) ld8(esk, next.skip + o);
+      if (next.skip) ld8(esw, next.skip_w + c);
+      if (next.skip_g) ld8(esg, next.skip_g + c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const NextIn::Out q = next.calc(x[i], NextIn::El{ex0[i], esk[i], esw[i], esg[i], em0[i], em1[i]});
+        ob[i] = q.base;
+        oa[i] = q.attn;
       }
-      if (next.base) next.put(o, x, pre.nx[j]);
+      st8(next.base + o, ob);
+      if (next.attn != next.base) st8(next.attn + o, oa);
     }
   }
 };
