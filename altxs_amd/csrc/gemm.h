@@ -682,7 +682,8 @@ hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect&
 constexpr int BIG_M = 64, BIG_N = 128, BIG_AST = 256 + 8;  // A k-block LDS row stride (elements)
 
 // Epilogues that also offer strip<Cfg>(strip C tile, r0, n0, R) -- the same
-// per-element arithmetic over a 16 x BIG_N strip -- set kStrip.
+// per-element arithmetic over a 16 x BIG_N strip, used when strip_ok() -- set
+// kStrip.
 template <class E, class = void> struct epi_has_strip : std::false_type {};
 template <class E>
 struct epi_has_strip<E, std::void_t<decltype(E::kStrip)>> : std::integral_constant<bool, E::kStrip> {};
@@ -841,12 +842,14 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
     }
   __syncthreads();
   if constexpr (epi_has_strip<Epi>::value) {  // whole 16 x 128 strips, vector accesses
-    for (int mb = 0; mb < MB; ++mb) {
-      const int r0 = m0 + 16 * mb;
-      if (r0 >= R) break;  // uniform
-      epi.template strip<Cfg>(Cs + (size_t)mb * NSUB * 16 * Cfg::CS, r0, n0, R);
+    if (epi.strip_ok()) {  // uniform
+      for (int mb = 0; mb < MB; ++mb) {
+        const int r0 = m0 + 16 * mb;
+        if (r0 >= R) break;  // uniform
+        epi.template strip<Cfg>(Cs + (size_t)mb * NSUB * 16 * Cfg::CS, r0, n0, R);
+      }
+      return;
     }
-    return;
   }
   for (int mb = 0; mb < MB; ++mb) {
     const int r0 = m0 + 16 * mb;

@@ -575,6 +575,7 @@ struct EpiO {
     }
   }
   static constexpr bool kStrip = true;
+  __device__ bool strip_ok() const { return true; }
   template <class Cfg>
   __device__ void strip(const float* Cst, int r0, int n0, int R) const {
     const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
@@ -610,6 +611,7 @@ struct EpiUp {
     }
   }
   static constexpr bool kStrip = true;
+  __device__ bool strip_ok() const { return true; }
   template <class Cfg>
   __device__ void strip(const float* Cst, int r0, int n0, int R) const {
     const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
@@ -678,6 +680,7 @@ struct EpiDown {
     }
   }
   static constexpr bool kStrip = true;
+  __device__ bool strip_ok() const { return true; }
   template <class Cfg>
   __device__ void strip(const float* Cst, int r0, int n0, int R) const {
     const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
@@ -725,6 +728,11 @@ struct EpiDown {
   }
 };
 
+__device__ __forceinline__ float softcap_el(float l, float cp, float cn, float icp, float icn) {
+  const bool pos = l >= 0.f;
+  return (pos ? cp : cn) * tanh_fast(l * (pos ? icp : icn));
+}
+
 // Softcapped logits, plus per (row, 64-column tile) softmax statistics
 // (tile max m and sum of exp(l - m)) for the row-parallel CDF kernel.
 struct EpiLogits {
@@ -754,9 +762,7 @@ struct EpiLogits {
       const int r = m0 + rr, c = n0 + cc;
       v[j] = -INFINITY;
       if (r < R && c < V) {
-        const float l = C[rr * Cfg::CS + cc];
-        const bool pos = l >= 0.f;
-        v[j] = (pos ? pre.cp : pre.cn) * tanh_fast(l * (pos ? pre.icp : pre.icn));
+        v[j] = softcap_el(C[rr * Cfg::CS + cc], pre.cp, pre.cn, pre.icp, pre.icn);
         logits[(int64_t)r * V + c] = v[j];
       }
     }
@@ -776,6 +782,20 @@ struct EpiLogits {
         }
       }
     }
+  }
+  // strips only without tile statistics (the CDF kernel then forms them)
+  static constexpr bool kStrip = true;
+  __device__ bool strip_ok() const { return stats == nullptr; }
+  template <class Cfg>
+  __device__ void strip(const float* Cst, int r0, int n0, int R) const {
+    const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
+    if (r >= R) return;
+    const float* cs = strip_src<Cfg>(Cst, rr, c8);
+    const Pre<Cfg> pre = prefetch<Cfg>(0, 0, 0, 0);
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = softcap_el(cs[i], pre.cp, pre.cn, pre.icp, pre.icn);
+    st8(logits + (int64_t)r * V + n0 + c8, o);
   }
 };
 
