@@ -471,6 +471,88 @@ struct EpiQKV {
     }
   }
 
+  // Strips of the large-tile kernel (two heads of 16 rows): 8 threads per head
+  // row, 8 consecutive columns each.  The RMS sum keeps apply()'s order: the
+  // two 4-column partial sums of a thread are apply()'s lanes 2k and 2k + 1,
+  // which its first butterfly step (XOR 1) adds; its remaining steps (XOR 2,
+  // half-row mirror, row mirror over 16 lanes of 4 columns) pair the same
+  // lanes as XOR 1, quad reversal and half-row mirror over these 8 threads.
+  // The RoPE partner (rd / 2 columns away, a multiple of 8) is rd / 16
+  // threads away.  Without LoRA, bf16 cache only.
+  static constexpr bool kStrip = true;
+  __device__ bool strip_ok() const { return rank == 0 && kv_bf16 && rd % 16 == 0 && rd <= HD; }
+  template <class Cfg>
+  __device__ void strip(const float* Cst, int r0, int n0, int R) const {
+    const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
+    const int cw = c8 % HD, nt = (n0 + c8) / HD;
+    const int kind = nt < H ? 0 : (nt < H + Hkv ? 1 : 2);
+    const int head = kind == 0 ? nt : (kind == 1 ? nt - H : nt - H - Hkv);
+    const float* cs = strip_src<Cfg>(Cst, rr, c8);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = cs[i];
+    // every lane takes part in the DPP steps (rows past R included)
+    const int p = r < R ? row_pos(pos, W, r) : 0;
+    const bool pos_ok = p >= 0 && p < max_len;
+    if (kind < 2) {
+      float sa = 0.f, sb = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sa += v[i] * v[i];
+#pragma unroll
+      for (int i = 4; i < 8; ++i) sb += v[i] * v[i];
+      float ss = sa + sb;
+      ss += dpp_f<DPP_XOR1>(ss);
+      ss += dpp_f<0x1B>(ss);  // quad_perm [3, 2, 1, 0]
+      ss += dpp_f<DPP_HALF_MIRROR>(ss);
+      const float inv = rsqrtf(ss * (1.0f / HD) + eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] *= inv;
+      const int half = rd >> 1, off = half / 8;
+      const int pp = pos_ok ? p : 0;
+      float pv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float up = __shfl_down(v[i], off, WAVE);
+        const float dn = __shfl_up(v[i], off, WAVE);
+        pv[i] = (cw < half) ? up : dn;
+      }
+      if (cw < rd) {
+        const int fi = cw < half ? cw : cw - half;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float cs_ = cosb[(int64_t)pp * half + fi + i], sn_ = sinb[(int64_t)pp * half + fi + i];
+          if (cw < half) v[i] = v[i] * cs_ + pv[i] * sn_;
+          else v[i] = pv[i] * -sn_ + v[i] * cs_;
+        }
+      }
+    }
+    if (r >= R) return;
+    if (kind == 0) {
+      const float g = q_gain[nt];
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = v[i] * g;
+      st8(q + ((int64_t)r * H + head) * HD + cw, o);
+    } else if (pos_ok) {
+      const int b = r / W;
+      const int64_t head_base = (((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len * HD;
+      uint16_t* tile = (uint16_t*)kv + head_base + (int64_t)(p / ALTXS_KV_TILE) * (ALTXS_KV_TILE * HD);
+      const int kt = p % ALTXS_KV_TILE;
+      if (kind == 1) {  // K: dims cw .. cw+7 are one 16-byte run of the tile
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+        *(u32x4*)(tile + kv_tile_k(kt, cw)) = w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tile[kv_tile_v(kt, cw + i)] = f32_to_bf16(v[i]);
+      }
+    } else if (cw == 0) {
+      flag_err(err, ALTXS_EDEV_POS);
+    }
+  }
+
   template <class Cfg, class P>
   __device__ void apply(const float* C, const P& pre, const void* As, int m0, int n0, int R,
                         int) const {
