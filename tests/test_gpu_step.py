@@ -175,16 +175,18 @@ def test_dense_cdf_bit_identical_decode_encode(act):
     assert np.array_equal(cmb[0], cm1[0])
 
 
-@pytest.mark.parametrize("act,B", [("bf16", 4), ("fp32", 4), ("bf16", 2)])
-def test_long_window_bit_identical_to_rows(act, B):
+@pytest.mark.parametrize("profile,act,B", [("cfg1", "bf16", 4), ("cfg1", "fp32", 4), ("cfg1", "bf16", 2),
+                                            ("tiny", "bf16", 4)])
+def test_long_window_bit_identical_to_rows(profile, act, B):
     """A 512-token window per segment gives the logits and tables of 512
-    decode rows: 2048 rows take the launch shapes of chunk scoring (128 x 128
-    GEMM tiles, one workgroup per CDF row forming its own tile statistics),
-    1024 rows the 16-row GEMMs with one workgroup per CDF row."""
+    decode rows: 2048 bf16 rows take the launch shapes of chunk scoring (64 x
+    128 GEMM tiles with strip epilogues, one workgroup per CDF row forming its
+    own tile statistics), 1024 rows the 16-row GEMMs.  "tiny" adds parallel
+    lanes, skips popped from earlier slots, depth loops and GQA to the strips."""
     from altxs_amd.model import StepModel
 
-    _log(f"long window vs rows {act} B={B}")
-    sm = _synth("cfg1")
+    _log(f"long window vs rows {profile} {act} B={B}")
+    sm = _synth(profile)
     T = 512
     toks = np.random.default_rng(5).integers(0, sm.cfg.vocab_size, (B, T))
     model = StepModel(sm, act=act)
