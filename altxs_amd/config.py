@@ -116,7 +116,7 @@ def slot_itinerary(cfg: AltxsConfig) -> tuple[list[int], list[int]]:
 
 
 def make_config(profile: str = "large", **overrides) -> AltxsConfig:
-    """Profiles of the reference (config.py:195-228) plus the BASELINE configs."""
+    """Profiles of the reference (config.py:195-228) plus the benchmark configs cfg1-cfg5."""
     cfg = AltxsConfig()
     p = profile.strip().lower()
     if p == "large":

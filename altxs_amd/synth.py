@@ -138,7 +138,7 @@ def make_model(cfg: AltxsConfig, *, seed: int = WEIGHT_SEED, std: float = 0.02,
             small[f"blocks.{i}.attn.attn_gate_w"] = noise(H, gw, scale=0.3)
     if cfg.lora_rank > 0:
         # per-slot q/v adapters (TTTLoRA.q_loras/v_loras, ttt_lora.py:64-120), fp16
-        # values N(0, 0.01^2) for A and B (BASELINE cfg5; the reference starts B at 0)
+        # values N(0, 0.01^2) for A and B (benchmark cfg5; the reference starts B at 0)
         lrng = np.random.default_rng(seed + 2)
         r = cfg.lora_rank
         for sl in range(len(enc) + len(dec)):

@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Workload ("cfg3"): a ~40M-weight GPT (10 layers, d=512,
+Workload (benchmark config "cfg3"): a ~40M-weight GPT (10 layers, d=512,
 8 heads MHA of 64, FFN 2048, V=16384, mixed 2/3/4/6-bit group-64 weights at
 ~3.16 bpw) scoring one symbol for each of 64 independent segments whose KV
 caches hold 2047 previous tokens, so every attention row reads 2048 keys.  A
@@ -129,7 +129,7 @@ def cpu_baseline(sm, ctx: int, seconds: float, seed: int = 0) -> dict:
 
 def window_bench(a) -> int:
     """--window W > 1: one step scores W tokens of each of B segments from position 0
-    (the prefill-style chunk scoring of BASELINE cfg4: causal attention over the
+    (the prefill-style chunk scoring of benchmark cfg4: causal attention over the
     chunk, MFMA GEMMs, one CDF per token).  MFMA-bound, so ``roofline`` is in
     TFLOP/s against the dense bf16 peak."""
     import numpy as np
@@ -323,8 +323,8 @@ def main() -> int:
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
-        print("bench.py: this build runs on one GPU only (independent segments shard across GPUs "
-              "with no communication; see DESIGN.md); --gpus must be 1", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (independent segments would shard "
+              "across GPUs with no per-step communication); --gpus must be 1", file=sys.stderr)
         return 2
 
     import numpy as np

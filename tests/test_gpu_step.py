@@ -1,7 +1,7 @@
 """GPU parity of the whole per-symbol step (altxs_step through the C-ABI).
 
 * logits within 2e-3 absolute of the fp32 CPU oracle in the fp32 mode and in
-  the fp32-activation / bf16-KV mode (at the BASELINE weight scale, std 0.02);
+  the fp32-activation / bf16-KV mode (at the benchmark weight scale, std 0.02);
 * full bf16 mode against the oracle's bf16-rounding emulation: the rounding
   points match, but fp32 values one ulp apart can round to different bf16
   neighbours, and q_gain/attention amplify such flips.  Perturbing the
@@ -25,7 +25,7 @@ LOGIT_TOL = 2e-3  # north-star logit tolerance (absolute)
 CASES = {
     # profile: (B segments, T steps, weight std, softcap)
     "tiny": (3, 12, 0.08, (2.0, 1.5)),     # every motif feature, large activations
-    "cfg1": (2, 16, 0.02, (30.0, 24.0)),   # BASELINE cfg1 weights (std 0.02)
+    "cfg1": (2, 16, 0.02, (30.0, 24.0)),   # benchmark cfg1 weights (std 0.02)
     # the same with unmerged per-slot q/v LoRA (rank 8 exercises rank < 16)
     "tiny_lora": (3, 12, 0.08, (2.0, 1.5)),
     "cfg1_lora": (2, 16, 0.02, (30.0, 24.0)),
