@@ -36,6 +36,9 @@ LORA = {"tiny_lora": ("tiny", dict(lora_rank=8, lora_alpha=12.0)),
 # reference's default student (17 slots with loops, GQA, parallel lanes, V=256)
 CASES.update({"tiny_dense": (3, 12, 0.08, (2.0, 1.5)), "large_dense": (2, 10, 0.02, (30.0, 24.0))})
 DENSE = {"tiny_dense": "tiny", "large_dense": "large"}
+# other vocabularies (the row CDF kernel's 8 and 12 tiles per wave)
+CASES.update({"cfg1_v8k": (2, 6, 0.02, (30.0, 24.0)), "cfg1_v12k": (2, 6, 0.02, (30.0, 24.0))})
+VOCAB = {"cfg1_v8k": ("cfg1", dict(vocab_size=8192)), "cfg1_v12k": ("cfg1", dict(vocab_size=12288))}
 _MODELS: dict = {}
 
 
@@ -49,7 +52,7 @@ def _synth(profile):
         from altxs_amd.config import make_config
 
         B, T, std, cap = CASES[profile]
-        base, over = LORA.get(profile, (DENSE.get(profile, profile), {}))
+        base, over = LORA.get(profile, VOCAB.get(profile, (DENSE.get(profile, profile), {})))
         cfg = make_config(base, **over)
         _MODELS[profile] = synth.make_model(cfg, std=std, softcap=cap, dense=profile in DENSE)
     return _MODELS[profile]
@@ -246,11 +249,11 @@ def test_positions_and_state_advance():
     assert int(st.err.item()) == 0
 
 
-@pytest.mark.parametrize("profile", ["tiny", "cfg1"])
+@pytest.mark.parametrize("profile", ["tiny", "cfg1", "cfg1_v8k", "cfg1_v12k"])
 def test_step_probs_and_cdf_rule(profile):
     """The step's probabilities are a softmax of its logits, and its integer CDFs
-    are exactly _scale_cum_np of those probabilities (row-parallel CDF kernel:
-    V=256 in one chunk, V=4096 in two)."""
+    are exactly _scale_cum_np of those probabilities (V=256: the chunk kernel;
+    V=4096/8192/12288: the row kernel with 4/8/12 tiles per wave)."""
     from oracle import coder
 
     _log(f"probs/cdf rule {profile}")
