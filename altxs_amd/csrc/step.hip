@@ -258,7 +258,10 @@ struct StepRun {
     p.smear_w = d->smear_w; p.smear_lambda = d->smear_lambda; p.x0 = w.X0; p.err = d->err;
     p.sync = w.SYNC; p.nsync = w.nsync;
     p.mix0 = d->layers[d->slots[0].layer].resid_mix; p.xin0 = w.XIN;
-    hipLaunchKernelGGL(embed_kernel, dim3(G.nb * d->W), dim3(64), 0, st, p);
+    p.R = G.nb * d->W;
+    // many rows: four per workgroup (cfg4: 0.68 ms with one-wave workgroups)
+    const int rpw = p.R >= 4096 ? 4 : 1;
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((p.R + rpw - 1) / rpw)), dim3(64 * rpw), 0, st, p);
     return hipGetLastError();
   }
 

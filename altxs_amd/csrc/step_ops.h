@@ -98,12 +98,16 @@ struct EmbedP {
   int nsync;
   const float* mix0;  // resid_mix of slot 0's layer [2, D]
   float* xin0;        // slot 0's x_in = m0*x0 + m1*x0 (sequential, no skip)
+  int R;              // rows (B * W)
 };
 
 constexpr int MAX_RUNS = 4;  // D <= 64 lanes * 4 runs * 8 = 2048
 
-__global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
-  const int r = blockIdx.x, lane = threadIdx.x;
+// One wave per row; a workgroup holds blockDim.x / 64 rows (only wave-level
+// reductions, so the launch shape changes no bits).
+__global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
+  const int r = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64, lane = threadIdx.x % 64;
+  if (r >= a.R) return;
   if (r == 0)
     for (int i = lane; i < a.nsync; i += 64) a.sync[i] = 0;
   const int b = r / a.W, t = r % a.W;
@@ -173,13 +177,23 @@ __global__ __launch_bounds__(64) void embed_kernel(EmbedP a) {
   for (int j = 0; j < MAX_RUNS; ++j) {
     const int run = lane + 64 * j;
     if (run >= nruns) continue;
-    float* xo = a.x0 + (int64_t)r * a.D + 8 * run;
-    float* xi = a.xin0 + (int64_t)r * a.D + 8 * run;
+    // 8 consecutive floats per lane (32-byte aligned: D % 8 == 0): vector accesses
+    const f32x4* m0 = (const f32x4*)(a.mix0 + 8 * run);
+    const f32x4* m1 = (const f32x4*)(a.mix0 + a.D + 8 * run);
+    f32x4* xo = (f32x4*)(a.x0 + (int64_t)r * a.D + 8 * run);
+    f32x4* xi = (f32x4*)(a.xin0 + (int64_t)r * a.D + 8 * run);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float v = x[j][i] * inv;
-      xo[i] = v;
-      xi[i] = a.mix0[8 * run + i] * v + a.mix0[a.D + 8 * run + i] * v;
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 ma = m0[h], mb = m1[h];
+      f32x4 vo, vi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = x[j][4 * h + e] * inv;
+        vo[e] = v;
+        vi[e] = ma[e] * v + mb[e] * v;
+      }
+      xo[h] = vo;
+      xi[h] = vi;
     }
     if (t == a.W - 1) {
       float* co = a.cand_raw + (int64_t)b * a.D + 8 * run;
