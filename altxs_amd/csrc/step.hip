@@ -45,7 +45,9 @@ int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 constexpr int kLmHeadColWgs = 128;
 // Launches with at least this many rows use the 64 x 128 tile GEMMs
 // (gemm_big_kernel, bit-identical to the 16-row tasks); bf16 activations only.
-constexpr int kBigRows = 2048;
+// cfg3 windows at ctx 2048: W = 16 (1024 rows) 1.43 ms per step against 1.51
+// on the 16-row tasks; W = 8 (512 rows) 1.34 against 1.09.
+constexpr int kBigRows = 1024;
 // Preferred K-splits of the 4-wave GEMM stages (QKV and the LM head use
 // (NB, KS) = (4, 1): one 64-column head tile per task).
 constexpr int kKsO = 2, kKsUp = 2, kKsDown = 4;

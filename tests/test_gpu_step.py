@@ -182,10 +182,11 @@ def test_dense_cdf_bit_identical_decode_encode(act):
                                             ("tiny", "bf16", 4)])
 def test_long_window_bit_identical_to_rows(profile, act, B):
     """A 512-token window per segment gives the logits and tables of 512
-    decode rows: 2048 bf16 rows take the launch shapes of chunk scoring (64 x
-    128 GEMM tiles with strip epilogues, one workgroup per CDF row forming its
-    own tile statistics), 1024 rows the 16-row GEMMs.  "tiny" adds parallel
-    lanes, skips popped from earlier slots, depth loops and GQA to the strips."""
+    decode rows: 1024 and 2048 bf16 rows take the launch shapes of chunk
+    scoring (64 x 128 GEMM tiles with strip epilogues, one workgroup per CDF
+    row forming its own tile statistics), fp32 rows the 16-row GEMMs.  "tiny"
+    adds parallel lanes, skips popped from earlier slots, depth loops and GQA
+    to the strips."""
     from altxs_amd.model import StepModel
 
     _log(f"long window vs rows {profile} {act} B={B}")
