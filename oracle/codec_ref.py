@@ -8,7 +8,9 @@
   (weights/mixed_da_bpw3.15_upb1.8.json layouts).
 * :func:`symmetric_levels` restates ``_symmetric_levels`` (147-152).
 * :func:`dequantize_channels` restates ``dequantize_channels`` (172-229) for the
-  lloyd, symmetric, shared and fp4 modes.
+  lloyd, symmetric, shared, fp4 and hybrid modes; pinned bit for bit by the
+  reference's own outputs in every mode (tests/golden/codec_modes.npz) and on
+  channels of every bank of the shipped asset (tests/golden/shipped_slice.npz).
 * :func:`from_channels` restates ``_from_channels`` (116-144); pinned by a
   hand-built 2-layer example (tests/test_codec.py).
 * :func:`dequant_group64` is the symmetric rule with 64-wide groups along K

@@ -17,10 +17,16 @@ tests run (XSA_AC_FUSED=0): ``GPT.static_extend`` (src/xsa_ttt/model.py:
   (src/xsa_ttt/ttt_lora.py:22-55) as _block_with_lora adds it (143-151).
 
 Pinning: against logits written by the reference GPT itself on the same
-weights and tokens (tests/golden/model_*.npz from tests/golden/make_golden.py);
+weights and tokens (tests/golden/model_*.npz from tests/golden/make_golden.py:
+"tiny", cfg1, cfg1 over 136 steps, and the cfg3 benchmark model);
 against its own full causal forward (incremental rows == teacher-forced rows);
 and, with every motif switch off, against a textbook pre-norm GPT written
 with F.scaled_dot_product_attention (tests/test_oracle_model.py).
+
+``segment_rows_tf`` restates the probability engine's row semantics
+(``_segment_rows_tf`` / ``reset_segment``, src/xsa_ttt/incremental.py:858-897,
+1238-1271, with ``_softmax_np``, compress.py:64-85); pinned by rows the
+reference's ``StaticACEngine`` wrote (tests/golden/engine_rows.npz).
 
 ``act="bf16"`` additionally rounds, exactly where the GPU's bf16 mode does,
 the GEMM inputs (normed activations, attention output, MLP hidden), the
@@ -374,3 +380,69 @@ class OracleModel:
 def softmax_probs(logits: torch.Tensor) -> np.ndarray:
     """Probabilities as the engine computes them: fp32 torch.softmax (incremental.py:603-605)."""
     return torch.softmax(logits.float(), dim=-1).numpy().astype(np.float32)
+
+
+# ---- probability-engine row semantics ---------------------------------------------
+
+def softmax_np(logits: torch.Tensor) -> np.ndarray:
+    """``_softmax_np`` (src/xsa_ttt/compress.py:64-85) for one row: fp32
+    torch.softmax, then ``p /= float(p.sum())`` in numpy float32 (a non-finite
+    or non-positive sum gives the uniform row)."""
+    p = torch.softmax(logits.detach().float().reshape(-1), dim=-1).numpy().astype(np.float32)
+    s = float(p.sum())
+    if s <= 0 or not math.isfinite(s):
+        return np.full(p.size, 1.0 / p.size, dtype=np.float32)
+    p /= s
+    return p
+
+
+def chunk_ctx_start(start: int, block: int) -> tuple[int, int]:
+    """``_chunk_ctx_start`` (compress.py:122-125)."""
+    p0 = 1 if int(start) == 0 else int(start)
+    return p0, max(0, p0 - int(block))
+
+
+def engine_max_len(block: int, every: int, win: int) -> int:
+    """Static-state length of ``StaticACEngine`` (incremental.py:239-241): the
+    RoPE table is warmed at this length (warm_rotary, 106-113), which sets the
+    YaRN scale."""
+    return int(block) + (max(1, int(every)) + int(win) - 1) // int(win) * int(win)
+
+
+@torch.no_grad()
+def segment_rows_tf(om: OracleModel, arr, seg, start: int, block: int, win: int) -> np.ndarray:
+    """Teacher-forced probability rows of one segment, as ``_segment_rows_tf``
+    (incremental.py:1238-1271) with ``reset_segment`` (858-897): rows[0] is
+    the carry -- ``_softmax_np`` of the logits after the context window
+    ``arr[ctx_start:start]`` (uniform 1/V at the stream start) -- and
+    rows[i + 1] = torch.softmax of the logits after seg[:i + 1].  The context
+    is run as committed windows (the reference prefills it with one causal
+    forward; incremental and teacher-forced logits agree to fp32 rounding).
+    ``om`` must be built with ``max_len = engine_max_len(...)``."""
+    V = om.cfg.vocab_size
+    _, c0 = chunk_ctx_start(start, block)
+    ctx = np.asarray(arr[c0:int(start)], dtype=np.int64)
+    seg = np.asarray(seg, dtype=np.int64)
+    st = om.new_state()
+    if ctx.size:
+        last = None
+        for w0 in range(0, ctx.size, win):
+            w = ctx[w0:w0 + win]
+            last = om.step(st, w)[-1]
+            om.advance(st, w.size)
+        carry = softmax_np(last)
+    else:
+        carry = np.full(V, 1.0 / V, dtype=np.float32)
+    n = seg.size
+    rows = np.empty((n, V), dtype=np.float32)
+    w0 = 0
+    while w0 < n:
+        w = min(win, n - w0)
+        probs = torch.softmax(om.step(st, seg[w0:w0 + w]).float(), dim=-1).numpy()
+        rows[w0] = carry
+        if w > 1:
+            rows[w0 + 1:w0 + w] = probs[:w - 1]
+        carry = probs[w - 1]
+        om.advance(st, w)
+        w0 += w
+    return rows

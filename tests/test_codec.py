@@ -239,3 +239,63 @@ def test_shipped_layouts_match_bank_parts():
         assert lay["channel_width"] == cfg.model_dim
         assert sum(p.n for p in parts) == lay["channels"]
         assert sorted((p.c0, p.c0 + p.n) for p in parts)[-1][1] == lay["channels"]
+
+
+# ---- reference-written vectors (tests/golden/make_golden.py) ---------------------
+
+MODES = ["lloyd", "symmetric", "shared", "fp4", "hybrid_fp4_symmetric"]
+
+
+def _mode_inputs(z, mode):
+    books = {b: z[f"{mode}/codebook_b{b}"] for b in (2, 3, 4)}
+    packed = {b: z[f"{mode}/packed_b{b}"] for b in (2, 3, 4)}
+    scales = {b: z[f"{mode}/scale_b{b}"] for b in (2, 3, 4) if f"{mode}/scale_b{b}" in z.files}
+    return packed, books, scales or None
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_dequantize_channels_matches_reference(golden_dir, mode):
+    """The oracle decoder equals the reference's dequantize_channels
+    (mixed_bit_delta.py:172-229) bit for bit in every codebook mode, on
+    seeded channels of mixed width with dead ones."""
+    z = np.load(os.path.join(golden_dir, "codec_modes.npz"))
+    packed, books, scales = _mode_inputs(z, mode)
+    bits = z["bits"].copy()
+    got = codec_ref.dequantize_channels(bits, books, packed, channel_width=int(z["width"]),
+                                        mode=mode, scales=scales)
+    assert np.array_equal(got, z[f"{mode}/out"])
+
+
+def test_dequantize_channels_mode_mistakes_fail(golden_dir):
+    """Plausible mistakes fail the reference vectors: decoding lloyd codebooks
+    with the symmetric rule, or codes MSB-first."""
+    z = np.load(os.path.join(golden_dir, "codec_modes.npz"))
+    packed, books, scales = _mode_inputs(z, "symmetric")
+    bits = z["bits"].copy()
+    want = z["symmetric/out"]
+    flipped = {b: np.unpackbits(p, bitorder="little").reshape(-1, 8)[:, ::-1].copy() for b, p in packed.items()}
+    flipped = {b: np.packbits(f.reshape(-1), bitorder="little") for b, f in flipped.items()}
+    got = codec_ref.dequantize_channels(bits, books, flipped, channel_width=int(z["width"]),
+                                        mode="symmetric")
+    assert not np.array_equal(got, want)
+    lp, lb, _ = _mode_inputs(z, "lloyd")
+    got = codec_ref.dequantize_channels(bits, {b: lb[b][:, :1] for b in lb}, lp,
+                                        channel_width=int(z["width"]), mode="symmetric")
+    assert not np.array_equal(got, z["lloyd/out"])
+
+
+def test_shipped_slice_matches_reference(golden_dir):
+    """Channels of every bank of the shipped asset, decoded by the oracle from
+    their packed bytes and codebook rows, equal what the reference decoded
+    from the whole bank (so rank -> byte offset and codebook row mapping
+    are pinned on the real file)."""
+    z = np.load(os.path.join(golden_dir, "shipped_slice.npz"))
+    assert str(z["mode"]) == "lloyd"
+    for bank in ("tok_emb.weight", "qo_bank", "kv_bank", "mlp_up_bank", "mlp_down_bank"):
+        bits = z[f"{bank}/bits"]
+        packed = {b: z[f"{bank}/packed_b{b}"] for b in (2, 3, 4)}
+        books = {b: z[f"{bank}/codebook_b{b}"] for b in (2, 3, 4)}
+        got = codec_ref.dequantize_channels(bits, books, packed, channel_width=int(z[f"{bank}/width"]),
+                                            mode="lloyd")
+        assert np.array_equal(got, z[f"{bank}/out"]), bank
+        assert (bits == 0).any() == (~z[f"{bank}/out"].any(axis=1)).any() or not (bits == 0).any()

@@ -2,7 +2,9 @@
 
 1. Against logits the reference GPT itself produced on the same weights and
    tokens (tests/golden/model_*.npz, written by tests/golden/make_golden.py):
-   W=1 static_extend rows, W=4 windows and forward_logits.
+   W=1 static_extend rows, W=4 windows and forward_logits -- for "tiny",
+   cfg1, cfg1 over 136 steps (rows cross two 64-key tiles) and the cfg3
+   benchmark model (V=16384).
 2. Invariants: incremental rows == teacher-forced rows; W=4 windows == W=1.
 3. With the motif switched off, the oracle equals an independently written
    pre-norm GPT (F.scaled_dot_product_attention, complex-number RoPE).
@@ -24,9 +26,14 @@ from oracle.model_ref import OracleModel
 TOL = 3e-5  # fp32 reassociation between two implementations of the same math
 
 
+# fixture name -> config profile (cfg1_long: 136 steps, rows past two 64-key
+# attention tiles; cfg3: the benchmark model, V=16384, 10 layers)
+FIXTURES = {"tiny": "tiny", "cfg1": "cfg1", "cfg1_long": "cfg1", "cfg3": "cfg3"}
+
+
 def _load(golden_dir, profile):
     g = np.load(os.path.join(golden_dir, f"model_{profile}.npz"))
-    cfg = make_config(profile)
+    cfg = make_config(FIXTURES[profile])
     sm = synth.make_model(cfg, std=float(g["std"]), softcap=tuple(g["softcap"].tolist()))
     om = OracleModel(cfg, sm.state_dict(), max_len=int(g["max_len"]))
     return g, cfg, om
@@ -43,7 +50,7 @@ def _check(got: np.ndarray, g, key: str):
     assert np.all(np.abs(ss - g[key + "_ss"]) <= 1e-5 * np.abs(g[key + "_ss"]) + 1e-6), key + "_ss"
 
 
-@pytest.mark.parametrize("profile", ["tiny", "cfg1"])
+@pytest.mark.parametrize("profile", list(FIXTURES))
 def test_oracle_matches_reference_rows(golden_dir, profile):
     g, cfg, om = _load(golden_dir, profile)
     toks = g["tokens"]
@@ -51,7 +58,7 @@ def test_oracle_matches_reference_rows(golden_dir, profile):
     _check(rows, g, "rows_w1")
 
 
-@pytest.mark.parametrize("profile", ["tiny", "cfg1"])
+@pytest.mark.parametrize("profile", list(FIXTURES))
 def test_oracle_matches_reference_windows(golden_dir, profile):
     g, cfg, om = _load(golden_dir, profile)
     toks = g["tokens"]
@@ -63,7 +70,7 @@ def test_oracle_matches_reference_windows(golden_dir, profile):
     _check(torch.cat(out).numpy(), g, "rows_w4")
 
 
-@pytest.mark.parametrize("profile", ["tiny", "cfg1"])
+@pytest.mark.parametrize("profile", list(FIXTURES))
 def test_oracle_matches_reference_full(golden_dir, profile):
     g, cfg, om = _load(golden_dir, profile)
     _check(om.forward_logits(g["tokens"]).numpy(), g, "full")
