@@ -54,6 +54,7 @@ class AltxsConfig:
     attn_out_gate_enabled: bool = False
     gated_attn_enabled: bool = False
     block_size: int = 2048  # RoPE train_seq_len (model.py:1023)
+    online_retrain_every: int = 2048  # segment length (config.py:58); sets the engine length
     # build-only fields
     lora_rank: int = 0  # unmerged q/v LoRA rank (0 = off); ttt_lora.py:22-55
     lora_alpha: float = 16.0

@@ -12,11 +12,18 @@ give the rows of decode bit for bit (the step is batch- and window-invariant).
 Row semantics (incremental.py:1238-1271): ``rows[0]`` is the carry -- the
 distribution after the segment's context (uniform at the stream start) -- and
 ``rows[i + 1] = P(. | context, seg[:i + 1])``.  Here every row is the step's
-integer CDF (and, on request, its fp32 probabilities); the carry of a non-empty
-context is the same kernel's table for the context's last token, so encoder and
-decoder use one rule for every row.  (The reference forms its carry with a
-host softmax and notes that it differs from the device rows by a few integer
-masses, incremental.py:878-882.)
+integer CDF (and, on request, its fp32 probabilities).  The carry follows the
+reference's rule for it (``reset_segment`` applies ``_softmax_np``: fp32
+softmax, then ``p /= sum(p)``, compress.py:64-85, incremental.py:878-886): the
+context's last window runs with the step's renormalisation flag, so the
+carry's counts come from renormalised probabilities while every later row
+uses the plain softmax, as the reference's device rows do.  Encoder and
+decoder both form it this way.
+
+Lengths: the engine's static length is ``block + ceil(every / W) * W``
+(incremental.py:239-242) and the RoPE table is warmed at that length
+(warm_rotary, 106-113), which sets the YaRN scale; the KV cache is that
+length rounded up to the step's 256-key granule unless ``max_len`` is given.
 """
 
 from __future__ import annotations
@@ -25,13 +32,19 @@ import numpy as np
 import torch
 
 from .coder import RangeCoder
-from .model import StaticState, StepModel
+from .model import CHUNK, StaticState, StepModel
 
 
 def chunk_ctx_start(start: int, block: int) -> tuple[int, int]:
     """``(p0, ctx_start)`` of a chunk starting at ``start`` (compress.py:122-125)."""
     p0 = 1 if start == 0 else int(start)
     return p0, max(0, p0 - int(block))
+
+
+def engine_length(block: int, every: int, win: int) -> int:
+    """Static length of the engine (incremental.py:239-242): the context block
+    plus whole windows covering one retrain segment of ``every`` symbols."""
+    return int(block) + (max(1, int(every)) + int(win) - 1) // int(win) * int(win)
 
 
 def uniform_cum(V: int, device) -> torch.Tensor:
@@ -44,14 +57,19 @@ class StaticACEngine:
     """B segments stepped in lockstep; every segment of a batch has the same
     context length and position (the reference runs one segment at a time)."""
 
-    def __init__(self, model: StepModel, *, batch: int = 1, win: int = 64, max_len: int = 2048,
-                 block: int | None = None, want_probs: bool = False):
+    def __init__(self, model: StepModel, *, batch: int = 1, win: int = 64, max_len: int | None = None,
+                 block: int | None = None, every: int | None = None, want_probs: bool = False):
         self.model = model
         self.batch, self.win = int(batch), int(win)
         self.block = int(block if block is not None else model.cfg.block_size)
+        self.every = int(every if every is not None else model.cfg.online_retrain_every)
         self.V = model.cfg.vocab_size
-        self.st: StaticState = model.make_static_state(max_len, win=self.win, batch=self.batch,
-                                                       want_probs=want_probs)
+        self.rope_len = engine_length(self.block, self.every, self.win)
+        if max_len is None:
+            max_len = (self.rope_len + CHUNK - 1) // CHUNK * CHUNK
+        self.st: StaticState = model.make_static_state(int(max_len), win=self.win, batch=self.batch,
+                                                       want_probs=want_probs,
+                                                       rope_len=self.rope_len)
         self.uniform = uniform_cum(self.V, model.device)
         self.carry = torch.empty(self.batch, self.V + 1, dtype=torch.int32, device=model.device)
         self.ctx_len = 0
@@ -83,27 +101,32 @@ class StaticACEngine:
         self.pos = 0
         if L == 0:  # stream start: uniform first row, smear sees zeros
             self.carry.copy_(self.uniform.expand(self.batch, -1))
+            if st.probs is not None:
+                self.carry_probs = torch.full((self.batch, self.V), 1.0 / self.V,
+                                              dtype=torch.float32, device=self.model.device)
             return
         ctx = np.stack(ctxs)
         w0 = 0
-        while w0 < L:  # committed windows; the last one is narrower
+        while w0 < L:  # committed windows; the last one is narrower and renormalises
             w = min(self.win, L - w0)
-            self._run(ctx[:, w0:w0 + w], commit=True)
+            self._run(ctx[:, w0:w0 + w], commit=True, renorm=w0 + w >= L)
             w0 += w
         self.carry.copy_(st.cum[:self.batch * w].view(self.batch, w, -1)[:, w - 1])
+        if st.probs is not None:
+            self.carry_probs = st.probs[:self.batch * w].view(self.batch, w, -1)[:, w - 1].clone()
 
     def carry_row_dev(self) -> torch.Tensor:
         """[B, V+1] table of each segment's first symbol (rows[0])."""
         return self.carry
 
     # ---- steps ----------------------------------------------------------------
-    def _run(self, tokens, *, commit: bool) -> int:
+    def _run(self, tokens, *, commit: bool, renorm: bool = False) -> int:
         toks = torch.as_tensor(np.asarray(tokens) if not torch.is_tensor(tokens) else tokens)
         w = int(toks.shape[-1])
         if self.pos + w > self.st.max_len:
             raise ValueError("window past max_len")
         self.st.tokens(w).copy_(toks.reshape(self.batch, w).to(torch.int32))
-        self.model.step(self.st, commit=commit, width=w)
+        self.model.step(self.st, commit=commit, renorm=renorm, width=w)
         if commit:
             self.pos += w
         self.n_steps += 1
@@ -204,3 +227,30 @@ def decode_segments_gpu(engine: StaticACEngine, prefixes, payloads: list[bytes],
         rc.decode(rows, out[:, i + 1:i + 2], out_stride=n)
     rc.check()
     return out.cpu().numpy().astype(np.int64)
+
+
+def segment_prob_rows_tf(engine: StaticACEngine, prefixes, segs, starts):
+    """The teacher-forced rows of :func:`segment_rows_tf` as probabilities
+    too (the engine must keep them: ``want_probs=True``): returns
+    ``(probs [B, n, V] fp32, cum [B, n, V+1] int64)``; ``probs[:, 0]`` is the
+    renormalised carry (incremental.py:878-886)."""
+    if engine.st.probs is None:
+        raise ValueError("segment_prob_rows_tf needs an engine built with want_probs=True")
+    engine.reset_segment(prefixes, starts)
+    seg = np.stack([np.asarray(s, dtype=np.int64) for s in segs])
+    B, n = seg.shape
+    probs = np.empty((B, n, engine.V), dtype=np.float32)
+    cum = np.empty((B, n, engine.V + 1), dtype=np.int64)
+    cprob = engine.carry_probs.cpu().numpy()
+    ccum = engine.carry_row_dev().cpu().numpy()
+    w0 = 0
+    while w0 < n:
+        w = min(engine.win, n - w0)
+        rows = engine.run_window(seg[:, w0:w0 + w], w0, commit=True).cpu().numpy()
+        pr = engine.st.probs[:B * w].view(B, w, -1).cpu().numpy()
+        probs[:, w0], cum[:, w0] = cprob, ccum
+        if w > 1:
+            probs[:, w0 + 1:w0 + w], cum[:, w0 + 1:w0 + w] = pr[:, :w - 1], rows[:, :w - 1]
+        cprob, ccum = pr[:, w - 1], rows[:, w - 1]
+        w0 += w
+    return probs, cum

@@ -150,20 +150,23 @@ def make_model(cfg: AltxsConfig, *, seed: int = WEIGHT_SEED, std: float = 0.02,
     return SynthModel(cfg, packed, small)
 
 
-def rope_table(cfg: AltxsConfig, max_len: int):
+def rope_table(cfg: AltxsConfig, max_len: int, rope_len: int | None = None):
     """cos/sin [max_len, rope_dims/2] fp32, built as Rotary.forward does.
 
     Follows src/xsa_ttt/model.py:130-192: inv_freq = 1 / base^(arange(0, rd, 2)/rd)
     in fp32; with YaRN and a table longer than train_seq_len (= block_size),
     base <- base * (len/train_seq_len)^(rd/(rd-2)); freqs = outer(t, inv_freq).
-    The engine warms the table at max_len once (incremental.py:106-113).
+    ``len`` is the length the table is warmed at, ``rope_len`` (default
+    max_len): the engine warms it once at its static length
+    (incremental.py:106-113, 239-242), which can differ from the rows kept.
     """
     import torch
 
     rd = cfg.rope_dims_eff
     base = cfg.rope_base
-    if cfg.rope_yarn and max_len > cfg.block_size:
-        scale = max_len / cfg.block_size
+    L = int(rope_len) if rope_len is not None else int(max_len)
+    if cfg.rope_yarn and L > cfg.block_size:
+        scale = L / cfg.block_size
         new_base = base * scale ** (rd / (rd - 2))
         inv_freq = 1.0 / new_base ** (torch.arange(0, rd, 2, dtype=torch.float32) / rd)
     else:

@@ -1,7 +1,8 @@
 """The probability engine (altxs_amd.engine, after StaticACEngine).
 
 * teacher-forced tables from windows (the last one narrower) equal the tables
-  of width-1 decode rows, with a context prefilled by committed windows;
+  of width-1 decode rows, with a context prefilled by committed windows; the
+  carry is the renormalised table after the context (reference rule);
 * the stream-start carry is the count rule applied to the uniform row (the
   oracle's scale_cum on p = 1/V);
 * a compress -> decompress round trip of two segments after a context: the
@@ -56,10 +57,15 @@ def test_window_rows_equal_decode_rows_after_context():
     one = segment_rows_one_row(eng, streams, segs, starts)
     assert np.array_equal(tf, one)
     assert (tf[:, :, -1] > 0).all() and (np.diff(tf, axis=-1) >= 1).all()
-    # the carry is the table after the context's last token, as a decode row gives it
+    # the carry is the table after the context's last token, as a decode row
+    # with the renormalising count rule gives it (_softmax_np, incremental.py:878-886)
     eng.reset_segment([s[:0] for s in streams], [0, 0])
     for t in range(36, 100):
-        eng.run_decode_row_dev(torch.from_numpy(np.stack([s[t] for s in streams]).astype(np.int32)).cuda())
+        tok = torch.from_numpy(np.stack([s[t] for s in streams]).astype(np.int32)).cuda()
+        if t < 99:
+            eng.run_decode_row_dev(tok)
+        else:
+            eng._run(tok.reshape(2, 1), commit=True, renorm=True)
     assert np.array_equal(eng.st.cum[:2].cpu().numpy(), tf[:, 0])
 
 
