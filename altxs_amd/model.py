@@ -71,12 +71,14 @@ class StaticState:
 
     def __init__(self, model: "StepModel", batch: int, win: int, max_len: int,
                  want_probs: bool = True, want_cdf: bool = True, split: bool = False,
-                 persistent: bool = False):
+                 persistent: bool = False, rope_len: int | None = None):
         cfg, dev = model.cfg, model.device
         if max_len % CHUNK:
             raise ValueError(f"max_len must be a multiple of {CHUNK}")
         self.model = model
         self.batch, self.win, self.max_len = int(batch), int(win), int(max_len)
+        # length the RoPE table is warmed at (sets the YaRN scale); rows kept = max_len
+        self.rope_len = int(rope_len) if rope_len is not None else self.max_len
         B, W, V, D = self.batch, self.win, cfg.vocab_size, cfg.model_dim
         R = B * W
         self.token = torch.zeros(B, W, dtype=torch.int32, device=dev)
@@ -193,20 +195,27 @@ class StepModel:
         self._cos_cache: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         self._disabled = False
 
-    def rope(self, max_len: int):
-        t = self._cos_cache.get(max_len)
+    def rope(self, max_len: int, rope_len: int | None = None):
+        """cos/sin rows [0, max_len) of the table warmed at ``rope_len`` (default
+        max_len), as ``Rotary.forward(rope_len)`` builds it (model.py:147-192)."""
+        key = (int(max_len), int(rope_len) if rope_len is not None else int(max_len))
+        t = self._cos_cache.get(key)
         if t is None:
-            cos, sin = rope_table(self.cfg, max_len)
+            cos, sin = rope_table(self.cfg, key[0], key[1])
             t = (cos.to(self.device).contiguous(), sin.to(self.device).contiguous())
-            self._cos_cache[max_len] = t
+            self._cos_cache[key] = t
         return t
 
     def make_static_state(self, max_len: int, device=None, win: int = 1, batch: int = 1,
                           want_probs: bool = True, want_cdf: bool = True,
-                          split: bool = False, persistent: bool = False) -> StaticState:
+                          split: bool = False, persistent: bool = False,
+                          rope_len: int | None = None) -> StaticState:
         """``split``: run the segments as two groups on two streams (B >= 2).
-        ``persistent``: run every slot in one persistent launch (bf16 KV, W | 16)."""
-        return StaticState(self, batch, win, max_len, want_probs, want_cdf, split, persistent)
+        ``persistent``: run every slot in one persistent launch (bf16 KV, W | 16).
+        ``rope_len``: the length the RoPE table is warmed at (default max_len);
+        the reference engine warms it at its static length (incremental.py:239-242)."""
+        return StaticState(self, batch, win, max_len, want_probs, want_cdf, split, persistent,
+                           rope_len)
 
     def _fill_desc(self, st: StaticState, flags: int) -> _lib.StepDesc:
         cfg = self.cfg
@@ -271,7 +280,7 @@ class StepModel:
                 sm["softcap_pn"] = torch.stack([sm["softcap_pos"].reshape(()),
                                                 sm["softcap_neg"].reshape(())]).contiguous()
             d.softcap_pn = sm["softcap_pn"].data_ptr()
-        cos, sin = self.rope(st.max_len)
+        cos, sin = self.rope(st.max_len, getattr(st, "rope_len", None))
         d.rope_cos, d.rope_sin = cos.data_ptr(), sin.data_ptr()
         d.tokens, d.pos = st.token.data_ptr(), st.pos.data_ptr()
         d.prev_raw, d.cand_raw = st.prev_raw.data_ptr(), st.cand_prev_raw.data_ptr()
