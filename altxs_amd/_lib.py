@@ -31,6 +31,7 @@ CDF_RENORM = 1
 ATTN_OPS_BF16 = 1
 ATTN_ROWS = 2
 KV_TILE = 64
+STEP_SCRATCH_BYTES = 24 << 20  # ALTXS_STEP_SCRATCH_BYTES
 
 SLOT_SEQ, SLOT_PAR = 0, 1
 
@@ -47,6 +48,7 @@ EXPORTS = (
     "altxs_step_plan_bytes",
     "altxs_step_plan_build",
     "altxs_step",
+    "altxs_step_noalloc",
     "altxs_range_init",
     "altxs_range_encode",
     "altxs_range_finish",
@@ -167,6 +169,8 @@ def load(path: str | None = None):
     L.altxs_step_plan_build.argtypes = [ctypes.POINTER(StepDesc), p, p, i64, p]
     L.altxs_step.restype = i32
     L.altxs_step.argtypes = [ctypes.POINTER(StepDesc), p]
+    L.altxs_step_noalloc.restype = i32
+    L.altxs_step_noalloc.argtypes = [ctypes.POINTER(StepDesc), p]
     L.altxs_range_init.restype = i32
     L.altxs_range_init.argtypes = [p, i32, p]
     L.altxs_range_encode.restype = i32

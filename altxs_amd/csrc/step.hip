@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -654,4 +655,61 @@ extern "C" int32_t altxs_step(const AltxsStepDesc* d, altxs_stream_t stream) {
   }
   ALTXS_CHECK_HIP(e);
   return ALTXS_OK;
+}
+
+// ---- allocation-free step: the workspace is a file-scope device array -------
+//
+// Each GPU that runs altxs_step_noalloc holds its own copy of `scratch` until
+// the process ends.  Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in symbol); it passes the per-device address
+// hipGetSymbolAddress returns, looked up once per device with that device
+// current.
+
+namespace {
+
+__device__ __align__(256) char scratch[ALTXS_STEP_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // guarded by g_scratch_mu
+
+int scratch_for_stream(hipStream_t st, void** out) {
+  int cur = -1;
+  ALTXS_CHECK_HIP(hipGetDevice(&cur));
+  hipDevice_t dev = cur;
+  if (st) ALTXS_CHECK_HIP(hipStreamGetDevice(st, &dev));
+  ALTXS_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "altxs_step_noalloc: device %d out of range",
+                (int)dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    if (dev != cur) ALTXS_CHECK_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) ALTXS_CHECK_HIP(hipSetDevice(cur));
+    ALTXS_CHECK_HIP(e);
+    ALTXS_REQUIRE(p != nullptr, "altxs_step_noalloc: no scratch address on device %d", (int)dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ALTXS_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t altxs_step_noalloc(const AltxsStepDesc* d, altxs_stream_t stream) {
+  ALTXS_REQUIRE(d, "altxs_step_noalloc: null descriptor");
+  ALTXS_REQUIRE(!d->plan_dev,
+                "altxs_step_noalloc: the persistent plan points at a caller workspace; use altxs_step");
+  const int64_t need = ws_bytes_needed(d);
+  ALTXS_REQUIRE(need <= (int64_t)ALTXS_STEP_SCRATCH_BYTES,
+                "altxs_step_noalloc: this step needs %lld workspace bytes, more than the %lld-byte "
+                "static scratch; use altxs_step with a caller workspace",
+                (long long)need, (long long)ALTXS_STEP_SCRATCH_BYTES);
+  void* ws = nullptr;
+  int rc = scratch_for_stream((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  AltxsStepDesc dd = *d;  // the caller's descriptor with the scratch as workspace
+  dd.ws = ws;
+  dd.ws_bytes = ALTXS_STEP_SCRATCH_BYTES;
+  return altxs_step(&dd, stream);
 }

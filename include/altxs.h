@@ -303,6 +303,28 @@ int32_t altxs_step_plan_build(const AltxsStepDesc *d, void *plan_host, void *pla
  */
 int32_t altxs_step(const AltxsStepDesc *d, altxs_stream_t stream);
 
+/* Size of the static device scratch altxs_step_noalloc uses as its workspace:
+ * 24 MiB, enough for decode rows of the cfg3 model up to B = 256. */
+#define ALTXS_STEP_SCRATCH_BYTES (24ll << 20)
+
+/*
+ * altxs_step without a caller workspace: d->ws and d->ws_bytes are ignored and
+ * the step's partial results (slot outputs, normalised rows, LM-head tile
+ * statistics, counters) live in a file-scope device array of
+ * ALTXS_STEP_SCRATCH_BYTES inside the library, one per GPU, held until the
+ * process ends.  It calls no allocator, so callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc -- can run the step; the caller still passes every input and
+ * output buffer.  Same results as altxs_step.  A step whose
+ * altxs_step_workspace_bytes() exceeds ALTXS_STEP_SCRATCH_BYTES, or with a
+ * persistent plan (d->plan_dev, built for a caller workspace), is rejected
+ * with ALTXS_ERR_ARG.  All calls on one GPU share its scratch and each call
+ * leaves its contents behind (the step's first kernel clears its counters):
+ * calls that overlap on one GPU (two streams, or two host threads) race.
+ * No counterpart in the reference.
+ */
+int32_t altxs_step_noalloc(const AltxsStepDesc *d, altxs_stream_t stream);
+
 /*
  * Range coder (the 32-bit Witten-Neal-Cleary coder with E3 bits of
  * arithmetic_coder_lm.py:90-288; replaces GpuRangeCoder, gpu_ac.py:397-479,
