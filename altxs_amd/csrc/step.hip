@@ -101,6 +101,18 @@ int64_t carve(const AltxsStepDesc* d, int nb, WS* w, char* base) {
   return off;
 }
 
+// Split mode: the second group's chain starts after the first group's slot-0
+// QKV (0), attention (1) or MLP (2) -- ALTXS_SPLIT_FORK, for tuning.
+int split_fork_stage() {
+  static int f = -1;
+  if (f < 0) {
+    const char* e = getenv("ALTXS_SPLIT_FORK");
+    f = e ? atoi(e) : 0;
+    if (f < 0 || f > 2) f = 0;
+  }
+  return f;
+}
+
 // Two segment groups (split mode) when the caller hands in a second stream.
 bool split_mode(const AltxsStepDesc* d) { return d->aux_stream != nullptr && d->B >= 2; }
 int64_t ws_bytes_needed(const AltxsStepDesc* d) {
@@ -174,9 +186,14 @@ int validate(const AltxsStepDesc* d) {
     if ((rc = check_tensor(L.down, d->D, d->F, "down", l))) return rc;
     ALTXS_REQUIRE(L.resid_mix && L.attn_scale && L.mlp_scale && L.q_gain,
                   "altxs_step: layer %d small params missing", l);
+    // read with 16-byte vector loads (embedding and strip epilogues)
+    ALTXS_REQUIRE((((uintptr_t)L.resid_mix | (uintptr_t)L.attn_scale | (uintptr_t)L.mlp_scale) & 15) == 0,
+                  "altxs_step: layer %d resid_mix / attn_scale / mlp_scale must be 16-byte aligned", l);
     if (d->flags & ALTXS_F_SPARSE_GATE)
       ALTXS_REQUIRE(L.attn_gate_w, "altxs_step: layer %d attn_gate_w missing", l);
   }
+  ALTXS_REQUIRE((((uintptr_t)d->skip_weights | (uintptr_t)d->skip_gates) & 15) == 0,
+                "altxs_step: skip_weights / skip_gates must be 16-byte aligned");
   int rc;
   if ((rc = check_tensor(d->emb, d->V, d->D, "emb", -1))) return rc;
   for (int s = 0; s < d->n_slots; ++s) {
@@ -575,17 +592,21 @@ hipError_t run_split(const AltxsStepDesc* d, const Group (&G)[2], hipStream_t s0
   hipEvent_t* ev = (hipEvent_t*)d->attn_events;    // timing hook: [(g*n + s)*2 + 0/1]
   const hipStream_t st[2] = {s0, s1};
   const int n = d->n_slots;
+  const int fork = split_fork_stage();
   hipError_t e;
   for (int g = 0; g < 2; ++g) {
     if (g == 1 && (e = hipStreamWaitEvent(s1, sync[0], 0)) != hipSuccess) return e;
     if ((e = run.embed(G[g], st[g])) != hipSuccess) return e;
     for (int s = 0; s < n; ++s) {
+      const bool fk = g == 0 && s == 0;
       if ((e = run.qkv(G[g], s, st[g])) != hipSuccess) return e;
-      if (g == 0 && s == 0 && (e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
+      if (fk && fork == 0 && (e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
       const int k = (g * n + s) * 2;
       if ((e = run.attn(G[g], s, st[g], ev ? ev[k] : nullptr, ev ? ev[k + 1] : nullptr)) != hipSuccess)
         return e;
+      if (fk && fork == 1 && (e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
       if ((e = run.mlp(G[g], s, st[g])) != hipSuccess) return e;
+      if (fk && fork >= 2 && (e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
     }
     if ((e = run.head(G[g], st[g])) != hipSuccess) return e;
   }

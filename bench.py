@@ -16,10 +16,13 @@ bytes.  Weights are seeded N(0, 0.02^2) then quantised; tokens are Zipf(1.1).
 The line also carries:
 * ``roofline``: the decode-attention kernel (the dominant one), algorithmic
   bytes per launch / its mean launch duration, timed with HIP events on the
-  step's stream around 20 back-to-back launches over slot 0's cache (the same
-  kernel and launch shape as in the step); ``us_per_launch_in_step`` is the
-  mean of events recorded around every attention launch inside the timed
-  steps, which also includes each launch's gap after the preceding kernel;
+  step's stream around 20 back-to-back launches that walk the ten slots'
+  caches in turn (the same kernel, launch shape and cache footprint as in
+  the step: each launch reads a 268 MB cache the previous nine launches did
+  not touch, so nothing is served from the 256 MB Infinity Cache);
+  ``us_per_launch_in_step`` is the mean of events recorded around every
+  attention launch inside the timed steps, which also includes each launch's
+  gap after the preceding kernel;
   ``traffic`` comes from profiles/traffic_attn.txt (rocprofv3 FETCH_SIZE +
   WRITE_SIZE, scaled by a plain copy of known size);
 * ``step_roofline``: algorithmic bytes of the whole step / step time;
@@ -40,6 +43,15 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 
 METRIC = "scored symbols/sec @32M mixed-3.15bpw, 64 segs ctx2048; % HBM roofline"
+
+
+def decode_metric(profile: str, B: int, ctx: int, bpw: float | None) -> str:
+    """The headline metric string for the default workload; the same wording
+    with this run's model, bit width, segment count and context otherwise."""
+    if (profile, B, ctx) == ("cfg3", 64, 2048) and bpw is not None:
+        return METRIC
+    w = "dense bf16" if bpw is None else f"mixed-{bpw:.2f}bpw"
+    return f"scored symbols/sec @{profile} {w}, {B} segs ctx{ctx}; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
 
 
@@ -60,8 +72,9 @@ def read_traffic(kernel: str):
 
 def attn_kernel_ms(model, st, reps: int = 20) -> float:
     """Mean duration of the decode-attention kernel: HIP events around ``reps``
-    back-to-back launches on the step's stream, over slot 0's cache and
-    positions with the step's launch configuration (XSA on, bf16 operands)."""
+    back-to-back launches on the step's stream with the step's launch
+    configuration (XSA on, bf16 operands), launch i reading slot i's cache
+    (mod the slot count), as the step's launches do."""
     import ctypes
 
     import torch
@@ -73,27 +86,51 @@ def attn_kernel_ms(model, st, reps: int = 20) -> float:
     g = torch.Generator(device="cuda").manual_seed(5)
     q = torch.randn(B, H, 64, generator=g, device="cuda")
     y = torch.empty(B, H * 64, dtype=torch.bfloat16 if model.act_bf16 else torch.float32, device="cuda")
-    kv0 = st.kv[0]
-    a = _lib.AttnArgs()
-    a.B, a.W, a.H, a.Hkv, a.head_dim, a.max_len = B, 1, H, Hkv, 64, max_len
-    a.kv_bf16, a.y_bf16 = int(model.kv_bf16), int(model.act_bf16)
-    esz = kv0.element_size()
-    a.q, a.k = q.data_ptr(), kv0.data_ptr()
-    a.v = kv0.data_ptr() + Hkv * max_len * 64 * esz
-    a.kv_seg_stride = 2 * Hkv * max_len * 64
-    a.pos, a.gate, a.use_xsa = st.pos.data_ptr(), None, 1
-    a.flags = _lib.ATTN_OPS_BF16 if model.act_bf16 else 0
-    a.y, a.err = y.data_ptr(), st.err.data_ptr()
+    args = []
+    for s in range(model.n_slots):
+        kv = st.kv[s]
+        a = _lib.AttnArgs()
+        a.B, a.W, a.H, a.Hkv, a.head_dim, a.max_len = B, 1, H, Hkv, 64, max_len
+        a.kv_bf16, a.y_bf16 = int(model.kv_bf16), int(model.act_bf16)
+        esz = kv.element_size()
+        a.q, a.k = q.data_ptr(), kv.data_ptr()
+        a.v = kv.data_ptr() + Hkv * max_len * 64 * esz
+        a.kv_seg_stride = 2 * Hkv * max_len * 64
+        a.pos, a.gate, a.use_xsa = st.pos.data_ptr(), None, 1
+        a.flags = _lib.ATTN_OPS_BF16 if model.act_bf16 else 0
+        a.y, a.err = y.data_ptr(), st.err.data_ptr()
+        args.append(a)
     L, stream = _lib.load(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    _lib.check(L.altxs_decode_attn(ctypes.byref(a), stream), "altxs_decode_attn")
+    for a in args:
+        _lib.check(L.altxs_decode_attn(ctypes.byref(a), stream), "altxs_decode_attn")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
-    for _ in range(reps):
-        L.altxs_decode_attn(ctypes.byref(a), stream)
+    for i in range(reps):
+        L.altxs_decode_attn(ctypes.byref(args[i % len(args)]), stream)
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu "Model name", else /proc/cpuinfo)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001
+        pass
+    try:
+        for line in open("/proc/cpuinfo", encoding="utf8"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(sm, ctx: int, seconds: float, seed: int = 0) -> dict:
@@ -122,7 +159,7 @@ def cpu_baseline(sm, ctx: int, seconds: float, seed: int = 0) -> dict:
         el = time.perf_counter() - t0
         if (el >= seconds and n >= 8) or n >= 100000:
             break
-    return {"value": n / el, "unit": "sym/s", "cores": cores, "kind": "port",
+    return {"value": n / el, "unit": "sym/s", "cores": cores, "kind": "port", "cpu": cpu_model(),
             "sample": f"{n} single-segment decode steps at ctx {ctx} (fp32 oracle, B=1, "
                       f"{el:.1f} s, torch threads={cores})"}
 
@@ -190,7 +227,7 @@ def window_bench(a) -> int:
         t0 = time.perf_counter()
         om.forward_logits(ids)
         el = time.perf_counter() - t0
-        cpu = {"value": W / el, "unit": "sym/s", "cores": cores, "kind": "port",
+        cpu = {"value": W / el, "unit": "sym/s", "cores": cores, "kind": "port", "cpu": cpu_model(),
                "sample": f"one segment of {W} tokens, fp32 oracle full causal forward, {el:.1f} s"}
     out = {
         "metric": (f"scored symbols/sec, {a.profile} chunk scoring {B} segments x {W} tokens"
@@ -463,7 +500,7 @@ def main() -> int:
 
     value = B / (ms * 1e-3)
     out = {
-        "metric": METRIC,
+        "metric": decode_metric(a.profile, B, ctx, None if a.dense else sm.bits_summary()["bpw"]),
         "value": round(value, 1),
         "unit": "sym/s",
         "n_gpus": 1,

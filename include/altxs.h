@@ -186,9 +186,9 @@ typedef struct AltxsLayer {
   AltxsQTensor o;            /* [D, D] */
   AltxsQTensor up;           /* [F, D] */
   AltxsQTensor down;         /* [D, F] */
-  const float *resid_mix;    /* [2, D] */
-  const float *attn_scale;   /* [D] */
-  const float *mlp_scale;    /* [D] */
+  const float *resid_mix;    /* [2, D], 16-byte aligned */
+  const float *attn_scale;   /* [D], 16-byte aligned */
+  const float *mlp_scale;    /* [D], 16-byte aligned */
   const float *q_gain;       /* [H] */
   const float *attn_gate_w;  /* [H, gate_window] or NULL */
   const float *par_resid;    /* [2] parallel_resid_lambdas[layer] or NULL */
@@ -226,8 +226,8 @@ typedef struct AltxsStepDesc {
   AltxsLayer layers[ALTXS_MAX_LAYERS];
   AltxsSlot slots[ALTXS_MAX_SLOTS];
   AltxsQTensor emb;          /* tied embedding / LM head [V, D] */
-  const float *skip_weights; /* [n_skip, D] */
-  const float *skip_gates;   /* [n_skip, D] or NULL */
+  const float *skip_weights; /* [n_skip, D], 16-byte aligned */
+  const float *skip_gates;   /* [n_skip, D] or NULL, 16-byte aligned */
   const float *smear_w;      /* [gate_window] */
   const float *smear_lambda; /* [1] */
   const float *softcap_pn;   /* [2] = (softcap_pos, softcap_neg) */

@@ -2,12 +2,16 @@
 
 * logits within 2e-3 absolute of the fp32 CPU oracle in the fp32 mode and in
   the fp32-activation / bf16-KV mode (at the benchmark weight scale, std 0.02);
-* full bf16 mode against the oracle's bf16-rounding emulation: the rounding
-  points match, but fp32 values one ulp apart can round to different bf16
-  neighbours, and q_gain/attention amplify such flips.  Perturbing the
-  emulation's pre-rounding values by 2e-7 (relative) moves its logits by up
-  to 1.7e-2 (tiny, std 0.08) / 6e-3 (cfg1, std 0.05), so this mode is checked
-  on mean and max error with bounds above that noise floor;
+* full bf16 mode: its parity gate is coded bits/symbol within 0.1% of the
+  fp32 oracle's (here on cfg1, and on 2048 cfg3 symbols in
+  test_gpu_parity.py); a logit gate against fp32 cannot hold for bf16
+  activations (rounding the LM-head input alone, as the reference's bf16
+  path does, moves cfg3 logits by > 2e-3: test_oracle_model.py).  The
+  comparison with the oracle's bf16-rounding emulation below is a diagnostic
+  bound, not a gate: fp32 values one ulp apart can round to different bf16
+  neighbours and q_gain/attention amplify such flips (perturbing the
+  emulation's pre-rounding values by 2e-7 relative moves its logits by up to
+  1.7e-2 on tiny / 6e-3 on cfg1);
 * integer CDFs bit-identical between decode rows (W=1), encode windows (W=4)
   and batches of different sizes, and from run to run;
 * coded bits/symbol within 0.1% of the oracle's coder on the oracle's tables.
@@ -125,6 +129,7 @@ def test_step_fp32_act_bf16_kv_meets_tolerance():
                                                       ("tiny_dense", 3e-3, 6e-2),
                                                       ("large_dense", 5e-4, 1e-2)])
 def test_step_bf16_matches_oracle_emulation(profile, mean_tol, max_tol):
+    """Diagnostic bound on the bf16 mode (its gate is bits/symbol)."""
     _log(f"step bf16 {profile}")
     got, _, _, _ = _gpu_decode(profile, "bf16")
     d = np.abs(got - _oracle_rows(profile, "bf16"))

@@ -157,6 +157,47 @@ def test_bf16_emulation_is_close_to_fp32():
     assert 0 < d < 0.1
 
 
+def test_reference_bf16_lm_head_rounding_alone_exceeds_logit_gate():
+    """Why a bf16-activation step cannot meet a 2e-3 logit gate against the
+    fp32 path: the reference's own bf16 path (_logits_fused_rows,
+    src/xsa_ttt/ac_gemv.py:312-355) feeds the LM head a bf16 hidden state, a
+    bf16 RMS scale and a bf16 normalised row.  Applying only that rounding to
+    the fp32 oracle's final hidden state moves cfg3 logits (the benchmark
+    model at the benchmark weight scale) by more than 2e-3."""
+    cfg = make_config("cfg3")
+    sm = synth.make_model(cfg, std=0.02, softcap=(30.0, 24.0))
+    om = OracleModel(cfg, sm.state_dict(), max_len=256)
+    toks = synth.zipf_tokens(cfg.vocab_size, (12,), seed=2026)
+    st = om.new_state()
+    hidden = []
+    orig = om._logits
+
+    def keep(x):
+        hidden.append(x.clone())
+        return orig(x)
+
+    om._logits = keep
+    rows = []
+    for t in toks:
+        rows.append(om.step(st, [int(t)]))
+        om.advance(st, 1)
+    want = torch.cat(rows)
+    x = torch.cat(hidden)
+    bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    src = bf(x)
+    scale = bf(torch.rsqrt((src * src).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps))
+    lg = F.linear(bf(src * scale), om.sd["tok_emb.weight"])
+    sp, sn = om.sd["softcap_pos"], om.sd["softcap_neg"]
+    got = torch.where(lg >= 0, sp * torch.tanh(lg / sp), sn * torch.tanh(lg / sn))
+    d = (got - want).abs().max().item()
+    assert d > 2e-3, d
+    # the same path without the rounding reproduces the oracle's logits
+    lg = F.linear(x * torch.rsqrt((x * x).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps),
+                  om.sd["tok_emb.weight"])
+    got = torch.where(lg >= 0, sp * torch.tanh(lg / sp), sn * torch.tanh(lg / sn))
+    assert (got - want).abs().max().item() < 1e-5
+
+
 def test_lora_unmerged_equals_merged():
     """Unmerged per-slot q/v LoRA (x @ A.T @ B.T * alpha/r, ttt_lora.py:53-55,
     added to the q and v projections, 143-151) equals the dense model whose q
