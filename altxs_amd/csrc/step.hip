@@ -678,6 +678,36 @@ extern "C" int32_t altxs_step(const AltxsStepDesc* d, altxs_stream_t stream) {
   return ALTXS_OK;
 }
 
+// ---- normalised-rows GEMM: y = (RMSNorm(x) * ln_scale) . W^T ----------------
+// The step's LM-head prologue (ProNorm) with a plain store: the standalone form
+// of logits_stage_rows (final RMS -> LM projection, ac_gemv.py:562-582).
+
+extern "C" int32_t altxs_rms_qgemm(const AltxsQTensor* w, const float* x, int64_t rows, float ln_scale,
+                                   float eps, int32_t act_bf16, float* y, altxs_stream_t stream) {
+  ALTXS_REQUIRE(w && w->codes && (w->bits == 16 || w->scales), "altxs_rms_qgemm: null tensor");
+  ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6 || w->bits == 16,
+                "altxs_rms_qgemm: bits=%d", w->bits);
+  ALTXS_REQUIRE(w->N > 0 && w->N % 16 == 0 && w->N < (1 << 24), "altxs_rms_qgemm: N=%lld",
+                (long long)w->N);
+  ALTXS_REQUIRE(w->K == 256 || w->K == 512, "altxs_rms_qgemm: K=%lld must be 256 or 512",
+                (long long)w->K);
+  ALTXS_REQUIRE(((uintptr_t)w->codes & 15) == 0 && ((uintptr_t)w->scales & 7) == 0,
+                "altxs_rms_qgemm: misaligned tensor");
+  ALTXS_REQUIRE(x && y && ((uintptr_t)x & 15) == 0, "altxs_rms_qgemm: x must be 16-byte aligned");
+  ALTXS_REQUIRE(rows >= 1 && rows <= (1 << 20), "altxs_rms_qgemm: rows=%lld", (long long)rows);
+  ProNorm pro{x, nullptr, 0, ln_scale, eps, (int)w->K};
+  EpiStore epi{y, (int)w->N, 0};
+  const QT q = qt_of(*w);
+  hipStream_t st = (hipStream_t)stream;
+  const hipError_t e =
+      act_bf16 ? launch_gemm_bits<A_BF16, 4, 1>(w->bits, q, (int)rows, 1, 0, 0, ADirect{nullptr, 0}, pro,
+                                                  epi, 0, st)
+               : launch_gemm_bits<A_F32, 4, 1>(w->bits, q, (int)rows, 1, 0, 0, ADirect{nullptr, 0}, pro,
+                                                 epi, 0, st);
+  ALTXS_CHECK_HIP(e);
+  return ALTXS_OK;
+}
+
 // ---- allocation-free step: the workspace is a file-scope device array -------
 //
 // Each GPU that runs altxs_step_noalloc holds its own copy of `scratch` until

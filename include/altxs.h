@@ -84,14 +84,15 @@ int32_t altxs_scale_cum(const float *probs, int64_t rows, int64_t V, uint32_t *c
 int32_t altxs_softmax_cdf(const float *logits, int64_t rows, int64_t V, int32_t flags,
                           float *probs, uint32_t *cum, altxs_stream_t stream);
 
-/* Dense fp32 copy of a packed tensor: out[N, K].  Replaces dequantize_channels
- * (mixed_bit_delta.py:172-229) for the group-64 format. */
+/* Dense fp32 copy of a packed tensor (bits in {2,3,4,6}): out[N, K].  Replaces
+ * dequantize_channels (mixed_bit_delta.py:172-229) for the group-64 format. */
 int32_t altxs_dequant(const AltxsQTensor *w, float *out, altxs_stream_t stream);
 
 /*
  * y[rows, N] = x[rows, K] . W^T with the dequantisation fused into an MFMA
  * GEMM (fp32 accumulate).  x_dtype: ALTXS_F16 / ALTXS_BF16 (one MFMA pass) or
- * ALTXS_F32 (three-way bf16 split of x, fp32-faithful).  Row results do not
+ * ALTXS_F32 (three-way bf16 split of x, fp32-faithful); bits 16 (dense bf16
+ * weights in the tiled order, scales unused) takes fp32 or bf16 x.  Row results do not
  * depend on `rows` (batch-invariant).  Replaces gemv_rows(x, w, out)
  * (src/xsa_ttt/ac_gemv.py:391-420) and F.linear in _projection_linear
  * (src/xsa_ttt/model.py:93-111).
@@ -108,6 +109,17 @@ int32_t altxs_qgemm(const AltxsQTensor *w, const void *x, int32_t x_dtype, int64
 int32_t altxs_qgemm_stream(const AltxsQTensor *w, int64_t count, int64_t codes_stride,
                            int64_t scales_stride, const void *x, int32_t x_dtype,
                            int64_t rows, float *y, altxs_stream_t stream);
+
+/*
+ * y[rows, N] = (RMSNorm(x[rows, K]) * ln_scale) . W^T: the step's normalised
+ * prologue (x fp32, eps added to the mean square, one fixed reduction order
+ * per row) in front of the dequant GEMM; bits in {2,3,4,6,16}, K in {256,
+ * 512}.  act_bf16 = 1 rounds the normalised row to bf16 for the MFMAs (the
+ * reference's bf16 path), 0 keeps it fp32-faithful.  Replaces
+ * logits_stage_rows(src, weight, logit_buf) (src/xsa_ttt/ac_gemv.py:562-582).
+ */
+int32_t altxs_rms_qgemm(const AltxsQTensor *w, const float *x, int64_t rows, float ln_scale,
+                        float eps, int32_t act_bf16, float *y, altxs_stream_t stream);
 
 /*
  * KV cache layout.  Per (segment, kv head) the cache holds max_len keys of

@@ -8,8 +8,13 @@ altxs_pack_dense) and the dense bf16 step it feeds.
 * end to end: a codec written in the reference's file format (json +
   safetensors) for the "tiny" config, plus an Init state, decodes and packs on
   the device, and the step on those weights matches the fp32 oracle run on
-  bf16(Init + delta).  (The reference's own asset is not on the GPU box; the
-  oracle decoder is pinned against it on the CPU.)
+  bf16(Init + delta);
+* the real asset: slices of every bank of the reference's shipped codec
+  (weights/mixed_da_bpw3.15_upb1.8; packed bytes, bit widths and codebook
+  rows, tests/golden/shipped_slice.npz) decode on the device to exactly the
+  values the reference's own decoder produced from the whole bank, and the
+  five codebook modes decode to the reference's outputs on its vectors
+  (tests/golden/codec_modes.npz).  (The asset itself is not on the GPU box.)
 """
 
 from __future__ import annotations
@@ -184,3 +189,56 @@ def test_shipped_codec_end_to_end(tmp_path):
     err = np.abs(got - want).max()
     _log(f"max |dlogit| = {err:.3e}")
     assert err < 2e-4, err
+    # the reference-named loader gives the same step model
+    from altxs_amd import dropin
+
+    model2, meta2, _ = dropin.load_codec(stem + ".safetensors", device="cuda", init_state=init, act="fp32")
+    assert meta2["codebook_mode"] == "lloyd"
+    st2 = model2.make_static_state(256, win=1, batch=2)
+    for t in range(toks.shape[1]):
+        st2.token.copy_(torch.from_numpy(toks[:, t:t + 1]))
+        model2.step(st2, commit=True)
+        assert np.array_equal(st2.logits.cpu().numpy(), got[:, t])
+
+
+def _decode_on_device(bits, packed, books, mode, width, scales=None):
+    from altxs_amd import shipped
+
+    bank = shipped.DeviceBank(bits, packed, books, mode, scales, "cuda")
+    n = int(np.asarray(bits).size)
+    out = torch.full((n * width,), float("nan"), dtype=torch.float32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bank.decode(shipped.Part(0, n, "x", 0, width, 1), width, out, err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    return out.view(n, width).cpu().numpy()
+
+
+def test_shipped_asset_slices_decode_like_the_reference(golden_dir):
+    import os
+
+    _log("shipped asset slices on the device")
+    z = np.load(os.path.join(golden_dir, "shipped_slice.npz"))
+    mode = str(z["mode"])
+    for bank in ("tok_emb.weight", "qo_bank", "kv_bank", "mlp_up_bank", "mlp_down_bank"):
+        bits = z[f"{bank}/bits"]
+        packed = {b: z[f"{bank}/packed_b{b}"] for b in (2, 3, 4)}
+        books = {b: z[f"{bank}/codebook_b{b}"] for b in (2, 3, 4)}
+        got = _decode_on_device(bits, packed, books, mode, int(z[f"{bank}/width"]))
+        want = z[f"{bank}/out"]
+        assert got.view(np.uint32).tolist() == want.view(np.uint32).tolist(), bank
+
+
+@pytest.mark.parametrize("mode", ["lloyd", "symmetric", "shared", "fp4", "hybrid_fp4_symmetric"])
+def test_codec_modes_decode_like_the_reference(golden_dir, mode):
+    import os
+
+    _log(f"codec mode {mode} vs reference vectors")
+    z = np.load(os.path.join(golden_dir, "codec_modes.npz"))
+    bits, width = z["bits"], int(z["width"])
+    packed = {b: z[f"{mode}/packed_b{b}"] for b in (2, 3, 4)}
+    books = {b: z[f"{mode}/codebook_b{b}"] for b in (2, 3, 4)}
+    scales = {b: z[f"{mode}/scale_b{b}"] for b in (2, 3, 4) if f"{mode}/scale_b{b}" in z.files} or None
+    got = _decode_on_device(bits, packed, books, mode, width, scales)
+    want = z[f"{mode}/out"]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), mode
