@@ -148,15 +148,17 @@ __device__ __forceinline__ float code_center(int bits) {
 // 2- and 3-bit codes by table: every value c - center is exact in bf16, so a
 // byte table of the bf16 bits, read with v_perm_b32, gives the operand with
 // the same bits as the conversion below at about half the VALU work.
-// lut_bytes<BITS>(hi, half): byte i = low (hi = 0) or high byte of
-// bf16(c - center) for c = 4 * half + i (folded to constants).
-template <int BITS>
+// lut_bytes<BITS, F16>(hi, half): byte i = low (hi = 0) or high byte of
+// bf16(c - center) (fp16 with F16) for c = 4 * half + i (folded to constants).
+template <int BITS, bool F16 = false>
 __device__ __forceinline__ uint32_t lut_bytes(int hi, int half) {
   uint32_t w = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float v = (float)(4 * half + i) - 0.5f * (float)((1 << BITS) - 1);
-    const uint32_t b = __builtin_bit_cast(uint32_t, v) >> 16;  // exact: at most 3 mantissa bits
+    // exact in either format: at most 3 mantissa bits
+    const uint32_t b = F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v)
+                           : __builtin_bit_cast(uint32_t, v) >> 16;
     w |= ((hi ? b >> 8 : b) & 0xFFu) << (8 * i);
   }
   return w;
@@ -171,13 +173,13 @@ __device__ __forceinline__ uint32_t spread1to8(uint32_t x) {
   x = (x | (x << 14)) & 0x00030003u;
   return (x | (x << 7)) & 0x01010101u;
 }
-// Four codes (one per byte of c4) -> two words of bf16 pairs.
-template <int BITS>
+// Four codes (one per byte of c4) -> two words of bf16 (fp16 with F16) pairs.
+template <int BITS, bool F16 = false>
 __device__ __forceinline__ void lut4(uint32_t c4, uint32_t& w01, uint32_t& w23) {
   // v_perm_b32: byte selector k < 4 takes byte k of the second source, 4..7
   // byte k - 4 of the first
-  const uint32_t lo = __builtin_amdgcn_perm(lut_bytes<BITS>(0, 1), lut_bytes<BITS>(0, 0), c4);
-  const uint32_t hi = __builtin_amdgcn_perm(lut_bytes<BITS>(1, 1), lut_bytes<BITS>(1, 0), c4);
+  const uint32_t lo = __builtin_amdgcn_perm(lut_bytes<BITS, F16>(0, 1), lut_bytes<BITS, F16>(0, 0), c4);
+  const uint32_t hi = __builtin_amdgcn_perm(lut_bytes<BITS, F16>(1, 1), lut_bytes<BITS, F16>(1, 0), c4);
   w01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
   w23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
 }
@@ -244,6 +246,37 @@ __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* 
 template <int BITS>
 __device__ __forceinline__ f16x8 b_op_f16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
   static_assert(BITS != 16, "dense bf16 weights take bf16 or fp32 activations");
+  if constexpr (BITS == 2 || BITS == 3) {  // the bf16 path's byte table, with fp16 bytes
+    const uint32_t f0 = (p0[s >> 1] >> (16 * (s & 1))) & 0xFFFFu;
+    uint32_t ca = spread2to8(f0 & 0xFFu), cb = spread2to8(f0 >> 8);
+    if constexpr (BITS == 3) {
+      const uint32_t f1 = (p1[s >> 2] >> (8 * (s & 3))) & 0xFFu;
+      ca |= spread1to8(f1 & 0xFu) << 2;
+      cb |= spread1to8(f1 >> 4) << 2;
+    }
+    uint32_t r0, r1, r2, r3;
+    lut4<BITS, true>(ca, r0, r1);
+    lut4<BITS, true>(cb, r2, r3);
+    return __builtin_bit_cast(f16x8, u32x4{r0, r1, r2, r3});
+  }
+  if constexpr (BITS == 4) {
+    // fp16 0x4C00 | (c << 6) is exactly 16 + c (the mantissa step at 16 is
+    // 1/64), and (16 + c) - 23.5 = c - 7.5 exactly: the generic path's value.
+    // Byte j of t / u holds code 2j / 2j + 1 of the k-step.
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+    const uint32_t w = p0[s];
+    const uint32_t t = w & 0x0F0F0F0Fu, u = (w >> 4) & 0x0F0F0F0Fu;
+    const f16x2 off = {(_Float16)-23.5f, (_Float16)-23.5f};
+    uint32_t r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // bytes [t_j, 0, u_j, 0]: code 2j in bits 0-3, code 2j + 1 in bits 16-19
+      const uint32_t sel = (uint32_t)j | (0x0Cu << 8) | ((uint32_t)(4 + j) << 16) | (0x0Cu << 24);
+      const uint32_t m = (__builtin_amdgcn_perm(u, t, sel) << 6) | 0x4C004C00u;
+      r[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, m) + off);
+    }
+    return __builtin_bit_cast(f16x8, u32x4{r[0], r[1], r[2], r[3]});
+  }
   const float center = code_center<BITS>(bits);
   uint32_t c[8];
   codes_step<BITS == 0 ? 6 : BITS>(p0, p1, s, c);
@@ -696,13 +729,21 @@ __host__ __device__ constexpr size_t big_lds_bytes() {
   return a > c ? a : c;
 }
 
-template <int BITS, int NB, int KS, class Epi>
+// AM: A_BF16 (bf16 rows, bf16 MFMAs) or A_F16 (fp16 rows, fp16 MFMAs; the
+// operands are the same exact values).  blockIdx.z = batch: tensors at fixed
+// code / scale strides, A shared, the epilogue told the batch index.
+template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
 // Two workgroups per CU (at most 256 VGPRs a lane): the 4 x 2 accumulator
 // blocks per wave, their K-slice totals, the next k-block's weights and A rows
 // in flight.
 __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uint16_t* __restrict__ A,
-                                                          Epi epi) {
+                                                          Epi epi, int64_t codes_stride,
+                                                          int64_t scales_stride) {
+  static_assert(AM == A_BF16 || AM == A_F16, "16-bit A rows");
   using Cfg = TileCfg<NB, KS>;
+  const int batch = blockIdx.z;
+  w.codes += batch * codes_stride;
+  w.scales += batch * scales_stride;
   static_assert(Cfg::THREADS == 256, "the epilogues run on four waves");
   constexpr int MB = BIG_M / 16, NSUB = BIG_N / Cfg::NCOL;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -769,13 +810,23 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
       scale[j][0] = half_lo(wb[j].sc[0]); scale[j][1] = half_hi(wb[j].sc[0]);
       scale[j][2] = half_lo(wb[j].sc[1]); scale[j][3] = half_hi(wb[j].sc[1]);
     }
+    using BOp = std::conditional_t<AM == A_F16, f16x8, bf16x8>;
+    auto mfma = [](u32x4 a, BOp b, f32x4 c) {
+      if constexpr (AM == A_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
+      else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+    };
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      bf16x8 bo[2][2];
+      BOp bo[2][2];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int ss = 0; ss < 2; ++ss) bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+        for (int ss = 0; ss < 2; ++ss) {
+          if constexpr (AM == A_F16) bo[j][ss] = b_op_f16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+          else bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+        }
       // the 2*MB independent MFMA chains of the group first, then the scaled
       // accumulation (the same per-block arithmetic as compute_blk; issuing the
       // chains back to back keeps the matrix pipe busy instead of waiting on
@@ -793,14 +844,12 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          t[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ar[0][mb]), bo[j][0],
-                                                             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          t[mb][j] = mfma(ar[0][mb], bo[j][0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          t[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ar[1][mb]), bo[j][1],
-                                                             t[mb][j], 0, 0, 0);
+          t[mb][j] = mfma(ar[1][mb], bo[j][1], t[mb][j]);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -857,17 +906,18 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
     using P = decltype(epi.template prefetch<Cfg>(0, 0, 0, 0));
     P pre[NSUB];
 #pragma unroll
-    for (int c = 0; c < NSUB; ++c) pre[c] = epi.template prefetch<Cfg>(r0, n0 + c * Cfg::NCOL, R, 0);
+    for (int c = 0; c < NSUB; ++c) pre[c] = epi.template prefetch<Cfg>(r0, n0 + c * Cfg::NCOL, R, batch);
 #pragma unroll
     for (int c = 0; c < NSUB; ++c)
       epi.template apply<Cfg>(Cs + (size_t)(mb * NSUB + c) * 16 * Cfg::CS, pre[c], nullptr, r0,
-                              n0 + c * Cfg::NCOL, R, 0);
+                              n0 + c * Cfg::NCOL, R, batch);
   }
 }
 
-template <int BITS, int NB, int KS, class Epi>
-hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& epi, hipStream_t s) {
-  auto kfn = gemm_big_kernel<BITS, NB, KS, Epi>;
+template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
+hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& epi, hipStream_t s,
+                             int batch = 1, int64_t codes_stride = 0, int64_t scales_stride = 0) {
+  auto kfn = gemm_big_kernel<BITS, NB, KS, Epi, AM>;
   constexpr size_t lds = big_lds_bytes<NB, KS>();
   static bool configured = false;
   if (!configured) {
@@ -876,8 +926,8 @@ hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& e
     if (e != hipSuccess) return e;
     configured = true;
   }
-  dim3 grid((unsigned)(w.N / BIG_N), (unsigned)((R + BIG_M - 1) / BIG_M));
-  hipLaunchKernelGGL(kfn, grid, dim3(256), lds, s, w, R, A, epi);
+  dim3 grid((unsigned)(w.N / BIG_N), (unsigned)((R + BIG_M - 1) / BIG_M), (unsigned)batch);
+  hipLaunchKernelGGL(kfn, grid, dim3(256), lds, s, w, R, A, epi, codes_stride, scales_stride);
   return hipGetLastError();
 }
 

@@ -57,14 +57,30 @@ hipError_t run_gemm(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss
                     int64_t rows, float* y, hipStream_t s) {
   QT q = to_qt(w);
   EpiStore epi{y, q.N, rows * q.N};
-  const int KB = (int)(w->K / 256);
-  if (KB % 4 == 0)
-    return launch_gemm_bits<AM, 2, 4>(w->bits, q, (int)rows, (int)count, cs, ss, ADirect{x, 0},
-                                      ProNone{}, epi, 0, s);
-  if (KB % 2 == 0)
-    return launch_gemm_bits<AM, 2, 2>(w->bits, q, (int)rows, (int)count, cs, ss, ADirect{x, 0},
-                                      ProNone{}, epi, 0, s);
-  return launch_gemm_bits<AM, 2, 1>(w->bits, q, (int)rows, (int)count, cs, ss, ADirect{x, 0},
+  // Every launch shape uses (NB, KS) = (4, 1) -- each wave a 16-column block
+  // over the whole K, groups in increasing k -- so a row's result does not
+  // depend on the number of rows or matrices.  16-row tiles, one workgroup
+  // per 64 columns: B = 1 streams 2.3-4.1 TB/s over >= 2 GB of 2..6-bit
+  // matrices (the K-split shapes (2,2), (1,4), (2,4), (4,2) reached 1.5-2.6
+  // TB/s).  With 16-bit x and more rows, 64 x 128 tiles decode each weight
+  // once per 64 rows instead of once per 16 (bit-identical); they are used
+  // when the launch still fills the chip (>= 256 workgroups), so a single
+  // small GEMM keeps the wider 16-row grid.
+  if constexpr (AM != A_F32) {
+    const int64_t big_wgs = count * (w->N / BIG_N) * ((rows + BIG_M - 1) / BIG_M);
+    if (rows > 16 && w->N % BIG_N == 0 && w->bits <= 6 && big_wgs >= 256) {
+      const uint16_t* A = (const uint16_t*)x;
+      const int R = (int)rows, C = (int)count;
+      switch (w->bits) {
+        case 2: return launch_gemm_big_t<2, 4, 1, EpiStore, AM>(q, R, A, epi, s, C, cs, ss);
+        case 3: return launch_gemm_big_t<3, 4, 1, EpiStore, AM>(q, R, A, epi, s, C, cs, ss);
+        case 4: return launch_gemm_big_t<4, 4, 1, EpiStore, AM>(q, R, A, epi, s, C, cs, ss);
+        case 6: return launch_gemm_big_t<6, 4, 1, EpiStore, AM>(q, R, A, epi, s, C, cs, ss);
+        default: break;
+      }
+    }
+  }
+  return launch_gemm_bits<AM, 4, 1>(w->bits, q, (int)rows, (int)count, cs, ss, ADirect{x, 0},
                                     ProNone{}, epi, 0, s);
 }
 

@@ -52,6 +52,8 @@ def decode_metric(profile: str, B: int, ctx: int, bpw: float | None) -> str:
         return METRIC
     w = "dense bf16" if bpw is None else f"mixed-{bpw:.2f}bpw"
     return f"scored symbols/sec @{profile} {w}, {B} segs ctx{ctx}; % HBM roofline"
+
+
 HBM_PEAK_GBS = 8000.0
 
 
@@ -247,6 +249,117 @@ def window_bench(a) -> int:
     return 0
 
 
+def cfg2_bench(a) -> int:
+    """--cfg2: the fused dequant-GEMV/GEMM microbenchmark (benchmark config 2).
+
+    Weight matrices [N, K] = 512 x 2048 and 2048 x 512 packed at 2, 3, 4 and 6
+    bits (uniform random codes -- uniform random bytes in the tiled planes --
+    and random fp16 group-64 scales), fp16 activations ~N(0, 1), B = 1 and 64
+    rows.  One matrix is at most 0.8 MB and would sit in the 256 MB Infinity
+    Cache, so the HBM figure streams >= 2 GB of distinct matrices through one
+    ``altxs_qgemm_stream`` launch (each matrix's y written to its own rows);
+    algorithmic bytes per launch = codes + scales + y of every matrix + x
+    once.  The single-call latency is ``altxs_qgemm`` on one matrix, replayed
+    from a HIP graph (cache-resident, launch included).  MFMA figures count
+    the useful 2*N*K*B flops against the dense fp16 peak (2.5 PFLOP/s); at
+    B = 1 the 16-row MFMA tiles carry 15 empty rows."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from altxs_amd import _lib
+
+    L = _lib.load()
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    g = torch.Generator(device="cuda").manual_seed(2)
+    target = float(a.cfg2_gb) * 1e9
+    results = []
+    for (N, K) in ((512, 2048), (2048, 512)):
+        for bits in (2, 3, 4, 6):
+            cb = N * K * bits // 8
+            sb = N * K // 64 * 2
+            cs, ss = (cb + 255) // 256 * 256, (sb + 255) // 256 * 256
+            count = int(min(65535, max(1, -(-target // (cb + sb)))))
+            codes = torch.randint(0, 256, (count * cs,), dtype=torch.uint8, device="cuda", generator=g)
+            scales = (torch.rand(count * ss // 2, device="cuda", generator=g) * 0.05 + 0.001).half()
+            qt = _lib.QTensor(codes.data_ptr(), scales.data_ptr(), N, K, bits, 0)
+            for B in (1, 64):
+                x = torch.randn(B, K, device="cuda", generator=g).half()
+                y = torch.empty(count, B, N, dtype=torch.float32, device="cuda")
+                run = lambda: _lib.check(L.altxs_qgemm_stream(  # noqa: E731
+                    ctypes.byref(qt), count, cs, ss, x.data_ptr(), _lib.F16, B, y.data_ptr(), stream()),
+                    "altxs_qgemm_stream")
+                run()
+                torch.cuda.synchronize()
+                # spot check: the first and last matrix against dequant + fp64 matmul
+                for i in (0, count - 1):
+                    qi = _lib.QTensor(codes.data_ptr() + i * cs, scales.data_ptr() + i * ss, N, K, bits, 0)
+                    w = torch.empty(N, K, device="cuda")
+                    _lib.check(L.altxs_dequant(ctypes.byref(qi), w.data_ptr(), stream()), "altxs_dequant")
+                    ref = x.double() @ w.double().T
+                    err = (y[i].double() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+                    if err > 1e-3:
+                        raise RuntimeError(f"cfg2 check failed: [{N},{K}] b={bits} B={B} matrix {i}: {err:.2e}")
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                reps = 5
+                e0.record()
+                for _ in range(reps):
+                    run()
+                e1.record()
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / reps
+                nbytes = count * (cb + sb + B * N * 4) + B * K * 2
+                flops = 2.0 * N * K * B * count
+                # single call on one matrix, from a graph of 50 calls
+                y1 = torch.empty(B, N, dtype=torch.float32, device="cuda")
+                one = lambda: L.altxs_qgemm(ctypes.byref(qt), x.data_ptr(), _lib.F16, B,  # noqa: E731
+                                            y1.data_ptr(), stream())
+                one()
+                torch.cuda.synchronize()
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    for _ in range(50):
+                        one()
+                gr.replay()
+                torch.cuda.synchronize()
+                e0.record()
+                gr.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                us1 = e0.elapsed_time(e1) / 50 * 1e3
+                r = {"N": N, "K": K, "bits": bits, "B": B, "matrices": count,
+                     "stream_bytes": int(nbytes), "ms_per_launch": round(ms, 4),
+                     "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+                     "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4),
+                     "single_call_us": round(us1, 2)}
+                log(f"[{N},{K}] b={bits} B={B}: {count} matrices, {ms:.3f} ms, {r['GBps']:.0f} GB/s "
+                    f"({100 * r['hbm_frac']:.1f}% HBM), {r['TFLOPs']:.1f} TFLOP/s; single call {us1:.2f} us")
+                results.append(r)
+                del y, y1, gr
+            del codes, scales
+            torch.cuda.empty_cache()
+    b1 = [r for r in results if r["B"] == 1]
+    value = float(np.mean([r["GBps"] for r in b1]))
+    out = {
+        "metric": "cfg2 fused dequant-GEMV HBM throughput (B=1, >=2 GB of distinct packed matrices, "
+                  "mean over 512x2048 / 2048x512 and 2/3/4/6 bits)",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": 5, "warmup": 1,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: packed group-64 weights, fp16 scales, fp16 activations, B in {1, 64}",
+                   "stream_gb": a.cfg2_gb},
+        "roofline": {"kernel": "gemm_kernel (altxs_qgemm_stream), B=1", "bound": "hbm",
+                     "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+        "results": results,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def coder_bench(a) -> int:
     """--coder: the closed loop of compression on the cfg3 decode workload.
     Compress = step + the range coder encoding each segment's next symbol with
@@ -349,6 +462,10 @@ def main() -> int:
     ap.add_argument("--coder", action="store_true",
                     help="time compression (step + GPU range coder encode) and decompression "
                          "(step + decode into the next step's token buffer) instead")
+    ap.add_argument("--cfg2", action="store_true",
+                    help="the fused dequant-GEMV/GEMM microbenchmark (512x2048 and 2048x512, 2/3/4/6 bits, "
+                         "B=1 and 64) over >= --cfg2-gb GB of distinct packed matrices")
+    ap.add_argument("--cfg2-gb", type=float, default=2.0)
     ap.add_argument("--persistent", action="store_true",
                     help="run every slot in one persistent launch (tasks in dependency order)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -367,6 +484,8 @@ def main() -> int:
     import numpy as np
     import torch
 
+    if a.cfg2:
+        return cfg2_bench(a)
     if a.window > 1:
         return window_bench(a)
     if a.coder:

@@ -122,17 +122,26 @@ def test_qgemm_against_fp32_matmul(bits, shape, B, xdt):
     assert err < 1e-5 * max(1.0, ref.abs().max().item()) * math.sqrt(k)
 
 
-def test_qgemm_batch_invariant():
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(2048, 512), (512, 2048)])
+@pytest.mark.parametrize("bits", [3, 4])
+def test_qgemm_batch_invariant(xdt, shape, bits):
+    """Rows of 1, 17 and 64 (16-row tiles) equal the same rows of a 4200-row
+    launch (64 x 128 tiles for 16-bit x, enough of them to fill the chip) bit
+    for bit."""
     from altxs_amd import ops
 
-    _log("qgemm batch invariance")
-    p = _packed(3, 2048, 512, seed=3)
+    _log(f"qgemm batch invariance {xdt} {shape} b={bits}")
+    n, k = shape
+    p = _packed(bits, n, k, seed=3)
     w = ops.DeviceQTensor(p)
-    x = torch.randn(64, 512, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(DEV)
-    y64 = ops.qgemm(w, x)
-    for r in (0, 5, 31, 63):
+    x = torch.randn(4200, k, generator=torch.Generator().manual_seed(0)).to(xdt).to(DEV)
+    y_all = ops.qgemm(w, x)
+    y64 = ops.qgemm(w, x[:64].contiguous())
+    assert torch.equal(y_all[:64], y64)
+    for r in (0, 5, 31, 63, 100, 4199):
         y1 = ops.qgemm(w, x[r:r + 1].contiguous())
-        assert torch.equal(y1[0], y64[r])
+        assert torch.equal(y1[0], y_all[r])
     y17 = ops.qgemm(w, x[:17].contiguous())
     assert torch.equal(y17, y64[:17])
 
@@ -151,6 +160,19 @@ def test_qgemm_stream_matches_single():
     ops.qgemm_stream(codes, scales, count, n, k, bits, cs, ss, x, out)
     for i, p in enumerate(ps):
         assert torch.equal(out[i], ops.qgemm(ops.DeviceQTensor(p), x))
+    # 80 matrices x 40 rows: the stream takes the 64 x 128 tiles (320
+    # workgroups), a single matrix the 16-row tiles; the same bits
+    g = torch.Generator(device=DEV).manual_seed(1)
+    many = 80
+    codes2 = torch.randint(0, 256, (many * cs,), dtype=torch.uint8, device=DEV, generator=g)
+    scales2 = (torch.rand(many * ss // 2, device=DEV, generator=g) * 0.05 + 0.001).half().view(torch.int16)
+    x = torch.randn(40, k, device=DEV, generator=g).to(torch.float16)
+    out = torch.empty(many, 40, n, device=DEV)
+    ops.qgemm_stream(codes2, scales2, many, n, k, bits, cs, ss, x, out)
+    for i in (0, 37, many - 1):
+        one = torch.empty(40, n, device=DEV)
+        ops.qgemm_stream(codes2[i * cs:], scales2[i * ss // 2:], 1, n, k, bits, cs, ss, x, one)
+        assert torch.equal(out[i], one)
 
 
 # ---------------------------------------------------------- attention ----------
