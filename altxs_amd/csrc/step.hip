@@ -285,8 +285,10 @@ struct StepRun {
     return hipGetLastError();
   }
 
-  // QKV of slot s: RMSNorm * ln_scale of the attention input (+ sparse-gate multipliers)
-  hipError_t qkv(const Group& G, int s, hipStream_t st) const {
+  // QKV of slot s: RMSNorm * ln_scale of the attention input (+ sparse-gate
+  // multipliers) in the prologue; QK-RMS, RoPE, q_gain and the K/V write in the
+  // epilogue.
+  void qkv_parts(const Group& G, int s, ProNorm& pro, EpiQKV& epi) const {
     const WS& w = G.w;
     const int R = G.nb * d->W;
     const int64_t Rp = align_up(R, 16), D = d->D;
@@ -294,10 +296,10 @@ struct StepRun {
     const AltxsLayer& L = d->layers[S.layer];
     const bool par = S.kind == ALTXS_SLOT_PAR;
     const float* attn_in = par ? w.QIN + (s & 1) * Rp * D : w.XIN + (s & 1) * Rp * D;
-    ProNorm pro{attn_in, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
+    pro = ProNorm{attn_in, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
     pro.gate_w = (d->flags & ALTXS_F_SPARSE_GATE) ? L.attn_gate_w : nullptr;
     pro.gate_out = w.GATE; pro.gate_scale = d->gate_scale; pro.H = d->H; pro.gw = d->gate_window;
-    EpiQKV epi;
+    epi = EpiQKV{};
     epi.q = w.Q; epi.kv = slot_kv(G, s); epi.kv_bf16 = d->kv_bf16; epi.H = d->H; epi.Hkv = d->Hkv;
     epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = G.pos;
     epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
@@ -307,6 +309,16 @@ struct StepRun {
       epi.lora_s = S.lora_scale; epi.rank = d->lora_rank;
     }
     epi.D = d->D; epi.a_f32 = AM == A_F32 ? 1 : 0;
+  }
+
+  hipError_t qkv(const Group& G, int s, hipStream_t st) const {
+    const WS& w = G.w;
+    const int R = G.nb * d->W;
+    const AltxsSlot& S = d->slots[s];
+    const AltxsLayer& L = d->layers[S.layer];
+    ProNorm pro{};
+    EpiQKV epi{};
+    qkv_parts(G, s, pro, epi);
     if (big(R, L.qkv) && !S.lora_q_a) {  // normalised rows in Y (free until the attention)
       hipError_t e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st);
       if (e != hipSuccess) return e;
@@ -326,7 +338,7 @@ struct StepRun {
     return G.kv + (int64_t)s * d->B * 2 * d->Hkv * d->max_len * HD * esz;
   }
 
-  hipError_t attn(const Group& G, int s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) const {
+  AltxsAttnArgs attn_args(const Group& G, int s) const {
     const WS& w = G.w;
     const AltxsLayer& L = d->layers[d->slots[s].layer];
     const int64_t esz = d->kv_bf16 ? 2 : 4;
@@ -340,6 +352,11 @@ struct StepRun {
     a.gate = (d->flags & ALTXS_F_SPARSE_GATE) ? w.GATE : nullptr;
     a.use_xsa = L.use_xsa; a.y = w.Y; a.err = d->err;
     a.flags = AM == A_BF16 ? ALTXS_ATTN_OPS_BF16 : 0;
+    return a;
+  }
+
+  hipError_t attn(const Group& G, int s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) const {
+    const AltxsAttnArgs a = attn_args(G, s);
     hipError_t e;
     if (ev0 && (e = hipEventRecord(ev0, st)) != hipSuccess) return e;
     if ((e = altxs_launch_attn(a, st)) != hipSuccess) return e;
@@ -599,11 +616,11 @@ hipError_t run_split(const AltxsStepDesc* d, const Group (&G)[2], hipStream_t s0
     if ((e = run.embed(G[g], st[g])) != hipSuccess) return e;
     for (int s = 0; s < n; ++s) {
       const bool fk = g == 0 && s == 0;
+      const int k = (g * n + s) * 2;
+      hipEvent_t e0 = ev ? ev[k] : nullptr, e1 = ev ? ev[k + 1] : nullptr;
       if ((e = run.qkv(G[g], s, st[g])) != hipSuccess) return e;
       if (fk && fork == 0 && (e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
-      const int k = (g * n + s) * 2;
-      if ((e = run.attn(G[g], s, st[g], ev ? ev[k] : nullptr, ev ? ev[k + 1] : nullptr)) != hipSuccess)
-        return e;
+      if ((e = run.attn(G[g], s, st[g], e0, e1)) != hipSuccess) return e;
       if (fk && fork == 1 && (e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
       if ((e = run.mlp(G[g], s, st[g])) != hipSuccess) return e;
       if (fk && fork >= 2 && (e = hipEventRecord(sync[0], s0)) != hipSuccess) return e;
