@@ -28,7 +28,10 @@ with F.scaled_dot_product_attention (tests/test_oracle_model.py).
 1238-1271, with ``_softmax_np``, compress.py:64-85); pinned by rows the
 reference's ``StaticACEngine`` wrote (tests/golden/engine_rows.npz).
 
-``act="bf16"`` additionally rounds, exactly where the GPU's bf16 mode does,
+``act="bf16"`` (parity unpinned: a diagnostic, not a gate -- nothing the
+reference wrote fixes these rounding points, and the GPU's bf16 mode is gated
+on coded bits/symbol against the fp32 path instead) additionally rounds,
+exactly where the GPU's bf16 mode does,
 the GEMM inputs (normed activations, attention output, MLP hidden), the
 K/V entries written to the cache (the cached values are the ones attention
 and XSA read) and the query as the score operand.  The GPU's bf16 mode also
