@@ -1,6 +1,8 @@
 // Decode attention device code shared by the standalone kernels (attn.hip)
 // and the persistent layer kernel (step.hip).  See attn.hip for the design.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 #ifndef ALTXS_ATT_WAVES
@@ -326,7 +328,10 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
 #pragma unroll
     for (int i = 0; i < 8; ++i) vr[i] = vt[64 * i];
   };
-  auto tile = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8], int T) {
+  // MASK = false: a tile whose keys all precede every query of the workgroup
+  // (no key is masked for any of them, so skipping the mask changes nothing)
+  auto tile = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8], int T, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int k0 = T * TILE;
 #pragma unroll
     for (int gi = 0; gi < NG; ++gi) {
@@ -347,19 +352,22 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
       for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (k0 + 16 * blk + 4 * lg + i > pc[gi]) S[blk][i] = -INFINITY;
+          if (MASK && k0 + 16 * blk + 4 * lg + i > pc[gi]) S[blk][i] = -INFINITY;
           mt = fmaxf(mt, S[blk][i]);
         }
       mt = rows_max(mt);
       const float m_new = fmaxf(m_run[gi], mt);
-      const bool none = m_new == -INFINITY;  // no key of this query seen yet
-      const float alpha = none ? 1.f : __expf(m_run[gi] - m_new);
+      // A query with no key seen yet (m_new = -inf) subtracts 0 instead: its
+      // scores give exp(-inf) = 0 and alpha = 0, which leaves its state (l = 0,
+      // acc = 0) exactly as alpha = 1 and P = 0 would.
+      const float mu = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __expf(m_run[gi] - mu);
       float ps = 0.f;
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          S[blk][i] = none ? 0.f : __expf(S[blk][i] - m_new);
+          S[blk][i] = __expf(S[blk][i] - mu);
           ps += S[blk][i];
         }
       l_part[gi] = l_part[gi] * alpha + ps;
@@ -393,10 +401,21 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
   // that keeps NG = 2 at 164 VGPRs, three waves per SIMD, whose interleaving
   // hides the load latency far better than a second register buffer at one
   // wave per SIMD (288 VGPRs; cfg4: 0.93 vs 2.1 ms per slot).
-  for (int T = wave; T < ntiles; T += ATT_WAVES) {
+  // Tiles below the diagonal of every query first, without the mask (two
+  // loops rather than a branch in one: the branch costs the third wave).
+  int t_first = t0 + 16 * NG <= a.W ? base + t0 : -1;  // lowest query position, all active
+  t_first = t_first >= a.max_len ? -1 : t_first;
+  const int nfull = t_first < 0 ? 0 : (t_first + 1) / TILE;  // tiles 0 .. nfull-1 unmasked
+  int T = wave;
+  for (; T < nfull; T += ATT_WAVES) {
     u32x4 kr[8], vr[8];
     load_t(kr, vr, T);
-    tile(kr, vr, T);
+    tile(kr, vr, T, std::false_type{});
+  }
+  for (; T < ntiles; T += ATT_WAVES) {
+    u32x4 kr[8], vr[8];
+    load_t(kr, vr, T);
+    tile(kr, vr, T, std::true_type{});
   }
   // merge and store, one group of 16 queries at a time (wave w: queries w, w+4, ...)
 #pragma unroll

@@ -188,12 +188,10 @@ hipError_t launch_y(const AttnP& p, int group, bool kv_bf16, bool ops_bf16, bool
   do { hipLaunchKernelGGL(K, wgrid, block, 0, s, p); return hipGetLastError(); } while (0)
     if (ops_bf16) {
       if (ng == 1) WIN_GO((attn_window_kernel<1, 1, YBF16>));
-      if (ng == 2) WIN_GO((attn_window_kernel<2, 1, YBF16>));
-      WIN_GO((attn_window_kernel<4, 1, YBF16>));
+      WIN_GO((attn_window_kernel<2, 1, YBF16>));
     } else {
       if (ng == 1) WIN_GO((attn_window_kernel<1, 3, YBF16>));
-      if (ng == 2) WIN_GO((attn_window_kernel<2, 3, YBF16>));
-      WIN_GO((attn_window_kernel<4, 3, YBF16>));
+      WIN_GO((attn_window_kernel<2, 3, YBF16>));
     }
 #undef WIN_GO
   }

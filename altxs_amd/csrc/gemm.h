@@ -914,9 +914,223 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row-band variant for K = 512 (every stage but the MLP down-projection): the
+// workgroup's 64 A rows stay in LDS for the whole launch -- one 1 KB
+// global->LDS DMA per row, no register staging, no barrier inside the k-loop
+// -- and the workgroup walks column tiles ct = cx, cx + gridDim.x, ... of the
+// same rows, so a row band is read from L2/HBM once per workgroup instead of
+// once per column tile.  The weights of the next (column tile, k-block) are
+// loaded while the current one computes, across tile boundaries.  The
+// epilogue runs one 16-row strip at a time through a small LDS strip (the A
+// band must stay), which keeps two workgroups per CU.
+//
+// The MFMA sequence of every 16x16 output block is gemm_big_kernel's (and so
+// gemm_task's): same k-steps in the same order, acc += scale * t per 64-wide
+// group, K-slices of K/KS from zero added in order, and each strip is laid
+// out in LDS exactly as gemm_big_kernel lays out that strip.
+// ---------------------------------------------------------------------------
+constexpr int BAND_K = 512, BAND_AST = BAND_K + 8;  // A row stride in LDS: 1040 B
+
+template <int NB, int KS>
+__host__ __device__ constexpr size_t band_lds_bytes() {
+  using Cfg = TileCfg<NB, KS>;
+  return (size_t)BIG_M * BAND_AST * 2 + (size_t)(BIG_N / Cfg::NCOL) * 16 * Cfg::CS * 4;
+}
+
+template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
+__global__ __launch_bounds__(256, 2) void gemm_band_kernel(QT w, int R, const uint16_t* __restrict__ A,
+                                                           Epi epi, int64_t codes_stride,
+                                                           int64_t scales_stride) {
+  static_assert(AM == A_BF16 || AM == A_F16, "16-bit A rows");
+  using Cfg = TileCfg<NB, KS>;
+  static_assert(Cfg::THREADS == 256, "the epilogues run on four waves");
+  constexpr int MB = BIG_M / 16, NSUB = BIG_N / Cfg::NCOL, KB = BAND_K / 256, KBS = KB / KS;
+  const int batch = blockIdx.z;
+  w.codes += batch * codes_stride;
+  w.scales += batch * scales_stride;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  uint16_t* As = (uint16_t*)smem;
+  float* Cs = (float*)(smem + (size_t)BIG_M * BAND_AST * 2);  // one 16-row strip
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // every column group of a row band on one XCD, consecutively (as in
+  // gemm_big_kernel): the band enters that XCD's L2 once
+  int cx = blockIdx.x, ry = blockIdx.y;
+  if (gridDim.y % 8 == 0) {
+    const int bid = blockIdx.x + gridDim.x * blockIdx.y;
+    const int j = bid / 8;
+    ry = bid % 8 + 8 * (j / gridDim.x);
+    cx = j % gridDim.x;
+  }
+  const int m0 = ry * BIG_M, NT = w.N / BIG_N, GX = gridDim.x;
+  auto nblk = [&](int ct) { return ct * (BIG_N / 16) + 2 * wave; };  // this wave's first weight block
+
+  // the band: row r of the tile at As + r * BAND_AST, lane l bringing k = 8l .. 8l+7
+#pragma unroll 4
+  for (int i = 0; i < BIG_M / 4; ++i) {
+    const int r = wave * (BIG_M / 4) + i;
+    if (m0 + r < R)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(A + (int64_t)(m0 + r) * BAND_K + lane * 8),
+          (__attribute__((address_space(3))) void*)(As + r * BAND_AST), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  using BOp = std::conditional_t<AM == A_F16, f16x8, bf16x8>;
+  auto mfma = [](u32x4 a, BOp b, f32x4 c) {
+    if constexpr (AM == A_F16)
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+  };
+  using WBlk = Blk<BITS, A_BF16, false>;
+  WBlk wt[KB][2];  // a column tile's weights, both k-blocks
+  auto load_tile_w = [&](WBlk(&d)[KB][2], int ct) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      load_w(d[kb][0], w, nblk(ct), kb, lane);
+      load_w(d[kb][1], w, nblk(ct) + 1, kb, lane);
+    }
+  };
+  load_tile_w(wt, cx);
+  for (int ct = cx; ct < NT; ct += GX) {
+    const int n0 = ct * BIG_N;
+    f32x4 acc[MB][2], tot[MB][2];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = tot[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const WBlk(&wb)[2] = wt[kb];
+      float scale[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        scale[j][0] = half_lo(wb[j].sc[0]); scale[j][1] = half_hi(wb[j].sc[0]);
+        scale[j][2] = half_lo(wb[j].sc[1]); scale[j][3] = half_hi(wb[j].sc[1]);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        BOp bo[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int ss = 0; ss < 2; ++ss) {
+            if constexpr (AM == A_F16) bo[j][ss] = b_op_f16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+            else bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+          }
+        f32x4 t[MB][2];
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+          u32x4 ar[MB];
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            ar[mb] = *(const u32x4*)(As + (mb * 16 + (lane & 15)) * BAND_AST + kb * 256 + 64 * g +
+                                     32 * ss + 8 * (lane >> 4));
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              t[mb][j] = mfma(ar[mb], bo[j][ss], ss ? t[mb][j] : f32x4{0.f, 0.f, 0.f, 0.f});
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mb][j][i] += scale[j][g] * t[mb][j][i];
+      }
+      if (KS > 1 && (kb + 1) % KBS == 0) {  // end of a K-slice: add it to the slices before (in order)
+        const bool first = kb + 1 == KBS;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tot[mb][j][i] = first ? acc[mb][j][i] : tot[mb][j][i] + acc[mb][j][i];
+            acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+      }
+    }
+    // epilogue: one 16 x 128 strip at a time (one copy of the epilogue code;
+    // the accumulator blocks stay in registers through static indices)
+#pragma unroll 1
+    for (int mb = 0; mb < MB; ++mb) {
+      const int r0 = m0 + 16 * mb;
+#pragma unroll
+      for (int q = 0; q < MB; ++q) {
+        if (q != mb) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = 32 * wave + 16 * j + (lane & 15);
+          float* C = Cs + (size_t)(col / Cfg::NCOL) * 16 * Cfg::CS;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            C[(4 * (lane >> 4) + i) * Cfg::CS + col % Cfg::NCOL] = KS > 1 ? tot[q][j][i] : acc[q][j][i];
+        }
+      }
+      __syncthreads();
+      // the next column tile's weights fly during the epilogue (issued behind
+      // the barrier so they do not compete with this tile's operands)
+      if (mb == 0 && ct + GX < NT) load_tile_w(wt, ct + GX);
+      if (r0 < R) {  // uniform
+        bool done = false;
+        if constexpr (epi_has_strip<Epi>::value) {
+          if (epi.strip_ok()) {  // uniform
+            epi.template strip<Cfg>(Cs, r0, n0, R);
+            done = true;
+          }
+        }
+        if (!done) {
+          using P = decltype(epi.template prefetch<Cfg>(0, 0, 0, 0));
+          P pre[NSUB];
+#pragma unroll
+          for (int c = 0; c < NSUB; ++c) pre[c] = epi.template prefetch<Cfg>(r0, n0 + c * Cfg::NCOL, R, batch);
+#pragma unroll
+          for (int c = 0; c < NSUB; ++c)
+            epi.template apply<Cfg>(Cs + (size_t)c * 16 * Cfg::CS, pre[c], nullptr, r0, n0 + c * Cfg::NCOL, R,
+                                    batch);
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Column groups per row band: enough workgroups to fill the chip several times
+// over (two per CU), then as many column tiles per workgroup as that allows.
+inline int band_col_groups(int R, int N, int batch) {
+  const int bands = ((R + BIG_M - 1) / BIG_M) * batch, nt = N / BIG_N;
+  const int want = (4096 + bands - 1) / bands;
+  return want < 1 ? 1 : (want > nt ? nt : want);
+}
+
+template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
+hipError_t launch_gemm_band_t(const QT& w, int R, const uint16_t* A, const Epi& epi, hipStream_t s,
+                              int batch, int64_t codes_stride, int64_t scales_stride) {
+  auto kfn = gemm_band_kernel<BITS, NB, KS, Epi, AM>;
+  constexpr size_t lds = band_lds_bytes<NB, KS>();
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  dim3 grid((unsigned)band_col_groups(R, w.N, batch), (unsigned)((R + BIG_M - 1) / BIG_M), (unsigned)batch);
+  hipLaunchKernelGGL(kfn, grid, dim3(256), lds, s, w, R, A, epi, codes_stride, scales_stride);
+  return hipGetLastError();
+}
+
 template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
 hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& epi, hipStream_t s,
                              int batch = 1, int64_t codes_stride = 0, int64_t scales_stride = 0) {
+  // K = 512 with 16-byte aligned rows: the row-band kernel (same bits)
+  if constexpr ((BAND_K / 256) % KS == 0) {
+    if (w.K == BAND_K && ((uintptr_t)A & 15) == 0)
+      return launch_gemm_band_t<BITS, NB, KS, Epi, AM>(w, R, A, epi, s, batch, codes_stride, scales_stride);
+  }
   auto kfn = gemm_big_kernel<BITS, NB, KS, Epi, AM>;
   constexpr size_t lds = big_lds_bytes<NB, KS>();
   static bool configured = false;
