@@ -712,7 +712,11 @@ hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect&
 // slices are added in slice order, and the epilogue runs on 16 x (16*NB)
 // tiles laid out exactly as gemm_task leaves them in LDS.
 // ---------------------------------------------------------------------------
-constexpr int BIG_M = 64, BIG_N = 128, BIG_AST = 256 + 8;  // A k-block LDS row stride (elements)
+constexpr int BIG_M = 64, BIG_N = 128;
+// A k-block in LDS: 64 rows x 256 bf16 (512 B a row, no padding), the 16-byte
+// chunk c of row r stored at chunk position c ^ (r & 15): the 16 rows an MFMA
+// A-operand read touches at one k then fall on 16 different bank groups.
+__device__ __forceinline__ int big_a_off(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 3); }
 
 // Epilogues that also offer strip<Cfg>(strip C tile, r0, n0, R) -- the same
 // per-element arithmetic over a 16 x BIG_N strip, used when strip_ok() -- set
@@ -724,7 +728,7 @@ struct epi_has_strip<E, std::void_t<decltype(E::kStrip)>> : std::integral_consta
 template <int NB, int KS>
 __host__ __device__ constexpr size_t big_lds_bytes() {
   using Cfg = TileCfg<NB, KS>;
-  const size_t a = (size_t)BIG_M * BIG_AST * 2;
+  const size_t a = (size_t)2 * BIG_M * 256 * 2;  // two A k-block buffers
   const size_t c = (size_t)(BIG_M / 16) * (BIG_N / Cfg::NCOL) * 16 * Cfg::CS * 4;
   return a > c ? a : c;
 }
@@ -774,36 +778,33 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
   load_w(wb[0], w, nb0, 0, lane);
   load_w(wb[1], w, nb0 + 1, 0, lane);
 
-  // A rows m0.. of a k-block: 16-byte chunks, 32 per row, ACH per thread; the
-  // next k-block's chunks are loaded into registers while this one computes
-  constexpr int ACH = BIG_M * 32 / 256;
-  u32x4 av[ACH];
-  auto load_a_blk = [&](int kb) {
+  // A rows m0.. of k-block kb into LDS buffer kb & 1 by global->LDS DMA: one
+  // instruction moves two rows (lane i: row 2q + i / 32, its LDS chunk i % 32
+  // holding global chunk (i % 32) ^ (row & 15)); rows past R are left out
+  auto dma_a_blk = [&](int kb) {
+    uint16_t* buf = As + (kb & 1) * (BIG_M * 256);
+    const int half = lane >> 5, ch = lane & 31;
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int r = c >> 5, k8 = (c & 31) * 8;
-      av[i] = (m0 + r < R) ? *(const u32x4*)(A + (int64_t)(m0 + r) * w.K + kb * 256 + k8)
-                           : u32x4{0u, 0u, 0u, 0u};
+    for (int q = 0; q < BIG_M / 8; ++q) {
+      const int r = wave * (BIG_M / 4) + 2 * q + half;
+      if (m0 + r < R)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(A + (int64_t)(m0 + r) * w.K + kb * 256 +
+                                                           ((ch ^ (r & 15)) << 3)),
+            (__attribute__((address_space(3))) void*)(buf + (wave * (BIG_M / 4) + 2 * q) * 256), 16, 0, 0);
     }
   };
-  auto store_a_blk = [&]() {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      *(u32x4*)(As + (c >> 5) * BIG_AST + (c & 31) * 8) = av[i];
-    }
-  };
-  load_a_blk(0);
-  store_a_blk();
+  dma_a_blk(0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int kb = 0; kb < KB; ++kb) {
     if (kb + 1 < KB) {  // next k-block's A rows and weights fly during this one's MFMAs
-      load_a_blk(kb + 1);
+      dma_a_blk(kb + 1);
       load_w(wn[0], w, nb0, kb + 1, lane);
       load_w(wn[1], w, nb0 + 1, kb + 1, lane);
     }
+    const uint16_t* Ab = As + (kb & 1) * (BIG_M * 256);
     float scale[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -837,8 +838,7 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
       for (int ss = 0; ss < 2; ++ss)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
-          ar[ss][mb] = *(const u32x4*)(As + (mb * 16 + (lane & 15)) * BIG_AST + 64 * g + 32 * ss +
-                                       8 * (lane >> 4));
+          ar[ss][mb] = *(const u32x4*)(Ab + big_a_off(mb * 16 + (lane & 15), 8 * g + 4 * ss + (lane >> 4)));
       f32x4 t[MB][2];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
@@ -870,10 +870,10 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
           }
       }
     }
-    __syncthreads();  // every wave is done with this k-block's A
+    // the next k-block's rows have landed and every wave is done with this one's
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (kb + 1 < KB) {
-      store_a_blk();
-      __syncthreads();
       wb[0] = wn[0];
       wb[1] = wn[1];
     }
@@ -1126,9 +1126,11 @@ hipError_t launch_gemm_band_t(const QT& w, int R, const uint16_t* A, const Epi& 
 template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
 hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& epi, hipStream_t s,
                              int batch = 1, int64_t codes_stride = 0, int64_t scales_stride = 0) {
-  // K = 512 with 16-byte aligned rows: the row-band kernel (same bits)
+  // A rows come by 16-byte global->LDS DMA: 16-byte aligned rows only
+  if (((uintptr_t)A & 15) != 0) return hipErrorInvalidValue;
+  // K = 512: the row-band kernel (same bits)
   if constexpr ((BAND_K / 256) % KS == 0) {
-    if (w.K == BAND_K && ((uintptr_t)A & 15) == 0)
+    if (w.K == BAND_K)
       return launch_gemm_band_t<BITS, NB, KS, Epi, AM>(w, R, A, epi, s, batch, codes_stride, scales_stride);
   }
   auto kfn = gemm_big_kernel<BITS, NB, KS, Epi, AM>;

@@ -68,7 +68,9 @@ hipError_t run_gemm(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss
   // small GEMM keeps the wider 16-row grid.
   if constexpr (AM != A_F32) {
     const int64_t big_wgs = count * (w->N / BIG_N) * ((rows + BIG_M - 1) / BIG_M);
-    if (rows > 16 && w->N % BIG_N == 0 && w->bits <= 6 && big_wgs >= 256) {
+    // (the large tiles read A rows by 16-byte global->LDS DMA: aligned rows only)
+    if (rows > 16 && w->N % BIG_N == 0 && w->bits <= 6 && big_wgs >= 256 && ((uintptr_t)x & 15) == 0 &&
+        w->K % 8 == 0) {
       const uint16_t* A = (const uint16_t*)x;
       const int R = (int)rows, C = (int)count;
       switch (w->bits) {
