@@ -15,11 +15,11 @@ bytes.  Weights are seeded N(0, 0.02^2) then quantised; tokens are Zipf(1.1).
 
 The line also carries:
 * ``roofline``: the decode-attention kernel (the dominant one), algorithmic
-  bytes per launch / its mean launch duration, timed with HIP events on the
-  step's stream around 20 back-to-back launches that walk the ten slots'
-  caches in turn (the same kernel, launch shape and cache footprint as in
-  the step: each launch reads a 268 MB cache the previous nine launches did
-  not touch, so nothing is served from the 256 MB Infinity Cache);
+  bytes per launch / its mean launch duration, timed with HIP events around
+  replays of a HIP graph of 20 launches that walk the ten slots' caches in
+  turn (the same kernel, launch shape and cache footprint as in the step's
+  graph: each launch reads a 268 MB cache the previous nine launches did not
+  touch, so nothing is served from the 256 MB Infinity Cache);
   ``us_per_launch_in_step`` is the mean of events recorded around every
   attention launch inside the timed steps, which also includes each launch's
   gap after the preceding kernel;
@@ -72,11 +72,12 @@ def read_traffic(kernel: str):
     return None
 
 
-def attn_kernel_ms(model, st, reps: int = 20) -> float:
-    """Mean duration of the decode-attention kernel: HIP events around ``reps``
-    back-to-back launches on the step's stream with the step's launch
-    configuration (XSA on, bf16 operands), launch i reading slot i's cache
-    (mod the slot count), as the step's launches do."""
+def attn_kernel_ms(model, st, reps: int = 20, replays: int = 5) -> float:
+    """Mean duration of the decode-attention kernel: ``reps`` launches with the
+    step's launch configuration (XSA on, bf16 operands), launch i reading slot
+    i's cache (mod the slot count) as the step's launches do, captured in one
+    HIP graph (back to back as in the step's own graph, no host launch gaps)
+    and replayed ``replays`` times between HIP events on the replay stream."""
     import ctypes
 
     import torch
@@ -102,17 +103,26 @@ def attn_kernel_ms(model, st, reps: int = 20) -> float:
         a.flags = _lib.ATTN_OPS_BF16 if model.act_bf16 else 0
         a.y, a.err = y.data_ptr(), st.err.data_ptr()
         args.append(a)
-    L, stream = _lib.load(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    L = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for a in args:
         _lib.check(L.altxs_decode_attn(ctypes.byref(a), stream), "altxs_decode_attn")
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(reps):
+            _lib.check(L.altxs_decode_attn(ctypes.byref(args[i % len(args)]), cap), "altxs_decode_attn")
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(reps):
-        L.altxs_decode_attn(ctypes.byref(args[i % len(args)]), stream)
+    for _ in range(replays):
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    del graph
+    return e0.elapsed_time(e1) / (reps * replays)
 
 
 def cpu_model() -> str:
