@@ -19,6 +19,17 @@ using namespace altxs;
 constexpr int HD = 64;
 
 // torch.lerp(start, end, w) (ATen's two-branch formula)
+// Sums of two (three) products in one fixed rounding order: the earlier
+// products rounded, the last one fused into an FMA over them.  Written out
+// because the compiler, free to contract a*b + c*d either way, fuses a
+// different product in different inlining contexts -- and every kernel that
+// produces a value must round it alike (tiles, strips, persistent tasks).
+__device__ __forceinline__ float dot2(float a, float b, float c, float d) {
+  return __builtin_fmaf(c, d, a * b);
+}
+__device__ __forceinline__ float dot3(float a, float b, float c, float d, float e, float f) {
+  return __builtin_fmaf(e, f, __builtin_fmaf(c, d, a * b));
+}
 __device__ __forceinline__ float lerp_t(float start, float end, float w) {
   return (fabsf(w) < 0.5f) ? start + w * (end - start) : end - (end - start) * (1.f - w);
 }
@@ -190,7 +201,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
       for (int e = 0; e < 4; ++e) {
         const float v = x[j][4 * h + e] * inv;
         vo[e] = v;
-        vi[e] = ma[e] * v + mb[e] * v;
+        vi[e] = dot2(ma[e], v, mb[e], v);
       }
       xo[h] = vo;
       xi[h] = vi;
@@ -340,7 +351,7 @@ struct NextIn {
       const float sc = e.sw * (skip_self ? x : e.sk);
       bs = skip_g ? lerp_t(sc, x, sigmoidf(e.sg)) : x + sc;
     }
-    const float in = e.m0 * bs + e.m1 * e.x0;
+    const float in = dot2(e.m0, bs, e.m1, e.x0);
     return {parallel ? bs : in, in};
   }
   __device__ void put(int64_t idx, float x, const El& e) const {
@@ -366,7 +377,7 @@ __device__ __forceinline__ DownOut down_el(float c, float sc, float xo, float l0
                                            const float* pr, const float* pp) {
   const float m = sc * c;
   if (!parallel) return {xo + m, 0.f};
-  return {pr[0] * l0 + pp[0] * xo + pp[2] * m, pr[1] * l1 + pp[1] * xo + pp[3] * m};
+  return {dot3(pr[0], l0, pp[0], xo, pp[2], m), dot3(pr[1], l1, pp[1], xo, pp[3], m)};
 }
 
 // Strips (large-tile kernel, 256 threads): 16 rows x 128 columns, thread t
@@ -535,8 +546,8 @@ struct EpiQKV {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float cs_ = cosb[(int64_t)pp * half + fi + i], sn_ = sinb[(int64_t)pp * half + fi + i];
-          if (cw < half) v[i] = v[i] * cs_ + pv[i] * sn_;
-          else v[i] = pv[i] * -sn_ + v[i] * cs_;
+          if (cw < half) v[i] = dot2(v[i], cs_, pv[i], sn_);
+          else v[i] = dot2(pv[i], -sn_, v[i], cs_);
         }
       }
     }
@@ -601,8 +612,8 @@ struct EpiQKV {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int c = c0 + i;
-        if (c < (rd >> 1)) v[i] = v[i] * pre.cs[i] + pv[i] * pre.sn[i];
-        else if (c < rd) v[i] = pv[i] * -pre.sn[i] + v[i] * pre.cs[i];
+        if (c < (rd >> 1)) v[i] = dot2(v[i], pre.cs[i], pv[i], pre.sn[i]);
+        else if (c < rd) v[i] = dot2(pv[i], -pre.sn[i], v[i], pre.cs[i]);
       }
     }
     if (r >= R) return;

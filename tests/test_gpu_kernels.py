@@ -124,7 +124,7 @@ def test_qgemm_against_fp32_matmul(bits, shape, B, xdt):
 
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("shape", [(2048, 512), (512, 2048)])
-@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("bits", [2, 3, 4, 6])
 def test_qgemm_batch_invariant(xdt, shape, bits):
     """Rows of 1, 17 and 64 (16-row tiles) equal the same rows of a 4200-row
     launch (64 x 128 tiles for 16-bit x, enough of them to fill the chip) bit
