@@ -256,6 +256,46 @@ def test_ragged_rows_large_tiles_bit_identical(profile):
         assert torch.equal(one.cum.cpu(), cm[b]), b
 
 
+def test_second_window_large_tiles_bit_identical():
+    """A committed 100-token window, then a 380-token window from position 100
+    for 3 segments (1140 rows: the large tiles read a prefilled cache, RoPE and
+    the causal mask start mid-tile, smear takes the committed previous token)
+    against the same two windows of each segment alone (16-row GEMMs)."""
+    from altxs_amd import synth
+    from altxs_amd.config import make_config
+    from altxs_amd.model import StepModel
+
+    _log("second window through the large tiles (tiny512)")
+    cfg = make_config("tiny", model_dim=512, num_heads=8, num_kv_heads=4)
+    sm = synth.make_model(cfg, std=0.02, softcap=(30.0, 24.0))
+    B, W1, W2, L = 3, 100, 380, 512
+    toks = np.random.default_rng(12).integers(0, cfg.vocab_size, (B, W1 + W2))
+    model = StepModel(sm, act="bf16")
+
+    def two_windows(tb):
+        s1 = model.make_static_state(L, win=W1, batch=tb.shape[0], want_probs=True)
+        s1.token.copy_(torch.from_numpy(tb[:, :W1].astype(np.int32)))
+        model.step(s1, commit=True)
+        s2 = model.make_static_state(L, win=W2, batch=tb.shape[0], want_probs=True)
+        s2.kv.copy_(s1.kv)
+        s2.pos.copy_(s1.pos)
+        s2.prev_raw.copy_(s1.prev_raw)
+        s2.token.copy_(torch.from_numpy(tb[:, W1:].astype(np.int32)))
+        model.step(s2)
+        torch.cuda.synchronize()
+        s1.check_errors()
+        s2.check_errors()
+        n = tb.shape[0]
+        return (s2.logits.view(n, W2, -1).cpu(), s2.probs.view(n, W2, -1).cpu(), s2.cum.view(n, W2, -1).cpu())
+
+    lg, pr, cm = two_windows(toks)
+    for b in range(B):
+        l1, p1, c1 = two_windows(toks[b:b + 1])
+        assert torch.equal(l1[0], lg[b]), b
+        assert torch.equal(p1[0], pr[b]), b
+        assert torch.equal(c1[0], cm[b]), b
+
+
 def test_bits_per_symbol_within_tenth_percent():
     from oracle import coder
     from oracle.model_ref import softmax_probs
