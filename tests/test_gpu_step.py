@@ -217,26 +217,29 @@ def test_long_window_bit_identical_to_rows(profile, act, B):
     st1.check_errors()
 
 
-@pytest.mark.parametrize("profile", ["tiny512", "cfg4"])
-def test_ragged_rows_large_tiles_bit_identical(profile):
+@pytest.mark.parametrize("profile,kv", [("tiny512", "bf16"), ("cfg4", "bf16"), ("tiny512", "fp32"),
+                                        ("cfg5", "bf16")])
+def test_ragged_rows_large_tiles_bit_identical(profile, kv):
     """3 segments x 361 tokens = 1083 rows, a row count that is no multiple of
     the 64-row bands: the K = 512 stages run the row-band kernel (its last band
     holds 59 rows) and the wider-K down-projection the DMA-fed 64 x 128 tiles;
     each segment's window alone (361 rows) runs the 16-row GEMMs.  Logits,
     probabilities and tables agree bit for bit.  "tiny512" is "tiny" at d = 512
     (GQA 8/4, parallel lanes, skips, depth loops, sparse gate, RoPE on 16 dims),
-    so every branch of the strip epilogues meets a partial band."""
+    so every branch of the strip epilogues meets a partial band; with an fp32
+    KV cache the QKV epilogue takes the per-tile path inside the band kernel;
+    cfg5's LoRA keeps its QKV on the 16-row tiles beside large O/UP/DOWN/LM."""
     from altxs_amd import synth
     from altxs_amd.config import make_config
     from altxs_amd.model import StepModel
 
-    _log(f"ragged rows through the large tiles: {profile}")
+    _log(f"ragged rows through the large tiles: {profile} kv={kv}")
     cfg = (make_config("tiny", model_dim=512, num_heads=8, num_kv_heads=4) if profile == "tiny512"
            else make_config(profile))
     sm = synth.make_model(cfg, std=0.02, softcap=(30.0, 24.0))
     B, T, L = 3, 361, 512
     toks = np.random.default_rng(11).integers(0, cfg.vocab_size, (B, T))
-    model = StepModel(sm, act="bf16")
+    model = StepModel(sm, act="bf16", kv=kv)
     st = model.make_static_state(L, win=T, batch=B, want_probs=True)
     st.token.copy_(torch.from_numpy(toks.astype(np.int32)))
     model.step(st)
