@@ -175,6 +175,32 @@ def test_qgemm_stream_matches_single():
         assert torch.equal(out[i], one)
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bits", [3, 6])
+def test_qgemm_stream_row_band_matches_single(xdt, bits):
+    """K = 512 matrices streamed 60 at a time with 100 rows: the batched
+    row-band kernel (its one band per matrix partly past the 100 rows) gives
+    the bits of each matrix alone on the 16-row tiles."""
+    from altxs_amd import ops
+
+    _log(f"qgemm_stream row band {xdt} b={bits}")
+    many, n, k, rows = 60, 1024, 512, 100
+    g = torch.Generator(device=DEV).manual_seed(7)
+    cs = n * k * bits // 8
+    ss = n * k // 64 * 2
+    codes = torch.randint(0, 256, (many * cs,), dtype=torch.uint8, device=DEV, generator=g)
+    scales = (torch.rand(many * ss // 2, device=DEV, generator=g) * 0.05 + 0.001).half().view(torch.int16)
+    x = torch.randn(rows, k, device=DEV, generator=g).to(xdt)
+    out = torch.empty(many, rows, n, device=DEV)
+    ops.qgemm_stream(codes, scales, many, n, k, bits, cs, ss, x, out)
+    for i in (0, 29, many - 1):
+        for r0, r1 in ((0, 16), (16, 33), (84, 100)):  # 16-row tiles
+            one = torch.empty(r1 - r0, n, device=DEV)
+            ops.qgemm_stream(codes[i * cs:], scales[i * ss // 2:], 1, n, k, bits, cs, ss,
+                             x[r0:r1].contiguous(), one)
+            assert torch.equal(out[i, r0:r1], one), (i, r0)
+
+
 # ---------------------------------------------------------- attention ----------
 
 def _attn_ref(q, k, v, pos, W, gate, use_xsa):
