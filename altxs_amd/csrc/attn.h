@@ -30,44 +30,109 @@ struct AttnP {
 };
 
 // Per-wave partial results, merged in wave order by the whole workgroup.
-template <int G> struct MergeLds {
+template <int G> struct alignas(16) MergeLds {
   float m[ATT_WAVES][G];
   float l[ATT_WAVES][G];
   float acc[ATT_WAVES][G][HD];
 };
 
-// Wave `wave` < G finishes query head g*G + wave: merge, XSA, gate, store.
-// v_at(p, d) returns the current token's value entry.
+// What the last step of a query row reads besides the partials: the current
+// token's value entries (XSA) and the row's gate multiplier.
+template <int NK>
+struct RowExtras {
+  float vv[NK];
+  float gv;
+};
+template <int NK, class VAt>
+__device__ __forceinline__ RowExtras<NK> row_extras(const AttnP& a, int r, int h, int p, int c, VAt v_at) {
+  RowExtras<NK> e;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) e.vv[k] = a.use_xsa ? v_at(p, c + 16 * k) : 0.f;
+  e.gv = a.gate ? a.gate[(int64_t)r * a.H + h] : 1.f;
+  return e;
+}
+
+// Sum over the 64 dims of a row of per-dim values x (layouts of finish_query):
+// (x[c] + x[c+16]) + (x[c+32] + x[c+48]) for each c, then the 16 of these
+// through the DPP butterfly.  NK = 4 forms the bracket in-lane, NK = 1 with
+// the lane swaps of rows_sum; every add pairs the same two values, so both
+// give the same bits, in every lane (rows_sum_ds: rows_sum's pairs).
+template <int NK>
+__device__ __forceinline__ float row_dims_sum(const float (&x)[NK]) {
+#pragma clang fp contract(off)
+  if constexpr (NK == 4) return row16_sum((x[0] + x[1]) + (x[2] + x[3]));
+  else return row16_sum(rows_sum_ds(x[0]));
+}
+
+// The last step of one query row (row r, query head h): merge the per-wave
+// partials in wave order, XSA, gate, store.  Two layouts with the same
+// arithmetic, so window rows get the bits of decode rows:
+//   NK = 4: the 16 lanes of one wave row, lane c holding dims c + 16k (k < 4)
+//           -- a wave finishes four rows at once and shares every per-row
+//           scalar (exponentials, norms, divisions' set-up) among them;
+//   NK = 1: a whole wave, lane c holding dim c (decode: one row per wave).
+// Contraction is off here: products are rounded before they are summed (the
+// compiler would otherwise fuse a product into the in-lane sum of one layout
+// and not into the cross-lane sum of the other), and the FMAs are explicit.
+// Wave w's partials: m[w * ms], l[w * ms], acc[w * as + d].
+template <int NK, int YBF16>
+__device__ __forceinline__ void finish_query(const AttnP& a, const float* m, const float* l, int ms,
+                                             const float* acc, int as, int r, int h, int c,
+                                             const RowExtras<NK>& e) {
+#pragma clang fp contract(off)
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, m[w * ms]);
+  float Ls = 0.f, y[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) y[k] = 0.f;
+#pragma unroll
+  for (int w = 0; w < ATT_WAVES; ++w) {
+    const float mw = m[w * ms];
+    if (mw == -INFINITY) continue;  // uniform over the row
+    const float f = __expf(mw - M);
+    Ls = __builtin_fmaf(l[w * ms], f, Ls);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) y[k] = __builtin_fmaf(acc[w * as + c + 16 * k], f, y[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < NK; ++k) y[k] = y[k] / Ls;
+  if (a.use_xsa) {  // y -= (y . v^) v^ with v^ = v / max(|v|, 1e-12), v the current token's value
+    float sq[NK], vn[NK], yv[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) sq[k] = e.vv[k] * e.vv[k];
+    const float nrm = fmaxf(sqrtf(row_dims_sum<NK>(sq)), 1e-12f);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      vn[k] = e.vv[k] / nrm;
+      yv[k] = y[k] * vn[k];
+    }
+    const float dot = row_dims_sum<NK>(yv);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) y[k] = __builtin_fmaf(-dot, vn[k], y[k]);
+  }
+  if (a.gate) {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) y[k] *= e.gv;
+  }
+  const int64_t o = ((int64_t)r * a.H + h) * HD + c;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    if (YBF16) ((uint16_t*)a.y)[o + 16 * k] = f32_to_bf16(y[k]);
+    else ((float*)a.y)[o + 16 * k] = y[k];
+  }
+}
+
+// Decode (and the fp32-cache kernel): wave j < G finishes query head j of the
+// kv head, one dim per lane.  v_at(p, d) returns the current token's value entry.
 template <int G, int YBF16, class VAt>
 __device__ __forceinline__ void merge_and_store(const AttnP& a, const MergeLds<G>& sm, int r, int g,
                                                 int p, int wave, int lane, VAt v_at) {
+  static_assert(G <= ATT_WAVES, "one wave per query head of the group");
   if (wave >= G) return;
-  const int j = wave, d = lane;
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, sm.m[w][j]);
-  float Ls = 0.f, Y = 0.f;
-#pragma unroll
-  for (int w = 0; w < ATT_WAVES; ++w) {
-    const float mw = sm.m[w][j];
-    if (mw == -INFINITY) continue;
-    const float f = __expf(mw - M);
-    Ls += sm.l[w][j] * f;
-    Y += sm.acc[w][j][d] * f;
-  }
-  float y = Y / Ls;
-  const int h = g * G + j;
-  if (a.use_xsa) {
-    const float vv = v_at(p, d);
-    const float nrm = sqrtf(wave_sum(vv * vv));
-    const float vn = vv / fmaxf(nrm, 1e-12f);
-    const float dot = wave_sum(y * vn);
-    y = y - dot * vn;
-  }
-  if (a.gate) y *= a.gate[(int64_t)r * a.H + h];
-  const int64_t o = ((int64_t)r * a.H + h) * HD + d;
-  if (YBF16) ((uint16_t*)a.y)[o] = f32_to_bf16(y);
-  else ((float*)a.y)[o] = y;
+  const RowExtras<1> e = row_extras<1>(a, r, g * G + wave, p, lane, v_at);
+  finish_query<1, YBF16>(a, &sm.m[0][wave], &sm.l[0][wave], G, &sm.acc[0][wave][0], G * HD, r,
+                         g * G + wave, lane, e);
 }
 
 __device__ __forceinline__ int clamp_pos(const AttnP& a, int b, int t) {
@@ -165,7 +230,7 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
         if (k0 + 16 * blk + 4 * lg + i >= nkeys) S[blk][i] = -INFINITY;
         mt = fmaxf(mt, S[blk][i]);
       }
-    mt = rows_max(mt);
+    mt = rows_max_ds(mt);
     const float m_new = fmaxf(m_run, mt);
     const float alpha = __expf(m_run - m_new);
     float ps = 0.f;
@@ -176,20 +241,17 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
         S[blk][i] = __expf(S[blk][i] - m_new);
         ps += S[blk][i];
       }
-    l_part = l_part * alpha + ps;
+    l_part = __builtin_fmaf(l_part, alpha, ps);
     m_run = m_new;
-    // acc rows 4*lg + i hold head i % G; this lane's alpha is head col % G's.
-    float al[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (G == 1) al[i] = alpha;
-      else al[i] = __shfl(alpha, (lane & ~(G - 1)) | (i % G), WAVE);
-    }
+    // (P x V)^T = V^T x P^T: acc[nb] row 4*lg + i is dim 16*nb + 4*lg + i,
+    // column col is head col % G -- this lane's own alpha.
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[nb][i] *= al[i];
-    // P x V: k-step s covers keys of blocks 2s and 2s+1 (this lane's own scores)
+      for (int i = 0; i < 4; ++i) acc[nb][i] *= alpha;
+    // k-step s covers keys of blocks 2s and 2s+1 (this lane's own scores); the
+    // V register of a lane is its A operand (dims x keys) as it is the B operand
+    // of P x V, and the P operand likewise
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       float pv[8];
@@ -202,7 +264,7 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
         const bf16x8 vop = __builtin_bit_cast(bf16x8, vr[4 * s + nb]);
 #pragma unroll
         for (int k = 0; k < NP; ++k)
-          acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[k], vop, acc[nb], 0, 0, 0);
+          acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[k], acc[nb], 0, 0, 0);
       }
     }
   };
@@ -227,13 +289,11 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
     }
   }
   // l: this lane's keys only; add the four lane groups (fixed butterfly).
-  l_part = rows_sum(l_part);
-  // acc row h (lane group 0, register h) is head h for h < G: dims 16*nb + col.
-  if (lg == 0) {
+  l_part = rows_sum_ds(l_part);
+  // column h < G is head h: dims 16*nb + 4*lg + i in acc[nb][i]
+  if (col < G) {
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) sm.acc[wave][h][16 * nb + col] = acc[nb][h];
+    for (int nb = 0; nb < 4; ++nb) *(f32x4*)&sm.acc[wave][col][16 * nb + 4 * lg] = acc[nb];
   }
   if (lane < G) {
     sm.m[wave][lane] = m_run;
@@ -256,10 +316,10 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
 // m = -inf), so a window row gives the bits of the decode row.
 // ---------------------------------------------------------------------------
 
-struct WinLds {
+struct alignas(16) WinLds {
   float m[ATT_WAVES][16];
   float l[ATT_WAVES][16];
-  float acc[ATT_WAVES][16][HD];
+  float acc[ATT_WAVES][16][HD + 4];  // rows padded: a wave's 16 query rows on distinct banks
 };
 
 template <int NG, int NP, int YBF16>
@@ -370,16 +430,14 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
           S[blk][i] = __expf(S[blk][i] - mu);
           ps += S[blk][i];
         }
-      l_part[gi] = l_part[gi] * alpha + ps;
+      l_part[gi] = __builtin_fmaf(l_part[gi], alpha, ps);
       m_run[gi] = m_new;
-      // acc row 4*lg + i is query column 4*lg + i: its alpha lives on that lane
-      float al[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lg + i, WAVE);
+      // acc[gi][nb] = (P x V)^T: row 4*lg + i is dim 16*nb + 4*lg + i, column
+      // col is this lane's query
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[gi][nb][i] *= al[i];
+        for (int i = 0; i < 4; ++i) acc[gi][nb][i] *= alpha;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         float pv[8];
@@ -392,13 +450,13 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
           const bf16x8 vop = __builtin_bit_cast(bf16x8, vr[4 * s + nb]);
 #pragma unroll
           for (int k = 0; k < NP; ++k)
-            acc[gi][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[k], vop, acc[gi][nb], 0, 0, 0);
+            acc[gi][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[k], acc[gi][nb], 0, 0, 0);
         }
       }
     }
   };
   // Tiles T = wave, wave + 4, ... in order, one tile in registers at a time:
-  // that keeps NG = 2 at 164 VGPRs, three waves per SIMD, whose interleaving
+  // that keeps NG = 2 at 152 VGPRs, three waves per SIMD, whose interleaving
   // hides the load latency far better than a second register buffer at one
   // wave per SIMD (288 VGPRs; cfg4: 0.93 vs 2.1 ms per slot).
   // Tiles below the diagonal of every query first, without the mask (two
@@ -417,50 +475,30 @@ __device__ __forceinline__ void attn_window_task(const AttnP& a, int b, int h, i
     load_t(kr, vr, T);
     tile(kr, vr, T, std::true_type{});
   }
-  // merge and store, one group of 16 queries at a time (wave w: queries w, w+4, ...)
+  // merge and store, one group of 16 queries at a time; wave w finishes
+  // queries 4w .. 4w+3 (one per wave row), then 4w + 4*ATT_WAVES ...
+  auto v_at = [&](int pp, int d) {
+    return bf16_to_f32(vb[(int64_t)(pp / TILE) * (TILE * HD) + kv_tile_v(pp % TILE, d)]);
+  };
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     const float lsum = rows_sum(l_part[gi]);
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm.acc[wave][4 * lg + i][16 * nb + col] = acc[gi][nb][i];
+    for (int nb = 0; nb < 4; ++nb) *(f32x4*)&sm.acc[wave][col][16 * nb + 4 * lg] = acc[gi][nb];
     if (lane < 16) {
       sm.m[wave][lane] = m_run[gi];
       sm.l[wave][lane] = lsum;
     }
     __syncthreads();
-    for (int q = wave; q < 16; q += ATT_WAVES) {
+    for (int q = 4 * wave + lg; q < 16; q += 4 * ATT_WAVES) {
       const int t = t0 + 16 * gi + q;
-      if (t >= a.W) continue;
-      const int r = b * a.W + t;
-      int p = base + t;
-      p = p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p);
-      const int d = lane;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, sm.m[w][q]);
-      float Ls = 0.f, Y = 0.f;
-#pragma unroll
-      for (int w = 0; w < ATT_WAVES; ++w) {
-        const float mw = sm.m[w][q];
-        if (mw == -INFINITY) continue;
-        const float f = __expf(mw - M);
-        Ls += sm.l[w][q] * f;
-        Y += sm.acc[w][q][d] * f;
+      if (t < a.W) {
+        int p = base + t;
+        p = p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p);
+        const RowExtras<4> rx = row_extras<4>(a, b * a.W + t, h, p, col, v_at);
+        finish_query<4, YBF16>(a, &sm.m[0][q], &sm.l[0][q], 16, &sm.acc[0][q][0], 16 * (HD + 4),
+                               b * a.W + t, h, col, rx);
       }
-      float y = Y / Ls;
-      if (a.use_xsa) {
-        const float vv = bf16_to_f32(vb[(int64_t)(p / TILE) * (TILE * HD) + kv_tile_v(p % TILE, d)]);
-        const float nrm = sqrtf(wave_sum(vv * vv));
-        const float vn = vv / fmaxf(nrm, 1e-12f);
-        const float dot = wave_sum(y * vn);
-        y = y - dot * vn;
-      }
-      if (a.gate) y *= a.gate[(int64_t)r * a.H + h];
-      const int64_t o = ((int64_t)r * a.H + h) * HD + d;
-      if (YBF16) ((uint16_t*)a.y)[o] = f32_to_bf16(y);
-      else ((float*)a.y)[o] = y;
     }
     __syncthreads();
   }

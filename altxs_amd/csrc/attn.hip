@@ -13,7 +13,9 @@
 // bf16 cache (attn_mfma_kernel): both products run on v_mfma_f32_16x16x32_bf16
 // the way the reference's split-prefix kernel uses tl.dot
 // (src/xsa_ttt/split_attn.py:55-152): q padded to 16 MFMA columns (column n
-// holds head n % G), scores = K-tile x q, then P x V with P the exp'd scores.
+// holds head n % G), scores = K-tile x q, then (P x V)^T = V^T x P^T with P the
+// exp'd scores (the output column is the query, so each lane rescales its
+// accumulator by its own query's alpha, with no cross-lane shuffle).
 // The K and V tiles are stored pre-swizzled (kv_tile_index below) so that every
 // lane's MFMA operand is one 16-byte load and a wave's load instruction reads
 // 1 KB of consecutive bytes.  Operand precision:
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
 
 // Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
 // per workgroup; grid = B x H x ceil(W / (16*NG)).  At most 256 VGPRs, so at
-// least two waves share a SIMD (NG <= 2 takes 164: three).
+// least two waves share a SIMD (NG <= 2 takes 152: three).
 template <int NG, int NP, int YBF16>
 __global__ __launch_bounds__(ATT_THREADS, 2) void attn_window_kernel(AttnP a) {
   __shared__ WinLds sm;
