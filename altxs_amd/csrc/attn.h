@@ -27,6 +27,7 @@ struct AttnP {
   int use_xsa;
   void* y;
   int32_t* err;
+  int xcd_rows;  // one-row kernel: rows in tiles of 8, tile t on XCD t % 8
 };
 
 // Per-wave partial results, merged in wave order by the whole workgroup.

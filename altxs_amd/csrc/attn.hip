@@ -41,8 +41,15 @@ namespace {
 template <int G, int NP, int YBF16>
 __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
+  int r = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
+  if (a.xcd_rows) {  // row tile t (8 rows x Hkv heads) on XCD t % 8
+    int t, j;
+    xcd_row_split(blockIdx.x, a.B * a.W / 8, t, j);
+    r = 8 * t + j / a.Hkv;
+    g = j % a.Hkv;
+  }
   // GQA launches have G times fewer workgroups: keep two tiles per wave in flight
-  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : ALTXS_ATT_PF)>(a, blockIdx.x / a.Hkv, blockIdx.x % a.Hkv, sm);
+  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : ALTXS_ATT_PF)>(a, r, g, sm);
 }
 
 // Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
@@ -89,7 +96,13 @@ __device__ __forceinline__ float transpose_reduce(float (&v)[N], int lane) {
 template <int G, int YBF16>
 __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
-  const int r = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
+  int r = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
+  if (a.xcd_rows) {  // row tile (8 rows x Hkv heads) tt on XCD tt % 8
+    int tt, j;
+    xcd_row_split(blockIdx.x, a.B * a.W / 8, tt, j);
+    r = 8 * tt + j / a.Hkv;
+    g = j % a.Hkv;
+  }
   const int b = r / a.W, t = r % a.W;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const int p = clamp_pos(a, b, t);
@@ -226,6 +239,7 @@ hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s) {
   const int group = a.H / a.Hkv;
   const bool ops_bf16 = (a.flags & ALTXS_ATTN_OPS_BF16) != 0;
   const bool rows_only = (a.flags & ALTXS_ATTN_ROWS) != 0;
+  p.xcd_rows = ((a.flags & ALTXS_ATTN_XCD_ROWS) != 0 && (int64_t)a.B * a.W % 64 == 0) ? 1 : 0;
   return a.y_bf16 ? launch_y<1>(p, group, a.kv_bf16 != 0, ops_bf16, rows_only, s)
                   : launch_y<0>(p, group, a.kv_bf16 != 0, ops_bf16, rows_only, s);
 }

@@ -266,13 +266,19 @@ template <int TPW>
 __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __restrict__ logits,
                                                               const float2* __restrict__ stats,
                                                               int V, float* __restrict__ probs,
-                                                              uint32_t* __restrict__ cum) {
+                                                              uint32_t* __restrict__ cum,
+                                                              int xcd_rows) {
   constexpr int NT = CH_WAVES * TPW;  // tiles of the row (V / 64, host check)
   static_assert(NT <= 4 * WAVE, "one wave forms the prefix of the tile totals");
   __shared__ float red[CH_WAVES];
   __shared__ float2 sst[NT];
   __shared__ uint32_t tex[NT];
-  const int64_t row = blockIdx.x;
+  int64_t row = blockIdx.x;
+  if (xcd_rows) {  // row tile rt of 8 rows on XCD rt % 8
+    int rt, j;
+    xcd_row_split((int)blockIdx.x, (int)(gridDim.x / 8), rt, j);
+    row = 8 * rt + j;
+  }
   const int t = threadIdx.x, w = t / WAVE, l = t % WAVE;
   const float* x = logits + row * (int64_t)V;
   float v[TPW];
@@ -360,18 +366,19 @@ bool altxs_cdf_rows_kernel(int64_t rows, int V) {
 }
 
 hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int64_t rows, int V,
-                                  float* probs, uint32_t* cum, hipStream_t s) {
+                                  float* probs, uint32_t* cum, hipStream_t s, bool xcd_rows) {
   if (rows <= 0) return hipSuccess;
   if (V % 64) return hipErrorInvalidValue;
   if (altxs_cdf_rows_kernel(rows, V)) {
     // many rows: one workgroup per row (bit-identical tables, no recount); with
     // stats == NULL it forms the tile statistics itself
     const dim3 grid((unsigned)rows), block(CH_THREADS);
+    const int xr = (xcd_rows && rows % 64 == 0) ? 1 : 0;
     switch (V / (64 * CH_WAVES)) {  // tiles per wave
-      case 4: hipLaunchKernelGGL(cdf_row_kernel<4>, grid, block, 0, s, logits, stats, V, probs, cum); break;
-      case 8: hipLaunchKernelGGL(cdf_row_kernel<8>, grid, block, 0, s, logits, stats, V, probs, cum); break;
-      case 12: hipLaunchKernelGGL(cdf_row_kernel<12>, grid, block, 0, s, logits, stats, V, probs, cum); break;
-      case 16: hipLaunchKernelGGL(cdf_row_kernel<16>, grid, block, 0, s, logits, stats, V, probs, cum); break;
+      case 4: hipLaunchKernelGGL(cdf_row_kernel<4>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
+      case 8: hipLaunchKernelGGL(cdf_row_kernel<8>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
+      case 12: hipLaunchKernelGGL(cdf_row_kernel<12>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
+      case 16: hipLaunchKernelGGL(cdf_row_kernel<16>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

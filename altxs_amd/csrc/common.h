@@ -118,6 +118,21 @@ __device__ __forceinline__ float rows_max_ds(float v) {
   return fmaxf(v, __shfl_xor(v, 32, WAVE));
 }
 
+// ---- row-local XCD placement of decode launches -----------------------------
+// Workgroups are dealt to the 8 XCDs round-robin by linear id, and the count
+// continues across launches, so in a chain of launches whose sizes are all
+// multiples of 8 workgroup id i of every launch lands on XCD (i + c) % 8 for
+// one c.  Decode launches (rows in tiles of 8, ntiles % 8 == 0) number their
+// workgroups so that every piece of row tile t runs with id % 8 == t % 8: a
+// stage then reads the rows the previous stage wrote from its own XCD's L2
+// (a dependent launch that reads another XCD's output measured ~1.3 us slower
+// per edge).  id -> (tile, j), j < per_tile; a bijection.
+__host__ __device__ __forceinline__ void xcd_row_split(int id, int ntiles, int& tile, int& j) {
+  const int q = ntiles / 8, b = id / 8;
+  tile = id % 8 + 8 * (b % q);
+  j = b / q;
+}
+
 // ---- device error word ------------------------------------------------------
 // Kernels never fault on bad runtime values (positions, token ids): they skip
 // the access and OR a code into *err, which the host reads when it syncs.

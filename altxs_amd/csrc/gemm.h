@@ -614,33 +614,44 @@ struct EpiStore {
 template <int BITS, int AM, int NB, int KS, class Pro, class Epi>
 __global__ __launch_bounds__(64 * NB * KS) void gemm_kernel(QT w, int R, int64_t codes_stride,
                                                             int64_t scales_stride, ADirect ad,
-                                                            Pro pro, Epi epi) {
+                                                            Pro pro, Epi epi, int rows8) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int batch = blockIdx.z;
   QT wb = w;
   wb.codes += batch * codes_stride;
   wb.scales += batch * scales_stride;
-  // Workgroups are dealt to the 8 XCDs round-robin by linear id.  When the
-  // column-task count is a multiple of 8, renumber so that every row tile of a
-  // column task lands on the same XCD: its weights then come into that XCD's
-  // L2 once instead of once per row tile.
-  int cx = blockIdx.x, ry = blockIdx.y;
-  if (gridDim.x % 8 == 0) {
-    const int bid = blockIdx.x + gridDim.x * blockIdx.y;
-    const int rest = bid / 8;
-    ry = rest % gridDim.y;
-    cx = (rest / gridDim.y) * 8 + bid % 8;
+  int cx = blockIdx.x, ry = blockIdx.y, m0, rows = R;
+  if (rows8) {
+    // decode launches: 8-row tiles (rows m0 .. m0+7 of a 16-row task; the
+    // rest are bounds-masked like rows past R), tile t on XCD t % 8
+    xcd_row_split(blockIdx.x + gridDim.x * blockIdx.y, gridDim.y, ry, cx);
+    m0 = 8 * ry;
+    rows = R < m0 + 8 ? R : m0 + 8;
+  } else {
+    // Workgroups are dealt to the 8 XCDs round-robin by linear id.  When the
+    // column-task count is a multiple of 8, renumber so that every row tile of
+    // a column task lands on the same XCD: its weights then come into that
+    // XCD's L2 once instead of once per row tile.
+    if (gridDim.x % 8 == 0) {
+      const int bid = blockIdx.x + gridDim.x * blockIdx.y;
+      const int rest = bid / 8;
+      ry = rest % gridDim.y;
+      cx = (rest / gridDim.y) * 8 + bid % 8;
+    }
+    m0 = 16 * ry;
   }
-  gemm_task<BITS, AM, NB, KS>(wb, R, ry * 16, cx, gridDim.x, ad, pro, epi, smem, batch);
+  gemm_task<BITS, AM, NB, KS>(wb, rows, m0, cx, gridDim.x, ad, pro, epi, smem, batch);
 }
 
 // Launch helper: column tiles are spread over `col_wgs` workgroups per row tile
-// (0 = one workgroup per column tile).  Sets the dynamic LDS limit once per
-// instantiation.
+// (0 = one workgroup per column tile).  rows8: decode placement (8-row tiles,
+// tile t on XCD t % 8; R % 64 == 0, batch 1).  Sets the dynamic LDS limit once
+// per instantiation.
 template <int BITS, int AM, int NB, int KS, class Pro, class Epi>
 hipError_t launch_gemm(const QT& w, int R, int batch, int64_t codes_stride, int64_t scales_stride,
                        const ADirect& ad, const Pro& pro, const Epi& epi, int col_wgs,
-                       hipStream_t s) {
+                       hipStream_t s, bool rows8 = false) {
+  if (rows8 && (R % 64 != 0 || batch != 1)) return hipErrorInvalidValue;
   auto kfn = gemm_kernel<BITS, AM, NB, KS, Pro, Epi>;
   const size_t lds = task_lds_bytes<AM, NB, KS, Pro>(w.K);
   static size_t configured = 0;
@@ -652,9 +663,9 @@ hipError_t launch_gemm(const QT& w, int R, int batch, int64_t codes_stride, int6
   }
   const int ntiles = (w.N + 16 * NB - 1) / (16 * NB);
   const int cw = (col_wgs <= 0 || col_wgs > ntiles) ? ntiles : col_wgs;
-  dim3 grid((unsigned)cw, (unsigned)((R + 15) / 16), (unsigned)batch);
+  dim3 grid((unsigned)cw, (unsigned)(rows8 ? R / 8 : (R + 15) / 16), (unsigned)batch);
   hipLaunchKernelGGL(kfn, grid, dim3(TileCfg<NB, KS>::THREADS), lds, s, w, R, codes_stride,
-                     scales_stride, ad, pro, epi);
+                     scales_stride, ad, pro, epi, rows8 ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -662,15 +673,15 @@ hipError_t launch_gemm(const QT& w, int R, int batch, int64_t codes_stride, int6
 template <int AM, int NB, int KS, class Pro, class Epi>
 hipError_t launch_gemm_bits(int bits, const QT& w, int R, int batch, int64_t codes_stride,
                             int64_t scales_stride, const ADirect& ad, const Pro& pro,
-                            const Epi& epi, int col_wgs, hipStream_t s) {
+                            const Epi& epi, int col_wgs, hipStream_t s, bool rows8 = false) {
   switch (bits) {
-    case 2: return launch_gemm<2, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
-    case 3: return launch_gemm<3, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
-    case 4: return launch_gemm<4, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
-    case 6: return launch_gemm<6, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+    case 2: return launch_gemm<2, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
+    case 3: return launch_gemm<3, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
+    case 4: return launch_gemm<4, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
+    case 6: return launch_gemm<6, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
     case 16:
       if constexpr (AM != A_F16)
-        return launch_gemm<16, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s);
+        return launch_gemm<16, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
@@ -685,11 +696,12 @@ __host__ __device__ constexpr int pick_ks(int K, int ks_max) {
 
 template <int AM, class Pro, class Epi>
 hipError_t launch_gemm4(int ks_max, int bits, const QT& w, int R, const ADirect& ad,
-                        const Pro& pro, const Epi& epi, int col_wgs, hipStream_t s) {
+                        const Pro& pro, const Epi& epi, int col_wgs, hipStream_t s,
+                        bool rows8 = false) {
   switch (pick_ks(w.K, ks_max)) {
-    case 4: return launch_gemm_bits<AM, 1, 4>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
-    case 2: return launch_gemm_bits<AM, 2, 2>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
-    default: return launch_gemm_bits<AM, 4, 1>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s);
+    case 4: return launch_gemm_bits<AM, 1, 4>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s, rows8);
+    case 2: return launch_gemm_bits<AM, 2, 2>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s, rows8);
+    default: return launch_gemm_bits<AM, 4, 1>(bits, w, R, 1, 0, 0, ad, pro, epi, col_wgs, s, rows8);
   }
 }
 

@@ -11,8 +11,9 @@ hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, boo
 // Whether altxs_launch_cdf_stats uses one workgroup per row for this shape
 // (it then also accepts stats == NULL and forms the tile statistics itself).
 bool altxs_cdf_rows_kernel(int64_t rows, int V);
+// xcd_rows (row kernel, rows % 64 == 0): row tile t of 8 rows on XCD t % 8.
 hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int64_t rows, int V,
-                                  float* probs, uint32_t* cum, hipStream_t s);
+                                  float* probs, uint32_t* cum, hipStream_t s, bool xcd_rows = false);
 
 struct AltxsAttnArgs;
 hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s);

@@ -151,7 +151,7 @@ struct Tasks {
     p.q = a.w.Q; p.k = kv; p.v = kv + (int64_t)a.Hkv * a.max_len * 64 * 2;
     p.seg_stride = 2ll * a.Hkv * a.max_len * 64; p.pos = a.pos;
     p.gate = (a.flags & ALTXS_F_SPARSE_GATE) ? a.w.GATE : nullptr;
-    p.use_xsa = uni(P.use_xsa); p.y = a.w.Y; p.err = a.err;
+    p.use_xsa = uni(P.use_xsa); p.y = a.w.Y; p.err = a.err; p.xcd_rows = 0;
     constexpr int NP = AM == A_BF16 ? 1 : 3;
     altxs_attn::attn_mfma_task<G, NP, AM == A_BF16 ? 1 : 0, ALTXS_PERSIST_ATT_PF>(
         p, r, g, *(MergeLds<G>*)smem);

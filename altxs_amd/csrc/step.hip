@@ -49,6 +49,21 @@ constexpr int kLmHeadColWgs = 128;
 // cfg3 windows at ctx 2048: W = 16 (1024 rows) 1.43 ms per step against 1.51
 // on the 16-row tasks; W = 8 (512 rows) 1.34 against 1.09.
 constexpr int kBigRows = 1024;
+// Decode launches (W = 1, rows a multiple of 64, at most kXcdRowsMax) place row
+// tile t (8 rows) of every launch of the step on XCD t % 8 (xcd_row_split), so
+// each launch reads the rows the previous one wrote from its own XCD's L2.
+// ALTXS_XCD_ROWS=0 turns it off (same bits either way; for measurement).
+// cfg3 (64 rows): 0.691 against 0.711 ms per step; at 256 rows (cfg5) the
+// 8-row tiles' doubled weight decoding costs more (3.79 against 3.58 ms).
+constexpr int kXcdRowsMax = 64;
+bool xcd_rows_on() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("ALTXS_XCD_ROWS");
+    v = (e && atoi(e) == 0) ? 0 : 1;
+  }
+  return v != 0;
+}
 // Preferred K-splits of the 4-wave GEMM stages (QKV and the LM head use
 // (NB, KS) = (4, 1): one 64-column head tile per task).
 constexpr int kKsO = 2, kKsUp = 2, kKsDown = 4;
@@ -269,6 +284,12 @@ struct StepRun {
   const AltxsStepDesc* d;
   static constexpr int hb16 = AM == A_BF16 ? 1 : 0;
 
+  // row-local XCD placement for this group's launches
+  bool xr(const Group& G) const {
+    const int R = G.nb * d->W;
+    return d->W == 1 && R % 64 == 0 && R <= kXcdRowsMax && xcd_rows_on();
+  }
+
   hipError_t embed(const Group& G, hipStream_t st) const {
     const WS& w = G.w;
     EmbedP p;
@@ -281,6 +302,7 @@ struct StepRun {
     p.R = G.nb * d->W;
     // many rows: four per workgroup (cfg4: 0.68 ms with one-wave workgroups)
     const int rpw = p.R >= 4096 ? 4 : 1;
+    p.xcd_rows = (rpw == 1 && xr(G)) ? 1 : 0;
     hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((p.R + rpw - 1) / rpw)), dim3(64 * rpw), 0, st, p);
     return hipGetLastError();
   }
@@ -325,7 +347,7 @@ struct StepRun {
       return launch_gemm_big<4, 1>(L.qkv.bits, qt_of(L.qkv), R, (const uint16_t*)w.Y, epi, st);
     }
     return launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
-                                      pro, epi, 0, st);
+                                      pro, epi, 0, st, xr(G));
   }
 
   // The large-tile GEMMs apply (bf16 activations, many rows, a tileable shape).
@@ -351,7 +373,7 @@ struct StepRun {
     a.kv_seg_stride = 2ll * d->Hkv * d->max_len * HD; a.pos = G.pos;
     a.gate = (d->flags & ALTXS_F_SPARSE_GATE) ? w.GATE : nullptr;
     a.use_xsa = L.use_xsa; a.y = w.Y; a.err = d->err;
-    a.flags = AM == A_BF16 ? ALTXS_ATTN_OPS_BF16 : 0;
+    a.flags = (AM == A_BF16 ? ALTXS_ATTN_OPS_BF16 : 0) | (xr(G) ? ALTXS_ATTN_XCD_ROWS : 0);
     return a;
   }
 
@@ -381,7 +403,7 @@ struct StepRun {
       if (big(R, L.o))
         e = launch_gemm_big4(kKsO, L.o.bits, qt_of(L.o), R, (const uint16_t*)w.Y, epi, st);
       else
-        e = launch_gemm4<AM>(kKsO, L.o.bits, qt_of(L.o), R, ADirect{w.Y, 0}, ProNone{}, epi, 0, st);
+        e = launch_gemm4<AM>(kKsO, L.o.bits, qt_of(L.o), R, ADirect{w.Y, 0}, ProNone{}, epi, 0, st, xr(G));
       if (e != hipSuccess) return e;
     }
     {  // MLP up + LeakyReLU(0.5)^2
@@ -391,7 +413,8 @@ struct StepRun {
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
         e = launch_gemm_big4(kKsUp, L.up.bits, qt_of(L.up), R, (const uint16_t*)w.Y, epi, st);
       } else {
-        e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0, st);
+        e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0, st,
+                             xr(G));
       }
       if (e != hipSuccess) return e;
     }
@@ -420,7 +443,7 @@ struct StepRun {
         e = launch_gemm_big4(kKsDown, L.down.bits, qt_of(L.down), R, (const uint16_t*)w.HB, epi, st);
       else
         e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
-                             epi, 0, st);
+                             epi, 0, st, xr(G));
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -448,14 +471,14 @@ struct StepRun {
         e = launch_gemm_big<4, 1>(d->emb.bits, qt_of(d->emb), R, (const uint16_t*)w.Y, epi, st);
       } else {
         e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0},
-                                       pro, epi, kLmHeadColWgs, st);
+                                       pro, epi, kLmHeadColWgs, st, xr(G));
       }
       if (e != hipSuccess) return e;
     }
     if (G.probs || G.cum) {
       if (fast_cdf && G.cum) {
         if ((e = altxs_launch_cdf_stats(G.logits, own_stats ? nullptr : w.STATS, R, d->V, G.probs,
-                                        G.cum, st)) != hipSuccess)
+                                        G.cum, st, xr(G))) != hipSuccess)
           return e;
       } else {
         const int fl = (d->flags & ALTXS_F_RENORM) ? ALTXS_CDF_RENORM : 0;

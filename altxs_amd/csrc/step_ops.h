@@ -110,6 +110,7 @@ struct EmbedP {
   const float* mix0;  // resid_mix of slot 0's layer [2, D]
   float* xin0;        // slot 0's x_in = m0*x0 + m1*x0 (sequential, no skip)
   int R;              // rows (B * W)
+  int xcd_rows;       // one row per workgroup, R % 64 == 0: row tile t of 8 on XCD t % 8
 };
 
 constexpr int MAX_RUNS = 4;  // D <= 64 lanes * 4 runs * 8 = 2048
@@ -117,7 +118,13 @@ constexpr int MAX_RUNS = 4;  // D <= 64 lanes * 4 runs * 8 = 2048
 // One wave per row; a workgroup holds blockDim.x / 64 rows (only wave-level
 // reductions, so the launch shape changes no bits).
 __global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
-  const int r = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64, lane = threadIdx.x % 64;
+  int r = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  if (a.xcd_rows) {
+    int rt, j;
+    xcd_row_split((int)blockIdx.x, a.R / 8, rt, j);
+    r = 8 * rt + j;
+  }
   if (r >= a.R) return;
   if (r == 0)
     for (int i = lane; i < a.nsync; i += 64) a.sync[i] = 0;

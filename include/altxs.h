@@ -144,6 +144,11 @@ int32_t altxs_rms_qgemm(const AltxsQTensor *w, const float *x, int64_t rows, flo
                                  decode kernel) instead of the window kernel,
                                  which serves up to 64 rows of a segment per
                                  K/V read; both give the same bits */
+#define ALTXS_ATTN_XCD_ROWS 4 /* one-row kernel, B*W % 64 == 0: rows in tiles
+                                 of 8, tile t's workgroups on XCD t % 8 (the
+                                 placement of the step's decode GEMMs, so each
+                                 reads the rows the previous launch wrote from
+                                 its own XCD's L2); same bits */
 
 /*
  * Decode attention over a KV cache.  For row r = b*W + t the query sits at

@@ -117,6 +117,35 @@ def test_cdf_row_kernel_v16384_benchmark_shape():
     st.check_errors()
 
 
+@pytest.mark.parametrize("act", ["bf16", "fp32"])
+def test_decode_64_segments_equals_8_segments(act):
+    """The benchmark's 64-segment decode launches place row tile t (8 rows) of
+    every kernel on XCD t % 8 (8-row GEMM tiles, remapped attention / embedding
+    / CDF workgroups); 8 segments take the ordinary 16-row placement.  The first
+    8 of 64 segments give the bits of the same 8 decoded alone: logits and
+    tables over 4 committed steps."""
+    from altxs_amd import synth
+    from altxs_amd.model import StepModel
+
+    _log(f"64 vs 8 segments, act={act}")
+    sm, _, _ = _setup("cfg3")
+    toks = synth.zipf_tokens(sm.cfg.vocab_size, (64, 4), seed=31)
+    model = StepModel(sm, act=act)
+    out = {}
+    for B in (64, 8):
+        st = model.make_static_state(MAX_LEN, win=1, batch=B)
+        lg, cm = [], []
+        for t in range(toks.shape[1]):
+            st.token.copy_(torch.from_numpy(toks[:B, t:t + 1].astype(np.int32)))
+            model.step(st, commit=True)
+            lg.append(st.logits.cpu()[:8].clone())
+            cm.append(st.cum.cpu()[:8].clone())
+        st.check_errors()
+        out[B] = (torch.stack(lg), torch.stack(cm))
+    assert torch.equal(out[64][0], out[8][0])
+    assert torch.equal(out[64][1], out[8][1])
+
+
 def _ideal_bits(cum_rows: np.ndarray, syms: np.ndarray) -> float:
     idx = np.arange(len(syms))
     f = cum_rows[idx, syms + 1] - cum_rows[idx, syms]
