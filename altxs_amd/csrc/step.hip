@@ -50,11 +50,14 @@ constexpr int kLmHeadColWgs = 128;
 // on the 16-row tasks; W = 8 (512 rows) 1.34 against 1.09.
 constexpr int kBigRows = 1024;
 // Decode launches (W = 1, rows a multiple of 64, at most kXcdRowsMax) place row
-// tile t (8 rows) of every launch of the step on XCD t % 8 (xcd_row_split), so
-// each launch reads the rows the previous one wrote from its own XCD's L2.
+// tile t (8 rows) on XCD t % 8 (xcd_row_split) in the out-projection, MLP,
+// attention, embedding and CDF launches, so each reads the rows the previous
+// one wrote from its own XCD's L2.  QKV and the LM head keep the column-task
+// placement: their 8-row tiles would decode each weight twice as often, which
+// measured slower than the reads it makes local (cfg3: 0.677 ms per step
+// against 0.687 with them, 0.693 with none).  At 256 rows (cfg5) the doubled
+// weight decoding costs more than it saves (3.79 against 3.58 ms).
 // ALTXS_XCD_ROWS=0 turns it off (same bits either way; for measurement).
-// cfg3 (64 rows): 0.691 against 0.711 ms per step; at 256 rows (cfg5) the
-// 8-row tiles' doubled weight decoding costs more (3.79 against 3.58 ms).
 constexpr int kXcdRowsMax = 64;
 bool xcd_rows_on() {
   static int v = -1;
@@ -347,7 +350,7 @@ struct StepRun {
       return launch_gemm_big<4, 1>(L.qkv.bits, qt_of(L.qkv), R, (const uint16_t*)w.Y, epi, st);
     }
     return launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
-                                      pro, epi, 0, st, xr(G));
+                                      pro, epi, 0, st);
   }
 
   // The large-tile GEMMs apply (bf16 activations, many rows, a tileable shape).
@@ -471,7 +474,7 @@ struct StepRun {
         e = launch_gemm_big<4, 1>(d->emb.bits, qt_of(d->emb), R, (const uint16_t*)w.Y, epi, st);
       } else {
         e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0},
-                                       pro, epi, kLmHeadColWgs, st, xr(G));
+                                       pro, epi, kLmHeadColWgs, st);
       }
       if (e != hipSuccess) return e;
     }
