@@ -30,6 +30,7 @@ F_FINAL_MLP = 1 << 7
 CDF_RENORM = 1
 ATTN_OPS_BF16 = 1
 ATTN_ROWS = 2
+ATTN_XCD_ROWS = 4
 KV_TILE = 64
 STEP_SCRATCH_BYTES = 24 << 20  # ALTXS_STEP_SCRATCH_BYTES
 

@@ -120,7 +120,8 @@ def qgemm_stream(codes: torch.Tensor, scales: torch.Tensor, count: int, N: int, 
 def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor, *,
                 W: int = 1, gate: torch.Tensor | None = None, use_xsa: bool = False,
                 y_bf16: bool = False, ops_bf16: bool = False, tiled: bool = False,
-                err: torch.Tensor | None = None, rows: bool = False) -> torch.Tensor:
+                err: torch.Tensor | None = None, rows: bool = False,
+                xcd_rows: bool = False) -> torch.Tensor:
     """q [B*W, H, 64] fp32; k/v [B, Hkv, max_len, 64] (fp32 or bf16); pos [B] int32.
 
     bf16 k/v are given in natural [key][dim] order and tiled here
@@ -129,6 +130,8 @@ def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Te
     (the reference's tl.dot arithmetic); otherwise fp32-faithful splits.
     ``rows`` runs windows (W > 1) of a bf16 cache one row per workgroup (the
     decode kernel) instead of the window kernel; the bits are the same.
+    ``xcd_rows`` places the one-row kernel's workgroups in 8-row tiles, tile t
+    on XCD t % 8 (B*W a multiple of 64; otherwise ignored); the bits are the same.
     """
     from .codec import tile_kv
 
@@ -150,7 +153,8 @@ def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Te
     a.pos = pos.data_ptr()
     a.gate = gate.data_ptr() if gate is not None else None
     a.use_xsa = int(use_xsa)
-    a.flags = (_lib.ATTN_OPS_BF16 if ops_bf16 else 0) | (_lib.ATTN_ROWS if rows else 0)
+    a.flags = ((_lib.ATTN_OPS_BF16 if ops_bf16 else 0) | (_lib.ATTN_ROWS if rows else 0)
+               | (_lib.ATTN_XCD_ROWS if xcd_rows else 0))
     y = torch.empty(B * W, H * hd, dtype=torch.bfloat16 if y_bf16 else torch.float32,
                     device=q.device)
     a.y = y.data_ptr()

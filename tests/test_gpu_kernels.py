@@ -319,6 +319,26 @@ def test_decode_attention_window_equals_rows():
             assert torch.equal(y1, y4.view(B, 4, -1)[:, t])
 
 
+def test_decode_attention_xcd_row_placement_same_bits():
+    """The row-local XCD placement (8-row tiles, tile t on XCD t % 8) through the
+    public entry gives the bits of the linear placement, for 64 and 128 rows,
+    MHA and GQA; at 24 rows (not a multiple of 64) the flag is ignored."""
+    from altxs_amd import ops
+
+    _log("attn xcd row placement vs linear")
+    L = 512
+    for B, H, Hkv in ((64, 8, 8), (128, 8, 4), (24, 8, 8)):
+        gen = torch.Generator().manual_seed(B + Hkv)
+        k = torch.randn(B, Hkv, L, 64, generator=gen).to(torch.bfloat16).to(DEV)
+        v = torch.randn(B, Hkv, L, 64, generator=gen).to(torch.bfloat16).to(DEV)
+        q = (torch.randn(B, H, 64, generator=gen) * 3).to(DEV)
+        pos = torch.randint(0, L, (B,), generator=gen, dtype=torch.int32).to(DEV)
+        for ob in (False, True):
+            want = ops.decode_attn(q, k, v, pos, use_xsa=True, ops_bf16=ob, y_bf16=True)
+            got = ops.decode_attn(q, k, v, pos, use_xsa=True, ops_bf16=ob, y_bf16=True, xcd_rows=True)
+            assert torch.equal(got, want), (B, Hkv, ob)
+
+
 def test_attention_position_error_flag():
     from altxs_amd import ops
 
