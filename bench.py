@@ -155,7 +155,7 @@ def cpu_baseline(sm, ctx: int, seconds: float, seed: int = 0) -> dict:
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    om = OracleModel(sm.cfg, sm.state_dict(), act="fp32", max_len=ctx)
+    om = OracleModel(sm.cfg, sm.state_dict(), max_len=ctx)
     st = om.new_state(ctx)
     g = torch.Generator().manual_seed(seed)
     for s in range(om.n_slots):
@@ -234,7 +234,7 @@ def window_bench(a) -> int:
 
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)
-        om = OracleModel(cfg, sm.state_dict(), act="fp32", max_len=max_len)
+        om = OracleModel(cfg, sm.state_dict(), max_len=max_len)
         ids = synth.zipf_tokens(cfg.vocab_size, (W,), seed=3)
         t0 = time.perf_counter()
         om.forward_logits(ids)

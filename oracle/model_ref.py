@@ -28,16 +28,9 @@ with F.scaled_dot_product_attention (tests/test_oracle_model.py).
 1238-1271, with ``_softmax_np``, compress.py:64-85); pinned by rows the
 reference's ``StaticACEngine`` wrote (tests/golden/engine_rows.npz).
 
-``act="bf16"`` (parity unpinned: a diagnostic, not a gate -- nothing the
-reference wrote fixes these rounding points, and the GPU's bf16 mode is gated
-on coded bits/symbol against the fp32 path instead) additionally rounds,
-exactly where the GPU's bf16 mode does,
-the GEMM inputs (normed activations, attention output, MLP hidden), the
-K/V entries written to the cache (the cached values are the ones attention
-and XSA read) and the query as the score operand.  The GPU's bf16 mode also
-rounds the unnormalised softmax weights to bf16 for the P x V product (as
-the reference's tl.dot does, split_attn.py:131-141); that rounding depends on
-the kernel's key tiling and is not emulated here.  ``act="fp32"`` is the reference's arithmetic.
+The model computes in fp32 throughout, the reference's arithmetic.  The
+GPU's bf16 mode is not emulated here: its gate is an fp32-anchored bound
+(logits and coded bits/symbol against this fp32 model).
 """
 
 from __future__ import annotations
@@ -109,11 +102,8 @@ class OracleState:
 
 
 class OracleModel:
-    def __init__(self, cfg, sd: dict, *, act: str = "fp32", max_len: int = 2048):
-        if act not in ("fp32", "bf16"):
-            raise ValueError(act)
+    def __init__(self, cfg, sd: dict, *, max_len: int = 2048):
         self.cfg = cfg
-        self.act = act
         self.sd = {k: torch.as_tensor(np.asarray(v), dtype=torch.float32) for k, v in sd.items()}
         self.L = cfg.num_layers
         self.D = cfg.model_dim
@@ -131,10 +121,6 @@ class OracleModel:
         self.lora_scale = float(cfg.lora_alpha) / self.lora_rank if self.lora_rank else 0.0
 
     # ---- helpers ----------------------------------------------------------
-    def _r(self, x: torch.Tensor) -> torch.Tensor:
-        """bf16 rounding point of the GPU's bf16 mode (identity in fp32)."""
-        return x.to(torch.bfloat16).float() if self.act == "bf16" else x
-
     def _bank(self, i: int):
         n, sd = self.L, self.sd
         return (sd["qo_bank"][i], sd["kv_bank"][i], sd["kv_bank"][n + i], sd["qo_bank"][n + i],
@@ -145,8 +131,8 @@ class OracleModel:
 
     def _mlp(self, i: int, n: torch.Tensor) -> torch.Tensor:
         _, _, _, _, up, down = self._bank(i)
-        h = F.leaky_relu(F.linear(self._r(n), up), negative_slope=0.5).square()
-        return F.linear(self._r(h), down)
+        h = F.leaky_relu(F.linear(n, up), negative_slope=0.5).square()
+        return F.linear(h, down)
 
     def _skip(self, j: int, dest: torch.Tensor, skips: list) -> torch.Tensor:
         """_apply_decoder_skip (model.py:1275-1291)."""
@@ -171,7 +157,7 @@ class OracleModel:
 
     def _logits(self, x: torch.Tensor) -> torch.Tensor:
         h = _rms(x)
-        lg = F.linear(self._r(h), self.sd["tok_emb.weight"])
+        lg = F.linear(h, self.sd["tok_emb.weight"])
         if self.cfg.asym_logit_rescale:
             sp, sn = self.sd["softcap_pos"], self.sd["softcap_neg"]
             return torch.where(lg >= 0, sp * torch.tanh(lg / sp), sn * torch.tanh(lg / sn))
@@ -189,14 +175,13 @@ class OracleModel:
         + QK-RMSNorm + RoPE + q_gain (model.py:783-812). n [T, D]."""
         q_w, k_w, v_w, _, _, _ = self._bank(i)
         T = n.shape[0]
-        nr = self._r(n)
-        q = F.linear(nr, q_w)
-        v = F.linear(nr, v_w)
+        q = F.linear(n, q_w)
+        v = F.linear(n, v_w)
         if self.lora_rank and slot >= 0:
-            q = q + self._lora("q", slot, nr)
-            v = v + self._lora("v", slot, nr)
+            q = q + self._lora("q", slot, n)
+            v = v + self._lora("v", slot, n)
         q = q.reshape(T, self.H, self.hd)
-        k = F.linear(nr, k_w).reshape(T, self.Hkv, self.hd)
+        k = F.linear(n, k_w).reshape(T, self.Hkv, self.hd)
         v = v.reshape(T, self.Hkv, self.hd)
         q = _rms(q)
         k = _rms(k)
@@ -220,7 +205,7 @@ class OracleModel:
                                  F.linear(n[:, : self.cfg.gate_window], gw))
             y = y * gate[..., None]
         _, _, _, o_w, _, _ = self._bank(i)
-        return F.linear(self._r(y.reshape(T, self.D)), o_w)
+        return F.linear(y.reshape(T, self.D), o_w)
 
     def _attend(self, q, k_all, v_all, n_vis: torch.Tensor):
         """Row t attends keys [0, n_vis[t]) (model.py:550-585 semantics)."""
@@ -241,8 +226,6 @@ class OracleModel:
         T = n.shape[0]
         pos = torch.arange(st.pos, st.pos + T)
         q, k, v = self._qkv(i, n, pos, slot)
-        k, v = self._r(k), self._r(v)  # cache storage rounding (bf16 mode)
-        q = self._r(q)  # bf16 score operand (split_attn.py:86-93 rounds q to bf16)
         st.k[slot][st.pos:st.pos + T] = k
         st.v[slot][st.pos:st.pos + T] = v
         Lv = st.pos + T
@@ -336,7 +319,6 @@ class OracleModel:
         def attn(i, n):
             q, k, v = self._qkv(i, n, pos, slot_ctr[0])
             slot_ctr[0] += 1
-            k, v = self._r(k), self._r(v)
             y = self._attend(q, k, v, pos + 1)
             return self._post_attn(i, y, v, n)
 

@@ -184,7 +184,7 @@ def test_shipped_codec_end_to_end(tmp_path):
         got.append(st.logits.cpu().numpy().copy())
     st.check_errors()
     got = np.stack(got, 1)
-    om = OracleModel(cfg, sd, act="fp32", max_len=256)
+    om = OracleModel(cfg, sd, max_len=256)
     want = np.stack([om.decode_rows(t).numpy() for t in toks.astype(np.int64)])
     err = np.abs(got - want).max()
     _log(f"max |dlogit| = {err:.3e}")

@@ -6,12 +6,8 @@
   fp32 oracle's (here on cfg1, and on 2048 cfg3 symbols in
   test_gpu_parity.py); a logit gate against fp32 cannot hold for bf16
   activations (rounding the LM-head input alone, as the reference's bf16
-  path does, moves cfg3 logits by > 2e-3: test_oracle_model.py).  The
-  comparison with the oracle's bf16-rounding emulation below is a diagnostic
-  bound, not a gate: fp32 values one ulp apart can round to different bf16
-  neighbours and q_gain/attention amplify such flips (perturbing the
-  emulation's pre-rounding values by 2e-7 relative moves its logits by up to
-  1.7e-2 on tiny / 6e-3 on cfg1);
+  path does, moves cfg3 logits by > 2e-3: test_oracle_model.py); its logits
+  also stay within a stated bound of the fp32 oracle's (below);
 * integer CDFs bit-identical between decode rows (W=1), encode windows (W=4)
   and batches of different sizes, and from run to run;
 * coded bits/symbol within 0.1% of the oracle's coder on the oracle's tables.
@@ -73,13 +69,13 @@ def _tokens(profile):
 _ORACLE: dict = {}
 
 
-def _oracle_rows(profile, act):
+def _oracle_rows(profile):
     from oracle.model_ref import OracleModel
 
-    key = (profile, act)
+    key = profile
     if key not in _ORACLE:
         sm = _synth(profile)
-        om = OracleModel(sm.cfg, sm.state_dict(), act=act, max_len=256)
+        om = OracleModel(sm.cfg, sm.state_dict(), max_len=256)
         _ORACLE[key] = np.stack([om.decode_rows(t).numpy() for t in _tokens(profile)])  # [B, T, V]
     return _ORACLE[key]
 
@@ -110,7 +106,7 @@ def _gpu_decode(profile, act, B=None, W=1, kv=None):
 def test_step_fp32_matches_oracle(profile):
     _log(f"step fp32 {profile}")
     got, _, _, _ = _gpu_decode(profile, "fp32")
-    want = _oracle_rows(profile, "fp32")
+    want = _oracle_rows(profile)
     err = np.abs(got - want).max()
     assert err < LOGIT_TOL, err
     assert err < 2e-4, err  # fp32-faithful path: far inside the tolerance
@@ -119,22 +115,27 @@ def test_step_fp32_matches_oracle(profile):
 def test_step_fp32_act_bf16_kv_meets_tolerance():
     _log("step fp32-act/bf16-kv cfg1")
     got, _, _, _ = _gpu_decode("cfg1", "fp32", kv="bf16")
-    err = np.abs(got - _oracle_rows("cfg1", "fp32")).max()
+    err = np.abs(got - _oracle_rows("cfg1")).max()
     _log(f"max |dlogit| = {err:.3e}")
     assert err < LOGIT_TOL, err
 
 
-@pytest.mark.parametrize("profile,mean_tol,max_tol", [("tiny", 3e-3, 6e-2), ("cfg1", 5e-4, 1e-2),
-                                                      ("cfg1_lora", 5e-4, 1e-2),
-                                                      ("tiny_dense", 3e-3, 6e-2),
-                                                      ("large_dense", 5e-4, 1e-2)])
-def test_step_bf16_matches_oracle_emulation(profile, mean_tol, max_tol):
-    """Diagnostic bound on the bf16 mode (its gate is bits/symbol)."""
+# bf16 mode against the fp32 oracle: measured max |dlogit| tiny 2.8e-2,
+# tiny_dense 2.7e-2 (std 0.08 weights, gain-amplified), cfg1 2.7e-3,
+# cfg1_lora 3.0e-3, large_dense 3.1e-3 (BASELINE weight scale); means 3.7e-3,
+# 3.5e-3 and 4.5e-4, 4.5e-4, 6.8e-4.
+@pytest.mark.parametrize("profile,mean_tol,max_tol", [("tiny", 1e-2, 6e-2), ("cfg1", 1e-3, 1e-2),
+                                                      ("cfg1_lora", 1e-3, 1e-2),
+                                                      ("tiny_dense", 1e-2, 6e-2),
+                                                      ("large_dense", 1e-3, 1e-2)])
+def test_step_bf16_within_bound_of_fp32_oracle(profile, mean_tol, max_tol):
+    """The bf16 mode (bf16 GEMM inputs, K/V cache and MFMA operands) stays
+    within a stated bound of the fp32 oracle's logits; its full gate adds coded
+    bits/symbol within 0.1% of the fp32 oracle's (test_gpu_parity.py)."""
     _log(f"step bf16 {profile}")
     got, _, _, _ = _gpu_decode(profile, "bf16")
-    d = np.abs(got - _oracle_rows(profile, "bf16"))
-    _log(f"bf16 vs emulation: max {d.max():.3e} mean {d.mean():.3e}; vs fp32 max "
-         f"{np.abs(got - _oracle_rows(profile, 'fp32')).max():.3e}")
+    d = np.abs(got - _oracle_rows(profile))
+    _log(f"bf16 vs fp32 oracle: max {d.max():.3e} mean {d.mean():.3e}")
     assert d.mean() < mean_tol and d.max() < max_tol, (d.mean(), d.max())
 
 
@@ -307,7 +308,7 @@ def test_bits_per_symbol_within_tenth_percent():
     _log("bits/symbol cfg1")
     toks = _tokens(profile)
     _, cm, _, _ = _gpu_decode(profile, "bf16")
-    want = _oracle_rows(profile, "fp32")
+    want = _oracle_rows(profile)
     V = want.shape[-1]
     # symbol i is coded with the row that predicts it (row i-1); row 0 is uniform
     uni = coder.scale_cum(np.full((1, V), 1.0 / V, np.float32))[0]
