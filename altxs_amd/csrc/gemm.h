@@ -935,7 +935,10 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
 // once per column tile.  The weights of the next (column tile, k-block) are
 // loaded while the current one computes, across tile boundaries.  The
 // epilogue runs one 16-row strip at a time through a small LDS strip (the A
-// band must stay), which keeps two workgroups per CU.
+// band must stay), which keeps two workgroups per CU.  Stages with a prologue
+// (Pro = ProNorm: QKV, MLP up, LM head) normalise the band's rows themselves
+// with the 16-row tasks' stage() instead of reading rows a separate launch
+// normalised.
 //
 // The MFMA sequence of every 16x16 output block is gemm_big_kernel's (and so
 // gemm_task's): same k-steps in the same order, acc += scale * t per 64-wide
@@ -950,10 +953,10 @@ __host__ __device__ constexpr size_t band_lds_bytes() {
   return (size_t)BIG_M * BAND_AST * 2 + (size_t)(BIG_N / Cfg::NCOL) * 16 * Cfg::CS * 4;
 }
 
-template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
+template <int BITS, int NB, int KS, class Epi, int AM = A_BF16, class Pro = ProNone>
 __global__ __launch_bounds__(256, 2) void gemm_band_kernel(QT w, int R, const uint16_t* __restrict__ A,
                                                            Epi epi, int64_t codes_stride,
-                                                           int64_t scales_stride) {
+                                                           int64_t scales_stride, Pro pro) {
   static_assert(AM == A_BF16 || AM == A_F16, "16-bit A rows");
   using Cfg = TileCfg<NB, KS>;
   static_assert(Cfg::THREADS == 256, "the epilogues run on four waves");
@@ -976,26 +979,7 @@ __global__ __launch_bounds__(256, 2) void gemm_band_kernel(QT w, int R, const ui
   }
   const int m0 = ry * BIG_M, NT = w.N / BIG_N, GX = gridDim.x;
   auto nblk = [&](int ct) { return ct * (BIG_N / 16) + 2 * wave; };  // this wave's first weight block
-
-  // the band: row r of the tile at As + r * BAND_AST, lane l bringing k = 8l .. 8l+7
-#pragma unroll 4
-  for (int i = 0; i < BIG_M / 4; ++i) {
-    const int r = wave * (BIG_M / 4) + i;
-    if (m0 + r < R)
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(A + (int64_t)(m0 + r) * BAND_K + lane * 8),
-          (__attribute__((address_space(3))) void*)(As + r * BAND_AST), 16, 0, 0);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  using BOp = std::conditional_t<AM == A_F16, f16x8, bf16x8>;
-  auto mfma = [](u32x4 a, BOp b, f32x4 c) {
-    if constexpr (AM == A_F16)
-      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
-    else
-      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
-  };
+  // the first column tile's weights fly while the band arrives
   using WBlk = Blk<BITS, A_BF16, false>;
   WBlk wt[KB][2];  // a column tile's weights, both k-blocks
   auto load_tile_w = [&](WBlk(&d)[KB][2], int ct) {
@@ -1006,6 +990,44 @@ __global__ __launch_bounds__(256, 2) void gemm_band_kernel(QT w, int R, const ui
     }
   };
   load_tile_w(wt, cx);
+
+  if constexpr (Pro::kStage) {
+    // the stage's prologue in place of a separate row-normalisation launch:
+    // stage() over the band's four 16-row strips (strip i at As + 16 i
+    // BAND_AST, BAND_AST being stage()'s row stride for K = 512), so the band
+    // holds the rows norm_rows_kernel would have written; side outputs
+    // (sparse-gate logits) from the first column group only.  The first
+    // column tile's weights are already in flight.  (Two strips' loads issued
+    // before their arithmetic measured no faster; with the early weight loads
+    // they spill.)
+    static_assert(Pro::kScratch == 0, "no prologue scratch in the band's LDS");
+    static_assert(BAND_AST == lds_stride(BAND_K, A_BF16), "stage() row stride");
+#pragma unroll
+    for (int i = 0; i < BIG_M / 16; ++i)
+      pro.template stage<AM, 256>(As + (size_t)i * 16 * BAND_AST, nullptr, m0 + 16 * i, R, BAND_K, batch,
+                                  cx == 0);
+    __syncthreads();
+  } else {
+    // the band: row r of the tile at As + r * BAND_AST, lane l bringing k = 8l .. 8l+7
+#pragma unroll 4
+    for (int i = 0; i < BIG_M / 4; ++i) {
+      const int r = wave * (BIG_M / 4) + i;
+      if (m0 + r < R)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(A + (int64_t)(m0 + r) * BAND_K + lane * 8),
+            (__attribute__((address_space(3))) void*)(As + r * BAND_AST), 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  using BOp = std::conditional_t<AM == A_F16, f16x8, bf16x8>;
+  auto mfma = [](u32x4 a, BOp b, f32x4 c) {
+    if constexpr (AM == A_F16)
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+  };
   for (int ct = cx; ct < NT; ct += GX) {
     const int n0 = ct * BIG_N;
     f32x4 acc[MB][2], tot[MB][2];
@@ -1118,10 +1140,11 @@ inline int band_col_groups(int R, int N, int batch) {
   return want < 1 ? 1 : (want > nt ? nt : want);
 }
 
-template <int BITS, int NB, int KS, class Epi, int AM = A_BF16>
+template <int BITS, int NB, int KS, class Epi, int AM = A_BF16, class Pro = ProNone>
 hipError_t launch_gemm_band_t(const QT& w, int R, const uint16_t* A, const Epi& epi, hipStream_t s,
-                              int batch, int64_t codes_stride, int64_t scales_stride) {
-  auto kfn = gemm_band_kernel<BITS, NB, KS, Epi, AM>;
+                              int batch, int64_t codes_stride, int64_t scales_stride,
+                              const Pro& pro = Pro{}) {
+  auto kfn = gemm_band_kernel<BITS, NB, KS, Epi, AM, Pro>;
   constexpr size_t lds = band_lds_bytes<NB, KS>();
   static bool configured = false;
   if (!configured) {
@@ -1131,7 +1154,7 @@ hipError_t launch_gemm_band_t(const QT& w, int R, const uint16_t* A, const Epi& 
     configured = true;
   }
   dim3 grid((unsigned)band_col_groups(R, w.N, batch), (unsigned)((R + BIG_M - 1) / BIG_M), (unsigned)batch);
-  hipLaunchKernelGGL(kfn, grid, dim3(256), lds, s, w, R, A, epi, codes_stride, scales_stride);
+  hipLaunchKernelGGL(kfn, grid, dim3(256), lds, s, w, R, A, epi, codes_stride, scales_stride, pro);
   return hipGetLastError();
 }
 
@@ -1182,6 +1205,33 @@ hipError_t launch_gemm_big4(int ks_max, int bits, const QT& w, int R, const uint
     case 4: return launch_gemm_big<1, 4>(bits, w, R, A, epi, s);
     case 2: return launch_gemm_big<2, 2>(bits, w, R, A, epi, s);
     default: return launch_gemm_big<4, 1>(bits, w, R, A, epi, s);
+  }
+}
+
+// K = 512 stages with a prologue (QKV, MLP up, LM head): the row-band kernel
+// runs the prologue itself (same rows, same bits as norm_rows_kernel followed
+// by the band kernel on them).  (NB, KS) as launch_gemm_big.
+inline bool band_norm_fits(const QT& w) { return big_gemm_fits(w) && w.K == BAND_K; }
+template <int NB, int KS, class Pro, class Epi>
+hipError_t launch_gemm_band_norm(int bits, const QT& w, int R, const Pro& pro, const Epi& epi,
+                                 hipStream_t s) {
+  static_assert((BAND_K / 256) % KS == 0, "K-slices of the band");
+  if (w.K != BAND_K) return hipErrorInvalidValue;
+  switch (bits) {
+    case 2: return launch_gemm_band_t<2, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
+    case 3: return launch_gemm_band_t<3, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
+    case 4: return launch_gemm_band_t<4, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
+    case 6: return launch_gemm_band_t<6, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
+    default: return hipErrorInvalidValue;
+  }
+}
+template <class Pro, class Epi>
+hipError_t launch_gemm_band_norm4(int ks_max, int bits, const QT& w, int R, const Pro& pro, const Epi& epi,
+                                  hipStream_t s) {
+  switch (pick_ks(w.K, ks_max)) {
+    case 2: return launch_gemm_band_norm<2, 2>(bits, w, R, pro, epi, s);
+    case 1: return launch_gemm_band_norm<4, 1>(bits, w, R, pro, epi, s);
+    default: return hipErrorInvalidValue;  // K = 512 allows at most two K-slices
   }
 }
 

@@ -344,7 +344,10 @@ struct StepRun {
     ProNorm pro{};
     EpiQKV epi{};
     qkv_parts(G, s, pro, epi);
-    if (big(R, L.qkv) && !S.lora_q_a) {  // normalised rows in Y (free until the attention)
+    if (big(R, L.qkv) && !S.lora_q_a) {
+      const QT q = qt_of(L.qkv);
+      if (band_norm_fits(q)) return launch_gemm_band_norm<4, 1>(L.qkv.bits, q, R, pro, epi, st);
+      // normalised rows in Y (free until the attention)
       hipError_t e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st);
       if (e != hipSuccess) return e;
       return launch_gemm_big<4, 1>(L.qkv.bits, qt_of(L.qkv), R, (const uint16_t*)w.Y, epi, st);
@@ -412,7 +415,9 @@ struct StepRun {
     {  // MLP up + LeakyReLU(0.5)^2
       ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       EpiUp epi{w.HB, d->F, hb16};
-      if (big(R, L.up)) {  // normalised rows in Y (the out-projection has read it)
+      if (big(R, L.up) && band_norm_fits(qt_of(L.up))) {
+        e = launch_gemm_band_norm4(kKsUp, L.up.bits, qt_of(L.up), R, pro, epi, st);
+      } else if (big(R, L.up)) {  // normalised rows in Y (the out-projection has read it)
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
         e = launch_gemm_big4(kKsUp, L.up.bits, qt_of(L.up), R, (const uint16_t*)w.Y, epi, st);
       } else {
@@ -469,7 +474,9 @@ struct StepRun {
       own_stats = big(R, d->emb) && fast_cdf && G.cum && altxs_cdf_rows_kernel(R, d->V);
       EpiLogits epi{G.logits, (fast_cdf && !own_stats) ? w.STATS : nullptr, d->V,
                     (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap, d->softcap_pn};
-      if (big(R, d->emb)) {
+      if (big(R, d->emb) && band_norm_fits(qt_of(d->emb))) {
+        e = launch_gemm_band_norm<4, 1>(d->emb.bits, qt_of(d->emb), R, pro, epi, st);
+      } else if (big(R, d->emb)) {
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
         e = launch_gemm_big<4, 1>(d->emb.bits, qt_of(d->emb), R, (const uint16_t*)w.Y, epi, st);
       } else {
