@@ -135,9 +135,19 @@ __device__ __forceinline__ void merge_and_store(const AttnP& a, const MergeLds<G
   finish_query<1, YBF16>(a, &sm.m[0][wave], &sm.l[0][wave], G, &sm.acc[0][wave][0], G * HD, r,
                          g * G + wave, lane, e);
 }
+// The same with the extras read beforehand (the bf16 kernel loads them at its
+// start, so the finish step waits on no memory).
+template <int G, int YBF16>
+__device__ __forceinline__ void merge_and_store(const AttnP& a, const MergeLds<G>& sm, int r, int g,
+                                                int wave, int lane, const RowExtras<1>& e) {
+  static_assert(G <= ATT_WAVES, "one wave per query head of the group");
+  if (wave >= G) return;
+  finish_query<1, YBF16>(a, &sm.m[0][wave], &sm.l[0][wave], G, &sm.acc[0][wave][0], G * HD, r,
+                         g * G + wave, lane, e);
+}
 
-__device__ __forceinline__ int clamp_pos(const AttnP& a, int b, int t) {
-  int p = a.pos[b] + t;
+__device__ __forceinline__ int clamp_pos(const AttnP& a, int b, int t, int pos_b) {
+  int p = pos_b + t;
   if (p < 0 || p >= a.max_len) {
     if (threadIdx.x == 0) flag_err(a.err, ALTXS_EDEV_POS);
     p = p < 0 ? 0 : a.max_len - 1;
@@ -174,32 +184,8 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   const int b = r / a.W, t = r % a.W;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const int lg = lane >> 4, col = lane & 15;
-  const int p = clamp_pos(a, b, t);
-  const int nkeys = p + 1;
-  const int ntiles = (nkeys + TILE - 1) / TILE;
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
-
-  // q operand (B of the score MFMA): column col holds head col % G; k-step ks
-  // covers dims 32*ks + 8*lg + [0, 8).  Scaled by 1/sqrt(64) (exact).
-  bf16x8 qop[2][NP];
-  {
-    const float* qh = a.q + ((int64_t)r * a.H + g * G + (col % G)) * HD;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const f32x4 lo = *(const f32x4*)(qh + 32 * ks + 8 * lg);
-      const f32x4 hi = *(const f32x4*)(qh + 32 * ks + 8 * lg + 4);
-      float x[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { x[i] = lo[i] * 0.125f; x[4 + i] = hi[i] * 0.125f; }
-      split_parts<NP>(x, qop[ks]);
-    }
-  }
-  float m_run = -INFINITY, l_part = 0.f;
-  f32x4 acc[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   auto load = [&](u32x4 (&kr)[8], u32x4 (&vr)[8], int T) {
     const u32x4* kt = (const u32x4*)(kb + (int64_t)T * (TILE * HD)) + lane;
     const u32x4* vt = (const u32x4*)(vb + (int64_t)T * (TILE * HD)) + lane;
@@ -208,6 +194,51 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
 #pragma unroll
     for (int i = 0; i < 8; ++i) vr[i] = __builtin_nontemporal_load(vt + 64 * i);
   };
+  // Every workgroup of a decode launch starts (and ends) at the same time, so
+  // a memory round trip after the last tile costs the whole launch: the
+  // finish step's extras (the current value for XSA, the gate) are read here,
+  // after the position and the q row, and kept raw until the finish step (the
+  // load counter retires in order, so a use right after their loads would wait
+  // for everything older).  Same values, same arithmetic; cfg3 0.675 -> 0.670
+  // ms.  (A variant that also issued each wave's first tile before the q row
+  // gave wrong rows whenever a row had more than two keys -- cause not found
+  // -- and is not in the build.)
+  const int p_raw = a.pos[b];
+  f32x4 qraw[2][2];
+  {
+    const float* qh = a.q + ((int64_t)r * a.H + g * G + (col % G)) * HD;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      qraw[ks][0] = *(const f32x4*)(qh + 32 * ks + 8 * lg);
+      qraw[ks][1] = *(const f32x4*)(qh + 32 * ks + 8 * lg + 4);
+    }
+  }
+  const int p = clamp_pos(a, b, t, p_raw);
+  const int nkeys = p + 1;
+  const int ntiles = (nkeys + TILE - 1) / TILE;
+  // unconditional loads (a load on one path only would leave the compiler
+  // unsure how many are in flight, and it would then wait for all of them);
+  // waves past G read a valid word they do not use
+  const int hx = g * G + (wave < G ? wave : G - 1);
+  const uint16_t v_raw = vb[(int64_t)(p / TILE) * (TILE * HD) + kv_tile_v(p % TILE, lane)];
+  const float g_raw = *(a.gate ? a.gate + (int64_t)r * a.H + hx : (const float*)a.pos);  // any readable word
+
+  // q operand (B of the score MFMA): column col holds head col % G; k-step ks
+  // covers dims 32*ks + 8*lg + [0, 8).  Scaled by 1/sqrt(64) (exact).
+  bf16x8 qop[2][NP];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const f32x4 lo = qraw[ks][0], hi = qraw[ks][1];
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { x[i] = lo[i] * 0.125f; x[4 + i] = hi[i] * 0.125f; }
+    split_parts<NP>(x, qop[ks]);
+  }
+  float m_run = -INFINITY, l_part = 0.f;
+  f32x4 acc[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
   auto process = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8], int T) {
     // scores: S[blk] row 4*lg + i = key 16*blk + 4*lg + i, column col
     f32x4 S[4];
@@ -301,9 +332,10 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
     sm.l[wave][lane] = l_part;
   }
   __syncthreads();
-  merge_and_store<G, YBF16>(a, sm, r, g, p, wave, lane, [&](int pp, int d) {
-    return bf16_to_f32(vb[(int64_t)(pp / TILE) * (TILE * HD) + kv_tile_v(pp % TILE, d)]);
-  });
+  RowExtras<1> ex;
+  ex.vv[0] = a.use_xsa ? bf16_to_f32(v_raw) : 0.f;
+  ex.gv = a.gate ? g_raw : 1.f;
+  merge_and_store<G, YBF16>(a, sm, r, g, wave, lane, ex);
 }
 
 // ---------------------------------------------------------------------------

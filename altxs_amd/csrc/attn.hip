@@ -105,7 +105,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
   }
   const int b = r / a.W, t = r % a.W;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  const int p = clamp_pos(a, b, t);
+  const int p = clamp_pos(a, b, t, a.pos[b]);
   const int nkeys = p + 1;
   const int ntiles = (nkeys + TILE - 1) / TILE;
   const float* kb = (const float*)a.k + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
