@@ -12,6 +12,8 @@ segments; ``value`` = 64 / step time.  The KV cache is filled with N(0, 1)
 bf16 values (the scale of QK-RMS-normalised keys) and the step runs at a
 fixed position, overwriting the same cache row, so each step moves the same
 bytes.  Weights are seeded N(0, 0.02^2) then quantised; tokens are Zipf(1.1).
+The timed K steps run as K/S replays of a HIP graph of S consecutive steps
+(``--graph-steps``, default 10; ``config.graph_steps``).
 
 The line also carries:
 * ``roofline``: the decode-attention kernel (the dominant one), algorithmic
@@ -461,6 +463,9 @@ def main() -> int:
     ap.add_argument("--act", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--kv", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
+    ap.add_argument("--graph-steps", type=int, default=10, metavar="S",
+                    help="decode steps captured per HIP graph (the timed K steps replay K/S graphs; "
+                         "S must divide K, else 1)")
     ap.add_argument("--streams", type=int, default=1, choices=[1, 2],
                     help="2: two segment groups on two streams, the second chain started half a slot later")
     ap.add_argument("--window", type=int, default=1, metavar="W",
@@ -536,12 +541,18 @@ def main() -> int:
     st.check_errors()
     log(f"warmup done ({a.warmup} steps)")
 
+    # S consecutive steps per graph: the steps are device-resident end to end
+    # (the engine's decode loop feeds each decoded symbol to the next step on
+    # the device), so a graph of S steps is a launch strategy a caller can use;
+    # it removes S - 1 of every S gaps between graph launches (~8 us each here).
+    gs = a.graph_steps if a.graph_steps >= 1 and a.steps % a.graph_steps == 0 else 1
     graph = None
     if not a.no_graph:
         try:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                model.step(st)
+                for _ in range(gs):
+                    model.step(st)
             torch.cuda.synchronize()
             graph.replay()
             torch.cuda.synchronize()
@@ -553,16 +564,18 @@ def main() -> int:
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
-    for _ in range(a.steps):
-        if graph is not None:
+    if graph is not None:
+        for _ in range(a.steps // gs):
             graph.replay()
-        else:
+    else:
+        for _ in range(a.steps):
             model.step(st)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / a.steps
     st.check_errors()
-    log(f"timed {a.steps} steps ({'graph' if graph is not None else 'eager'}): {ms:.3f} ms/step")
+    log(f"timed {a.steps} steps ({f'graphs of {gs} steps' if graph is not None else 'eager'}): "
+        f"{ms:.3f} ms/step")
 
     # ---- dominant kernel: HIP events around every attention launch ----------
     # The K instrumented steps are captured into one graph (distinct events per
@@ -649,6 +662,7 @@ def main() -> int:
                             f"{sm.bits_summary()['bpw']:.3f} bpw group-64 weights, ")
                          + f"{a.act} activations, {a.kv} KV"),
             "segments": B, "ctx": ctx, "timing": "hip-graph" if graph is not None else "eager",
+            "graph_steps": gs if graph is not None else 0,
             "streams": groups, "persistent": bool(a.persistent),
             "eager_ms_per_step": round(eager_ms, 4), "kernel_event_timing": event_timing,
         },
