@@ -200,9 +200,11 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   // after the position and the q row, and kept raw until the finish step (the
   // load counter retires in order, so a use right after their loads would wait
   // for everything older).  Same values, same arithmetic; cfg3 0.675 -> 0.670
-  // ms.  (A variant that also issued each wave's first tile before the q row
-  // gave wrong rows whenever a row had more than two keys -- cause not found
-  // -- and is not in the build.)
+  // ms.  (Also issuing each wave's first tile before the q row: with the tile
+  // buffer carried around the tile loop the rows came out wrong whenever a
+  // row had more than two keys, cause not found; with the first tile peeled
+  // into a buffer of its own the rows are right but the step is slower,
+  // 0.693 against 0.668 ms.  Neither is in the build.)
   const int p_raw = a.pos[b];
   f32x4 qraw[2][2];
   {
