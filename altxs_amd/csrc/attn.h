@@ -12,6 +12,8 @@
 namespace altxs_attn {
 
 constexpr int ATT_WAVES = ALTXS_ATT_WAVES;
+// The gate multiplier of launches without the sparse gate (read like a gate entry).
+static __device__ const float kNoGate = 1.f;
 constexpr int ATT_THREADS = ATT_WAVES * WAVE;
 constexpr int TILE = ALTXS_KV_TILE;
 constexpr int HD = 64;
@@ -223,7 +225,7 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   // waves past G read a valid word they do not use
   const int hx = g * G + (wave < G ? wave : G - 1);
   const uint16_t v_raw = vb[(int64_t)(p / TILE) * (TILE * HD) + kv_tile_v(p % TILE, lane)];
-  const float g_raw = *(a.gate ? a.gate + (int64_t)r * a.H + hx : (const float*)a.pos);  // any readable word
+  const float g_raw = *(a.gate ? a.gate + (int64_t)r * a.H + hx : &kNoGate);
 
   // q operand (B of the score MFMA): column col holds head col % G; k-step ks
   // covers dims 32*ks + 8*lg + [0, 8).  Scaled by 1/sqrt(64) (exact).
@@ -336,7 +338,7 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   __syncthreads();
   RowExtras<1> ex;
   ex.vv[0] = a.use_xsa ? bf16_to_f32(v_raw) : 0.f;
-  ex.gv = a.gate ? g_raw : 1.f;
+  ex.gv = g_raw;
   merge_and_store<G, YBF16>(a, sm, r, g, wave, lane, ex);
 }
 
