@@ -129,6 +129,32 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
   if (r == 0)
     for (int i = lane; i < a.nsync; i += 64) a.sync[i] = 0;
   const int b = r / a.W, t = r % a.W;
+  const int nruns = a.D / 8;
+  // Operands that do not depend on the token (resid_mix rows, smear weights
+  // and lambda, the carried raw row) are loaded before the token, so they do
+  // not add a memory round trip after the row's norm.
+  f32x4 mx[MAX_RUNS][2][2];
+  float sw[MAX_RUNS][8], prev[MAX_RUNS][8];
+#pragma unroll
+  for (int j = 0; j < MAX_RUNS; ++j) {
+    const int run = lane + 64 * j;
+    if (run >= nruns) continue;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      mx[j][0][h] = *((const f32x4*)(a.mix0 + 8 * run) + h);
+      mx[j][1][h] = *((const f32x4*)(a.mix0 + a.D + 8 * run) + h);
+    }
+    if (a.smear) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sw[j][i] = 8 * run + i < a.gw ? a.smear_w[8 * run + i] : 0.f;
+      if (t == 0) {
+        const float* pr = a.prev_raw + (int64_t)b * a.D + 8 * run;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) prev[j][i] = pr[i];
+      }
+    }
+  }
+  const float lam = a.smear ? a.smear_lambda[0] : 0.f;
   auto tok_at = [&](int tt) {
     int tk = a.tokens[(int64_t)b * a.W + tt];
     if (tk < 0 || tk >= a.V) {
@@ -138,8 +164,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
     return tk;
   };
   const int tok = tok_at(t);
-  const int nruns = a.D / 8;
-  float raw[MAX_RUNS][8], prev[MAX_RUNS][8];
+  float raw[MAX_RUNS][8];
 #pragma unroll
   for (int j = 0; j < MAX_RUNS; ++j) {
     const int run = lane + 64 * j;
@@ -152,13 +177,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
     for (int j = 0; j < MAX_RUNS; ++j) {
       const int run = lane + 64 * j;
       if (run >= nruns) continue;
-      if (ptok >= 0) {
-        dequant_run_bits(a.bits, a.emb, ptok, run, prev[j]);
-      } else {
-        const float* pr = a.prev_raw + (int64_t)b * a.D + 8 * run;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) prev[j][i] = pr[i];
-      }
+      if (ptok >= 0) dequant_run_bits(a.bits, a.emb, ptok, run, prev[j]);
     }
     // g = lambda * sigmoid(raw[:gw] . w_smear)
     float part = 0.f;
@@ -168,11 +187,11 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int k = 8 * run + i;
-        if (run < nruns && k < a.gw) part += raw[j][i] * a.smear_w[k];
+        if (run < nruns && k < a.gw) part += raw[j][i] * sw[j][i];
       }
     }
     const float gsum = wave_sum(part);
-    const float g = a.smear_lambda[0] * sigmoidf(gsum);
+    const float g = lam * sigmoidf(gsum);
 #pragma unroll
     for (int j = 0; j < MAX_RUNS; ++j)
 #pragma unroll
@@ -196,13 +215,11 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedP a) {
     const int run = lane + 64 * j;
     if (run >= nruns) continue;
     // 8 consecutive floats per lane (32-byte aligned: D % 8 == 0): vector accesses
-    const f32x4* m0 = (const f32x4*)(a.mix0 + 8 * run);
-    const f32x4* m1 = (const f32x4*)(a.mix0 + a.D + 8 * run);
     f32x4* xo = (f32x4*)(a.x0 + (int64_t)r * a.D + 8 * run);
     f32x4* xi = (f32x4*)(a.xin0 + (int64_t)r * a.D + 8 * run);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const f32x4 ma = m0[h], mb = m1[h];
+      const f32x4 ma = mx[j][0][h], mb = mx[j][1][h];
       f32x4 vo, vi;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
