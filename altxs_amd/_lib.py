@@ -12,7 +12,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libaltxs_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MAX_LAYERS = 32
 MAX_SLOTS = 64
@@ -32,6 +32,7 @@ ATTN_OPS_BF16 = 1
 ATTN_ROWS = 2
 ATTN_XCD_ROWS = 4
 KV_TILE = 64
+KV_F32, KV_BF16, KV_BF16_NATURAL = 0, 1, 2  # AltxsStepDesc.kv_bf16 / AltxsAttnArgs.kv_bf16
 STEP_SCRATCH_BYTES = 24 << 20  # ALTXS_STEP_SCRATCH_BYTES
 
 SLOT_SEQ, SLOT_PAR = 0, 1
@@ -40,6 +41,7 @@ EXPORTS = (
     "altxs_abi_version",
     "altxs_last_error",
     "altxs_scale_cum",
+    "altxs_scale_cum_f64",
     "altxs_softmax_cdf",
     "altxs_dequant",
     "altxs_qgemm",
@@ -79,7 +81,8 @@ class AttnArgs(ctypes.Structure):
                 ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
                 ("kv_seg_stride", ctypes.c_int64), ("pos", ctypes.c_void_p),
                 ("gate", ctypes.c_void_p), ("use_xsa", ctypes.c_int32),
-                ("flags", ctypes.c_int32), ("y", ctypes.c_void_p), ("err", ctypes.c_void_p)]
+                ("flags", ctypes.c_int32), ("kv_tail_end", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("y", ctypes.c_void_p), ("err", ctypes.c_void_p)]
 
 
 class Layer(ctypes.Structure):
@@ -109,7 +112,7 @@ class StepDesc(ctypes.Structure):
                 ("max_len", ctypes.c_int32), ("gate_window", ctypes.c_int32),
                 ("rope_dims", ctypes.c_int32), ("lora_rank", ctypes.c_int32),
                 ("act_bf16", ctypes.c_int32), ("kv_bf16", ctypes.c_int32),
-                ("flags", ctypes.c_int32),
+                ("kv_tail_end", ctypes.c_int32), ("flags", ctypes.c_int32),
                 ("norm_eps", ctypes.c_float), ("gate_scale", ctypes.c_float),
                 ("logit_softcap", ctypes.c_float),
                 ("layers", Layer * MAX_LAYERS), ("slots", Slot * MAX_SLOTS),
@@ -132,12 +135,13 @@ class StepDesc(ctypes.Structure):
 _lib = None
 
 
-def load(path: str | None = None):
-    """Load (once) and type the library; raise AltxsLibraryError if unusable."""
+def load():
+    """Load (once) and type the in-tree library (``LIB_PATH``, the only one this
+    package loads); raise AltxsLibraryError if it is missing or unusable."""
     global _lib
     if _lib is not None:
         return _lib
-    path = path or os.environ.get("ALTXS_LIB", LIB_PATH)
+    path = LIB_PATH
     if not os.path.exists(path):
         raise AltxsLibraryError(
             f"{path} not found: build it with `python -m altxs_amd.build` "
@@ -153,6 +157,8 @@ def load(path: str | None = None):
     L.altxs_last_error.argtypes = []
     L.altxs_scale_cum.restype = i32
     L.altxs_scale_cum.argtypes = [p, i64, i64, p, p]
+    L.altxs_scale_cum_f64.restype = i32
+    L.altxs_scale_cum_f64.argtypes = [p, i64, i64, p, p]
     L.altxs_softmax_cdf.restype = i32
     L.altxs_softmax_cdf.argtypes = [p, i64, i64, i32, p, p, p]
     L.altxs_dequant.restype = i32

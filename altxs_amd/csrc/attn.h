@@ -30,7 +30,15 @@ struct AttnP {
   void* y;
   int32_t* err;
   int xcd_rows;  // one-row kernel: rows in tiles of 8, tile t on XCD t % 8
+  int kv_tail = -1;  // natural layouts: first row of the window's K/V (-1: at pos + t)
 };
+
+// Row of the cache that holds key j of a query of segment b whose window starts
+// at pb (tail placement: keys pb .. p live in the rows from a.kv_tail on).
+// Keys past the query's own position keep their own row (read, then masked).
+__device__ __forceinline__ int key_row(const AttnP& a, int j, int pb, int p) {
+  return (a.kv_tail >= 0 && j >= pb && j <= p) ? a.kv_tail + (j - pb) : j;
+}
 
 // Per-wave partial results, merged in wave order by the whole workgroup.
 template <int G> struct alignas(16) MergeLds {

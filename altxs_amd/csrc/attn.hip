@@ -93,7 +93,25 @@ __device__ __forceinline__ float transpose_reduce(float (&v)[N], int lane) {
   return v[0];
 }
 
-template <int G, int YBF16>
+// Four consecutive dims of cache row `row` (natural layout) as fp32.
+template <class KVT>
+__device__ __forceinline__ f32x4 load4(const KVT* base, int64_t row, int d) {
+  if constexpr (std::is_same<KVT, float>::value) {
+    return __builtin_nontemporal_load((const f32x4*)(base + row * HD + d));
+  } else {
+    const u32x2 w = __builtin_nontemporal_load((const u32x2*)(base + row * HD + d));
+    return f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+  }
+}
+template <class KVT>
+__device__ __forceinline__ float load1(const KVT* base, int64_t row, int d) {
+  if constexpr (std::is_same<KVT, float>::value) return base[row * HD + d];
+  else return bf16_to_f32(base[row * HD + d]);
+}
+
+// KVT = float (fp32 cache) or uint16_t (bf16 values in the natural order; the
+// arithmetic is the fp32 kernel's on the widened values).
+template <int G, int YBF16, class KVT>
 __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
   int r = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
@@ -105,11 +123,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
   }
   const int b = r / a.W, t = r % a.W;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  const int p = clamp_pos(a, b, t, a.pos[b]);
+  int pb = a.pos[b];
+  if (a.kv_tail >= 0 && pb > a.kv_tail) {  // the prefix would run into the window rows
+    if (threadIdx.x == 0) flag_err(a.err, ALTXS_EDEV_POS);
+    pb = a.kv_tail;
+  }
+  const int p = clamp_pos(a, b, t, pb);
   const int nkeys = p + 1;
   const int ntiles = (nkeys + TILE - 1) / TILE;
-  const float* kb = (const float*)a.k + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
-  const float* vb = (const float*)a.v + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
+  const KVT* kb = (const KVT*)a.k + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
+  const KVT* vb = (const KVT*)a.v + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
   const int dslice = V_EPL * (lane % V_LPK);
   const int ksub = lane / V_LPK;
   float qv[G][V_EPL];
@@ -131,11 +154,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
     const int k0 = T * TILE;
     f32x4 kr[V_NI], vr[V_NI];
 #pragma unroll
-    for (int i = 0; i < V_NI; ++i)
-      kr[i] = __builtin_nontemporal_load((const f32x4*)(kb + (int64_t)(k0 + V_KPI * i + ksub) * HD + dslice));
+    for (int i = 0; i < V_NI; ++i) kr[i] = load4(kb, key_row(a, k0 + V_KPI * i + ksub, pb, p), dslice);
 #pragma unroll
-    for (int i = 0; i < V_NI; ++i)
-      vr[i] = __builtin_nontemporal_load((const f32x4*)(vb + (int64_t)(k0 + V_KPI * i + ksub) * HD + dslice));
+    for (int i = 0; i < V_NI; ++i) vr[i] = load4(vb, key_row(a, k0 + V_KPI * i + ksub, pb, p), dslice);
     const int my_key = k0 + V_KPI * (lane % V_LPK) + ksub;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
@@ -183,12 +204,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
   }
   __syncthreads();
   merge_and_store<G, YBF16>(a, sm, r, g, p, wave, lane,
-                            [&](int pp, int d) { return vb[(int64_t)pp * HD + d]; });
+                            [&](int pp, int d) { return load1(vb, key_row(a, pp, pb, p), d); });
 }
 
 template <int YBF16>
-hipError_t launch_y(const AttnP& p, int group, bool kv_bf16, bool ops_bf16, bool rows_only,
+hipError_t launch_y(const AttnP& p, int group, int kv_layout, bool ops_bf16, bool rows_only,
                     hipStream_t s) {
+  const bool kv_bf16 = kv_layout == ALTXS_KV_BF16;  // the MFMA kernels read the tiled layout
   dim3 grid((unsigned)(p.B * p.W * p.Hkv)), block(ATT_THREADS);
 #define ATT_GO(K) \
   do { hipLaunchKernelGGL(K, grid, block, 0, s, p); return hipGetLastError(); } while (0)
@@ -220,10 +242,14 @@ hipError_t launch_y(const AttnP& p, int group, bool kv_bf16, bool ops_bf16, bool
       if (group == 2) ATT_GO((attn_mfma_kernel<2, 3, YBF16>));
       if (group == 4) ATT_GO((attn_mfma_kernel<4, 3, YBF16>));
     }
+  } else if (kv_layout == ALTXS_KV_BF16_NATURAL) {
+    if (group == 1) ATT_GO((attn_valu_kernel<1, YBF16, uint16_t>));
+    if (group == 2) ATT_GO((attn_valu_kernel<2, YBF16, uint16_t>));
+    if (group == 4) ATT_GO((attn_valu_kernel<4, YBF16, uint16_t>));
   } else {
-    if (group == 1) ATT_GO((attn_valu_kernel<1, YBF16>));
-    if (group == 2) ATT_GO((attn_valu_kernel<2, YBF16>));
-    if (group == 4) ATT_GO((attn_valu_kernel<4, YBF16>));
+    if (group == 1) ATT_GO((attn_valu_kernel<1, YBF16, float>));
+    if (group == 2) ATT_GO((attn_valu_kernel<2, YBF16, float>));
+    if (group == 4) ATT_GO((attn_valu_kernel<4, YBF16, float>));
   }
 #undef ATT_GO
   return hipErrorInvalidValue;
@@ -240,8 +266,9 @@ hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s) {
   const bool ops_bf16 = (a.flags & ALTXS_ATTN_OPS_BF16) != 0;
   const bool rows_only = (a.flags & ALTXS_ATTN_ROWS) != 0;
   p.xcd_rows = ((a.flags & ALTXS_ATTN_XCD_ROWS) != 0 && (int64_t)a.B * a.W % 64 == 0) ? 1 : 0;
-  return a.y_bf16 ? launch_y<1>(p, group, a.kv_bf16 != 0, ops_bf16, rows_only, s)
-                  : launch_y<0>(p, group, a.kv_bf16 != 0, ops_bf16, rows_only, s);
+  p.kv_tail = a.kv_tail_end > 0 ? a.kv_tail_end - a.W : -1;
+  return a.y_bf16 ? launch_y<1>(p, group, a.kv_bf16, ops_bf16, rows_only, s)
+                  : launch_y<0>(p, group, a.kv_bf16, ops_bf16, rows_only, s);
 }
 
 extern "C" int32_t altxs_decode_attn(const AltxsAttnArgs* a, altxs_stream_t stream) {
@@ -259,6 +286,13 @@ extern "C" int32_t altxs_decode_attn(const AltxsAttnArgs* a, altxs_stream_t stre
                 "altxs_decode_attn: kv_seg_stride too small");
   ALTXS_REQUIRE((a->flags & ~(ALTXS_ATTN_OPS_BF16 | ALTXS_ATTN_ROWS | ALTXS_ATTN_XCD_ROWS)) == 0,
                 "altxs_decode_attn: unknown flags 0x%x", a->flags);
+  ALTXS_REQUIRE(a->kv_bf16 == ALTXS_KV_F32 || a->kv_bf16 == ALTXS_KV_BF16 ||
+                    a->kv_bf16 == ALTXS_KV_BF16_NATURAL,
+                "altxs_decode_attn: kv_bf16=%d is not a KV layout", a->kv_bf16);
+  ALTXS_REQUIRE(a->kv_tail_end == 0 || (a->kv_bf16 != ALTXS_KV_BF16 && a->kv_tail_end >= a->W &&
+                                        a->kv_tail_end <= a->max_len),
+                "altxs_decode_attn: kv_tail_end=%d needs a natural layout and W <= kv_tail_end <= "
+                "max_len", a->kv_tail_end);
   ALTXS_REQUIRE(((uintptr_t)a->k & 15) == 0 && ((uintptr_t)a->v & 15) == 0 && ((uintptr_t)a->q & 15) == 0,
                 "altxs_decode_attn: q, k and v must be 16-byte aligned");
   ALTXS_CHECK_HIP(altxs_launch_attn(*a, (hipStream_t)stream));

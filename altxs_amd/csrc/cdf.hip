@@ -25,6 +25,17 @@ __device__ __forceinline__ uint32_t scale_count(float p) {
   return (uint32_t)f;
 }
 
+// The same rule on a float64 probability (the reference converts every row to
+// float64 first, arithmetic_coder_lm.py:58-60; an fp32 value converts exactly).
+__device__ __forceinline__ uint32_t scale_count64(double p) {
+  double t = __dmul_rn(p, 1000000.0);
+  t = __dadd_rn(t, 0.5);
+  double f = floor(t);
+  if (!(f >= 1.0)) return 1u;
+  if (f >= 4294967295.0) return 0xffffffffu;
+  return (uint32_t)f;
+}
+
 // Fixed-order block reductions over 16 waves.
 __device__ __forceinline__ float block_max(float v, float* red) {
   v = wave_max(v);
@@ -119,6 +130,31 @@ __global__ __launch_bounds__(CDF_THREADS) void cdf_kernel(const float* __restric
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     f[i] = (base + i < V) ? scale_count(v[i]) : 0u;
+    tot += f[i];
+  }
+  uint32_t run = block_excl_scan(tot, wred);
+  uint32_t* co = cum + row * (int64_t)(V + 1);
+  if (threadIdx.x == 0) co[0] = 0u;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    run += f[i];
+    if (base + i < V) co[base + i + 1] = run;
+  }
+}
+
+// float64 probability rows -> CDF rows (one 1024-thread workgroup per row).
+template <int EPT>
+__global__ __launch_bounds__(CDF_THREADS) void cdf_f64_kernel(const double* __restrict__ in, int V,
+                                                               uint32_t* __restrict__ cum) {
+  __shared__ uint32_t wred[CDF_WAVES];
+  const int64_t row = blockIdx.x;
+  const double* x = in + row * (int64_t)V;
+  const int base = threadIdx.x * EPT;
+  uint32_t f[EPT];
+  uint32_t tot = 0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    f[i] = (base + i < V) ? scale_count64(x[base + i]) : 0u;
     tot += f[i];
   }
   uint32_t run = block_excl_scan(tot, wred);
@@ -402,6 +438,26 @@ extern "C" int32_t altxs_scale_cum(const float* probs, int64_t rows, int64_t V, 
   ALTXS_CHECK_HIP(altxs_launch_cdf(probs, rows, (int)V, 0, false, nullptr, cum,
                                    (hipStream_t)stream));
   return ALTXS_OK;
+}
+
+extern "C" int32_t altxs_scale_cum_f64(const double* probs, int64_t rows, int64_t V, uint32_t* cum,
+                                       altxs_stream_t stream) {
+  ALTXS_REQUIRE(probs && cum, "altxs_scale_cum_f64: null pointer");
+  ALTXS_REQUIRE(V >= 1 && V <= 65536, "altxs_scale_cum_f64: V=%lld outside [1, 65536]", (long long)V);
+  ALTXS_REQUIRE(rows >= 0 && rows < (1ll << 31), "altxs_scale_cum_f64: bad rows");
+  if (rows == 0) return ALTXS_OK;
+  const int ept = (int)((V + CDF_THREADS - 1) / CDF_THREADS);
+  const dim3 grid((unsigned)rows), block(CDF_THREADS);
+  hipStream_t s = (hipStream_t)stream;
+#define F64_CASE(E)                                                                                \
+  if (ept <= E) {                                                                                  \
+    hipLaunchKernelGGL(cdf_f64_kernel<E>, grid, block, 0, s, probs, (int)V, cum);                  \
+    ALTXS_CHECK_HIP(hipGetLastError());                                                            \
+    return ALTXS_OK;                                                                               \
+  }
+  F64_CASE(1) F64_CASE(2) F64_CASE(4) F64_CASE(8) F64_CASE(16) F64_CASE(32) F64_CASE(64)
+#undef F64_CASE
+  return ALTXS_ERR_ARG;
 }
 
 extern "C" int32_t altxs_softmax_cdf(const float* logits, int64_t rows, int64_t V, int32_t flags,

@@ -181,6 +181,12 @@ int validate(const AltxsStepDesc* d) {
   ALTXS_REQUIRE(d->n_slots >= 1 && d->n_slots <= ALTXS_MAX_SLOTS, "altxs_step: n_slots");
   ALTXS_REQUIRE(d->max_len >= 256 && d->max_len % 256 == 0, "altxs_step: max_len=%d must be a multiple of 256",
                 d->max_len);
+  ALTXS_REQUIRE(d->kv_bf16 == ALTXS_KV_F32 || d->kv_bf16 == ALTXS_KV_BF16 || d->kv_bf16 == ALTXS_KV_BF16_NATURAL,
+                "altxs_step: kv_bf16=%d is not a KV layout", d->kv_bf16);
+  ALTXS_REQUIRE(d->kv_tail_end == 0 || (d->kv_bf16 != ALTXS_KV_BF16 && d->kv_tail_end >= d->W &&
+                                        d->kv_tail_end <= d->max_len),
+                "altxs_step: kv_tail_end=%d needs a natural KV layout and W <= kv_tail_end <= max_len",
+                d->kv_tail_end);
   ALTXS_REQUIRE(d->rope_dims >= 8 && d->rope_dims <= HD && d->rope_dims % 8 == 0,
                 "altxs_step: rope_dims=%d", d->rope_dims);
   ALTXS_REQUIRE(d->gate_window >= 0 && d->gate_window <= d->D, "altxs_step: gate_window");
@@ -327,6 +333,7 @@ struct StepRun {
     epi = EpiQKV{};
     epi.q = w.Q; epi.kv = slot_kv(G, s); epi.kv_bf16 = d->kv_bf16; epi.H = d->H; epi.Hkv = d->Hkv;
     epi.W = d->W; epi.max_len = d->max_len; epi.rd = d->rope_dims; epi.pos = G.pos;
+    epi.kv_tail = d->kv_tail_end > 0 ? d->kv_tail_end - d->W : -1;
     epi.cosb = d->rope_cos; epi.sinb = d->rope_sin; epi.q_gain = L.q_gain; epi.eps = d->norm_eps;
     epi.err = d->err;
     if (S.lora_q_a) {
@@ -380,6 +387,7 @@ struct StepRun {
     a.gate = (d->flags & ALTXS_F_SPARSE_GATE) ? w.GATE : nullptr;
     a.use_xsa = L.use_xsa; a.y = w.Y; a.err = d->err;
     a.flags = (AM == A_BF16 ? ALTXS_ATTN_OPS_BF16 : 0) | (xr(G) ? ALTXS_ATTN_XCD_ROWS : 0);
+    a.kv_tail_end = d->kv_tail_end;
     return a;
   }
 
@@ -519,7 +527,7 @@ bool persist_ok(const AltxsStepDesc* d) {
     const AltxsLayer& L = d->layers[l];
     if (L.qkv.bits > 6 || L.o.bits > 6 || L.up.bits > 6 || L.down.bits > 6) return false;
   }
-  return d->kv_bf16 && 16 % d->W == 0 && !split_mode(d);
+  return d->kv_bf16 == ALTXS_KV_BF16 && d->kv_tail_end == 0 && 16 % d->W == 0 && !split_mode(d);
 }
 int64_t plan_slots_off() { return align_up((int64_t)sizeof(PersistArgs), 256); }
 int64_t plan_bytes_of(const AltxsStepDesc* d) {
@@ -691,7 +699,7 @@ extern "C" int32_t altxs_step_plan_build(const AltxsStepDesc* d, void* plan_host
   ALTXS_REQUIRE(bytes >= plan_bytes_of(d), "altxs_step_plan_build: %lld bytes < %lld",
                 (long long)bytes, (long long)plan_bytes_of(d));
   ALTXS_REQUIRE(persist_ok(d),
-                "altxs_step_plan_build: the persistent kernel needs a bf16 KV cache, W dividing 16 "
+                "altxs_step_plan_build: the persistent kernel needs a tiled bf16 KV cache (no tail rows), W dividing 16 "
                 "and one stream");
   const Group G = make_group(d, 0, d->B, (char*)d->ws);
   fill_plan(d, G, (char*)plan_host, (const char*)plan_dev);
@@ -710,7 +718,7 @@ extern "C" int32_t altxs_step(const AltxsStepDesc* d, altxs_stream_t stream) {
     ALTXS_REQUIRE(d->plan_host && d->plan_bytes >= plan_bytes_of(d),
                   "altxs_step: plan_dev needs plan_host and plan_bytes");
     ALTXS_REQUIRE(persist_ok(d),
-                  "altxs_step: the persistent kernel needs a bf16 KV cache, W dividing 16 and one stream");
+                  "altxs_step: the persistent kernel needs a tiled bf16 KV cache (no tail rows), W dividing 16 and one stream");
     const Group G = make_group(d, 0, d->B, (char*)d->ws);
     static thread_local std::vector<char> img;
     img.resize((size_t)plan_bytes_of(d));
@@ -741,6 +749,8 @@ extern "C" int32_t altxs_step(const AltxsStepDesc* d, altxs_stream_t stream) {
 
 extern "C" int32_t altxs_rms_qgemm(const AltxsQTensor* w, const float* x, int64_t rows, float ln_scale,
                                    float eps, int32_t act_bf16, float* y, altxs_stream_t stream) {
+  ALTXS_REQUIRE((act_bf16 & ~(ALTXS_RMS_ROUND_ROW | ALTXS_RMS_ROUND_SCALE)) == 0,
+                "altxs_rms_qgemm: unknown rounding flags 0x%x", act_bf16);
   ALTXS_REQUIRE(w && w->codes && (w->bits == 16 || w->scales), "altxs_rms_qgemm: null tensor");
   ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6 || w->bits == 16,
                 "altxs_rms_qgemm: bits=%d", w->bits);
@@ -753,11 +763,13 @@ extern "C" int32_t altxs_rms_qgemm(const AltxsQTensor* w, const float* x, int64_
   ALTXS_REQUIRE(x && y && ((uintptr_t)x & 15) == 0, "altxs_rms_qgemm: x must be 16-byte aligned");
   ALTXS_REQUIRE(rows >= 1 && rows <= (1 << 20), "altxs_rms_qgemm: rows=%lld", (long long)rows);
   ProNorm pro{x, nullptr, 0, ln_scale, eps, (int)w->K};
+  pro.round_scale = (act_bf16 & ALTXS_RMS_ROUND_SCALE) ? 1 : 0;
   EpiStore epi{y, (int)w->N, 0};
   const QT q = qt_of(*w);
   hipStream_t st = (hipStream_t)stream;
   const hipError_t e =
-      act_bf16 ? launch_gemm_bits<A_BF16, 4, 1>(w->bits, q, (int)rows, 1, 0, 0, ADirect{nullptr, 0}, pro,
+      (act_bf16 & ALTXS_RMS_ROUND_ROW)
+               ? launch_gemm_bits<A_BF16, 4, 1>(w->bits, q, (int)rows, 1, 0, 0, ADirect{nullptr, 0}, pro,
                                                   epi, 0, st)
                : launch_gemm_bits<A_F32, 4, 1>(w->bits, q, (int)rows, 1, 0, 0, ADirect{nullptr, 0}, pro,
                                                  epi, 0, st);

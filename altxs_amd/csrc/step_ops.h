@@ -265,6 +265,7 @@ struct ProNorm {
   float* gate_out = nullptr;      // [R, H]
   float gate_scale = 0.f;
   int H = 0, gw = 0;
+  int round_scale = 0;  // 1: the rsqrt factor rounded to bf16 before the products
   template <int AM, int NT>
   __device__ void stage(void* As, void*, int m0, int R, int K, int, bool first) const {
     static_assert(NT == 16 * PTPR, "one row per 16 lanes, 16 rows per task");
@@ -304,7 +305,8 @@ struct ProNorm {
       }
     }
     ss = row16_sum(ss);
-    const float inv = r < R ? rsqrtf(ss / (float)D + eps) : 0.f;
+    float inv = r < R ? rsqrtf(ss / (float)D + eps) : 0.f;
+    if (round_scale) inv = round_bf16(inv);
     float n0[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < PMAXJ; ++j) {
@@ -431,7 +433,10 @@ __device__ __forceinline__ int row_pos(const int32_t* pos, int W, int r) {
 struct EpiQKV {
   float* q;          // [R, H, 64]
   char* kv;          // this slot's cache: [B][2][Hkv][max_len][64]
-  int kv_bf16, H, Hkv, W, max_len, rd;
+  int kv_bf16, H, Hkv, W, max_len, rd;  // kv_bf16: ALTXS_KV_F32 / ALTXS_KV_BF16 / ALTXS_KV_BF16_NATURAL
+  // natural layouts: window token t's K/V go to row kv_tail + t (the reference's
+  // tail rows, model.py:259-461) instead of its position; -1 = at the position
+  int kv_tail = -1;
   const int32_t* pos;
   const float* cosb;  // [max_len, rd/2]
   const float* sinb;
@@ -529,7 +534,9 @@ struct EpiQKV {
   // The RoPE partner (rd / 2 columns away, a multiple of 8) is rd / 16
   // threads away.  Without LoRA, bf16 cache only.
   static constexpr bool kStrip = true;
-  __device__ bool strip_ok() const { return rank == 0 && kv_bf16 && rd % 16 == 0 && rd <= HD; }
+  __device__ bool strip_ok() const {
+    return rank == 0 && kv_bf16 == ALTXS_KV_BF16 && kv_tail < 0 && rd % 16 == 0 && rd <= HD;
+  }
   template <class Cfg>
   __device__ void strip(const float* Cst, int r0, int n0, int R) const {
     const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
@@ -642,7 +649,10 @@ struct EpiQKV {
     }
     if (r >= R) return;
     const int p = pre.p;
-    const bool pos_ok = p >= 0 && p < max_len;
+    // the row the K/V go to: the position, or the window's tail row (whose
+    // prefix [0, pos) must end at or before the tail)
+    const int krow = kv_tail >= 0 ? kv_tail + r % W : p;
+    const bool pos_ok = p >= 0 && p < max_len && (kv_tail < 0 || p - r % W <= kv_tail);
     static_assert(CPT == 4, "four consecutive columns per thread (16-byte q / K stores)");
     if (kind == 0) {  // q row: 16-byte aligned (c0 % 4 == 0)
       *(f32x4*)(q + ((int64_t)r * H + head) * HD + c0) =
@@ -650,9 +660,13 @@ struct EpiQKV {
     } else if (pos_ok) {
       const int b = r / W;
       const int64_t head_base = (((int64_t)b * 2 + (kind == 2 ? 1 : 0)) * Hkv + head) * max_len * HD;
-      if (kv_bf16) {  // tiled operand layout (kv_tile_k / kv_tile_v)
-        uint16_t* tile = (uint16_t*)kv + head_base + (int64_t)(p / ALTXS_KV_TILE) * (ALTXS_KV_TILE * HD);
-        const int kt = p % ALTXS_KV_TILE;
+      if (kv_bf16 == ALTXS_KV_BF16_NATURAL) {  // natural order: 4 dims = one 8-byte store
+        *(u32x2*)((uint16_t*)kv + head_base + (int64_t)krow * HD + c0) =
+            u32x2{(uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                  (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16)};
+      } else if (kv_bf16) {  // tiled operand layout (kv_tile_k / kv_tile_v)
+        uint16_t* tile = (uint16_t*)kv + head_base + (int64_t)(krow / ALTXS_KV_TILE) * (ALTXS_KV_TILE * HD);
+        const int kt = krow % ALTXS_KV_TILE;
         if (kind == 1) {  // K: dims c0 .. c0+3 are adjacent in the tile (one 8-byte store)
           *(u32x2*)(tile + kv_tile_k(kt, c0)) =
               u32x2{(uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
@@ -662,7 +676,7 @@ struct EpiQKV {
           for (int i = 0; i < CPT; ++i) tile[kv_tile_v(kt, c0 + i)] = f32_to_bf16(v[i]);
         }
       } else {
-        *(f32x4*)((float*)kv + head_base + (int64_t)p * HD + c0) = f32x4{v[0], v[1], v[2], v[3]};
+        *(f32x4*)((float*)kv + head_base + (int64_t)krow * HD + c0) = f32x4{v[0], v[1], v[2], v[3]};
       }
     } else if (li == 0) {
       flag_err(err, ALTXS_EDEV_POS);

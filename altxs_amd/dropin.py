@@ -17,8 +17,14 @@ library raises).
   persistent_step.py:1081-1119 / mega_encode.py:1693-1790: the W-token step
   into a reference-shaped ``StaticState`` (model.py:358-461) of a
   reference-shaped ``GPT`` (``model.cfg`` with the reference's config names,
-  ``model.state_dict()`` with its parameter names).  False (and disabled
-  after an error, logged once) when the step cannot run, as the reference.
+  ``model.state_dict()`` with its parameter names).  The state's slots become
+  views of the step's cache (:class:`_KVWorkspace`), so the engine's prefill,
+  row sync and commits are what the step reads.  False (and disabled after an
+  error, logged once) when the step cannot run, as the reference.
+* :func:`prepare_persistent` / :func:`prepare_mega_encode` <-
+  persistent_step.py:452-588 / mega_encode.py:1206-1351 (the workspace with
+  ``k_pack`` / ``v_pack`` that ``_rebind_packed_kv`` and ``commit_packed_row``
+  use); :func:`refresh_persistent_weights` / :func:`refresh_encode_weights`.
 * :func:`load_codec` <- ``load_codec(codec_path, *, device)``
   (src/hyperflow_distillation/mixed_bit_delta.py:232-312).
 * :func:`gemv_rows` / :func:`gemv_vec` / :func:`logits_stage_rows` <-
@@ -36,7 +42,8 @@ from __future__ import annotations
 import ctypes
 import dataclasses
 import sys
-from typing import Any, Callable, Sequence
+from collections import OrderedDict
+from typing import Callable, Sequence
 
 import numpy as np
 import torch
@@ -66,33 +73,32 @@ class _TableRows:
     def tables(self, p: np.ndarray) -> np.ndarray:
         rows, V = p.shape
         if self.probs is None or self.probs.shape[0] < rows or self.probs.shape[1] != V:
-            self.probs = torch.empty(max(rows, 1), V, dtype=torch.float32, device="cuda")
+            self.probs = torch.empty(max(rows, 1), V, dtype=torch.float64, device="cuda")
             self.cum = torch.empty(max(rows, 1), V + 1, dtype=torch.int32, device="cuda")
         pr, cm = self.probs[:rows], self.cum[:rows]
         pr.copy_(torch.from_numpy(p))
-        rc = _lib.load().altxs_scale_cum(pr.data_ptr(), rows, V, cm.data_ptr(), _stream(pr))
-        _lib.check(rc, "altxs_scale_cum")
+        rc = _lib.load().altxs_scale_cum_f64(pr.data_ptr(), rows, V, cm.data_ptr(), _stream(pr))
+        _lib.check(rc, "altxs_scale_cum_f64")
         return cm.cpu().numpy().view(np.uint32).astype(np.int64)
 
 
 _ROWS = _TableRows()
 
 
-def _fp32_rows(probs, n: int) -> np.ndarray:
-    p = np.asarray(probs)
-    if p.size != n:
-        raise ValueError(f"probs_fn must return {n} probabilities, got {p.size}")
-    p32 = p.astype(np.float32).reshape(1, n)
-    if p.dtype != np.float32 and not np.array_equal(p32.astype(np.float64), p.astype(np.float64).reshape(1, n)):
-        raise ValueError("probabilities must be float32 values (the device rule reads fp32 rows)")
-    return np.ascontiguousarray(p32)
+def _f64_rows(probs, n: int) -> np.ndarray:
+    """One probability row as float64, the type the reference's rule converts
+    every row to (arithmetic_coder_lm.py:56-59); fp32 values convert exactly."""
+    if len(probs) != n:
+        raise ValueError(f"probs_fn must return {n} probabilities, got {len(probs)}")
+    return np.ascontiguousarray(np.asarray(probs, dtype=np.float64).reshape(1, n))
 
 
 def _scale_cum_np(probs: Sequence[float], *, alphabet_size: int = 256) -> tuple[np.ndarray, int]:
-    """probs -> (cum int64[V+1], total): f_i = max(1, floor(p_i * 1e6 + 0.5)),
-    cum_0 = 0 (arithmetic_coder_lm.py:49-64), computed by ``altxs_scale_cum``."""
+    """probs -> (cum int64[V+1], total): f_i = max(1, floor(p_i * 1e6 + 0.5))
+    in float64, cum_0 = 0 (arithmetic_coder_lm.py:49-64), computed by
+    ``altxs_scale_cum_f64``."""
     n = int(alphabet_size)
-    cum = _ROWS.tables(_fp32_rows(probs, n))[0]
+    cum = _ROWS.tables(_f64_rows(probs, n))[0]
     return cum, int(cum[n])
 
 
@@ -121,9 +127,13 @@ class GpuRangeCoder:
         self._lib = _lib.load()
 
     def _table(self, probs: torch.Tensor) -> None:
-        p = probs.view(-1)
-        if p.dtype != torch.float32 or not p.is_contiguous() or p.numel() != self.vocab:
-            raise ValueError(f"probs must be {self.vocab} contiguous float32 values on the device")
+        # a float32 contiguous vector, cast like the reference's _probs_arg
+        # (gpu_ac.py:415-426)
+        p = probs.reshape(-1)
+        if p.dtype != torch.float32 or not p.is_contiguous():
+            p = p.float().contiguous()
+        if p.numel() != self.vocab or p.device.type != "cuda":
+            raise ValueError(f"probs must hold {self.vocab} values on the device")
         rc = self._lib.altxs_scale_cum(p.data_ptr(), 1, self.vocab, self._cum.data_ptr(), _stream(p))
         _lib.check(rc, "altxs_scale_cum")
 
@@ -166,15 +176,15 @@ def encode_with_probs(symbols, probs_fn: Callable, *, desc: str | None = None,
         raise ValueError(f"symbol {bad} out of alphabet [0, {V})")
     if desc is not None:
         print(f"[{desc}] starting ({n} sym)…", file=sys.stderr, flush=True)
-    rows = np.empty((max(n, 1), V), dtype=np.float32)
+    rows = np.empty((max(n, 1), V), dtype=np.float64)
     for i in range(n):
-        rows[i] = _fp32_rows(probs_fn(i, symbols[:i]), V)[0]
+        rows[i] = _f64_rows(probs_fn(i, symbols[:i]), V)[0]
     rc = RangeCoder(1, 64 + 4 * n)
     if n:
         pr = torch.from_numpy(rows[:n]).cuda()
         cum = torch.empty(n, V + 1, dtype=torch.int32, device="cuda")
-        _lib.check(_lib.load().altxs_scale_cum(pr.data_ptr(), n, V, cum.data_ptr(), _stream(pr)),
-                   "altxs_scale_cum")
+        _lib.check(_lib.load().altxs_scale_cum_f64(pr.data_ptr(), n, V, cum.data_ptr(), _stream(pr)),
+                   "altxs_scale_cum_f64")
         rc.encode(cum, torch.from_numpy(syms.astype(np.int32)).cuda().view(1, n))
     return rc.finish()[0]
 
@@ -191,14 +201,14 @@ def decode_with_probs(bitstream: bytes, n_symbols: int, probs_fn: Callable, *, d
         print(f"[{desc}] starting ({n_symbols} sym)…", file=sys.stderr, flush=True)
     rc = RangeCoder(1, len(bitstream) + 8)
     rc.begin_decode([bytes(bitstream)])
-    dev_rows = torch.empty(1, V, dtype=torch.float32, device="cuda")
+    dev_rows = torch.empty(1, V, dtype=torch.float64, device="cuda")
     cum = torch.empty(1, V + 1, dtype=torch.int32, device="cuda")
     sym = torch.empty(1, 1, dtype=torch.int32, device="cuda")
     L = _lib.load()
     for i in range(int(n_symbols)):
-        dev_rows.copy_(torch.from_numpy(_fp32_rows(probs_fn(i, buf), V)))
-        _lib.check(L.altxs_scale_cum(dev_rows.data_ptr(), 1, V, cum.data_ptr(), _stream(dev_rows)),
-                   "altxs_scale_cum")
+        dev_rows.copy_(torch.from_numpy(_f64_rows(probs_fn(i, buf), V)))
+        _lib.check(L.altxs_scale_cum_f64(dev_rows.data_ptr(), 1, V, cum.data_ptr(), _stream(dev_rows)),
+                   "altxs_scale_cum_f64")
         rc.decode(cum, sym)
         s = int(sym.item())
         buf.append(s)
@@ -235,36 +245,98 @@ def dense_model_from_state(cfg: AltxsConfig, state: dict, device="cuda") -> Synt
     return SynthModel(cfg, packed, small)
 
 
-class _Adapter:
-    """Per reference model: the step model and one mirror state per reference state."""
+class _KVWorkspace:
+    """The KV role of the reference's step workspaces (``_PersistWS`` /
+    ``_EncodeWS``, persistent_step.py:452-588, mega_encode.py:1206-1351) over
+    this build's cache.
 
-    def __init__(self, model, act: str):
-        self.cfg = config_from_reference(model.cfg)
-        dev = next((v.device for v in model.state_dict().values() if torch.is_tensor(v)), None)
-        self.device = dev if dev is not None and dev.type == "cuda" else torch.device("cuda")
-        self.step = StepModel(dense_model_from_state(self.cfg, model.state_dict(), self.device),
-                              device=self.device, act=act, kv=act)
-        self.states: dict[int, tuple[Any, StaticState]] = {}
+    ``k_pack`` / ``v_pack`` are ``[n_slots, n_kv, max_len, hd]`` views of the
+    step state's natural-order cache (bf16 for a bf16 model, fp32 otherwise),
+    and every reference slot's ``k`` / ``v`` is re-pointed to a view of them
+    exactly as ``prepare_persistent`` does (persistent_step.py:472-479), so the
+    engine's eager prefill, ``_rebind_packed_kv``, ``_sync_row_from_prefix``
+    (incremental.py:858-954), ``commit_window`` (model.py:449-461) and
+    ``commit_packed_row`` (row_commit.py:59-98) all land in the memory the
+    step reads.  The step keeps the reference's placement: prefix rows
+    ``[0, pos)``, the window's K/V in the last W rows, committed by the caller.
+    One workspace serves one state at a time, as the reference's does.
+    """
 
-    def mirror(self, state) -> StaticState:
-        hit = self.states.get(id(state))
-        if hit is not None and hit[0] is state:
-            return hit[1]
-        W, L = int(state.win), int(state.max_len)
-        st = self.step.make_static_state((L + CHUNK - 1) // CHUNK * CHUNK, win=W, batch=1,
-                                         want_probs=False, want_cdf=False, rope_len=L)
-        self.states[id(state)] = (state, st)
-        return st
+    def __init__(self, adapter: "_Adapter", state):
+        cfg = adapter.cfg
+        self.win, self.max_len = int(state.win), int(state.max_len)
+        self.n_slots, self.n_kv, self.hd = adapter.step.n_slots, cfg.num_kv_heads, cfg.head_dim
+        self.d = cfg.model_dim
+        if len(state.slots) not in (0, self.n_slots):
+            raise ValueError(f"state has {len(state.slots)} slots, the model's itinerary {self.n_slots}")
+        rows = (self.max_len + CHUNK - 1) // CHUNK * CHUNK
+        self.st = adapter.step.make_static_state(rows, win=self.win, batch=1, want_probs=False,
+                                                 want_cdf=False, rope_len=self.max_len,
+                                                 kv_tail_end=self.max_len)
+        self.k_pack = self.st.kv[:, 0, 0, :, :self.max_len]
+        self.v_pack = self.st.kv[:, 0, 1, :, :self.max_len]
+        self.adopt(state)
 
-    def run(self, state) -> None:
-        st = self.mirror(state)
-        W, D, V = st.win, self.cfg.model_dim, self.cfg.vocab_size
+    def serves(self, state) -> bool:
+        return (int(state.win) == self.win and int(state.max_len) == self.max_len
+                and len(state.slots) in (0, self.n_slots))
+
+    def adopt(self, state) -> None:
+        """Point every slot of ``state`` at this cache, copying in what a slot
+        held elsewhere (a fresh or reallocated ``StaticKV``)."""
+        L, hkv, hd = self.max_len, self.n_kv, self.hd
+        for i, sk in enumerate(state.slots):
+            pk, pv = self.k_pack[i], self.v_pack[i]
+            if sk.k is not None and sk.v is not None and sk.k.data_ptr() == pk.data_ptr() \
+                    and sk.v.data_ptr() == pv.data_ptr() and sk.k.dtype == pk.dtype:
+                continue
+            if sk.k is not None and sk.v is not None:
+                pk.copy_(sk.k.reshape(L, hkv, hd).permute(1, 0, 2))
+                pv.copy_(sk.v.reshape(L, hkv, hd).permute(1, 0, 2))
+            else:
+                pk.zero_()
+                pv.zero_()
+            sk.k = pk.permute(1, 0, 2).unsqueeze(0)
+            sk.v = pv.permute(1, 0, 2).unsqueeze(0)
+
+    def run(self, step: StepModel, state) -> None:
+        self.adopt(state)
+        st, W = self.st, self.win
+        V = step.cfg.vocab_size
         st.token.view(-1).copy_(state.token.view(-1)[:W])
         st.pos.view(-1).copy_(state.pos.view(-1)[:1])
-        st.prev_raw.view(-1).copy_(state.prev_raw.reshape(-1)[:D])
-        self.step.step(st, commit=False)
+        st.prev_raw.view(-1).copy_(state.prev_raw.reshape(-1)[:self.d])
+        step.step(st, commit=False)
         state.logits.view(W, V).copy_(st.logits)
-        state.cand_prev_raw.view(-1)[:D].copy_(st.cand_prev_raw.view(-1))
+        state.cand_prev_raw.view(-1)[:self.d].copy_(st.cand_prev_raw.view(-1))
+
+
+def _bf16_exact(t: torch.Tensor) -> bool:
+    t = t.detach().float()
+    return bool(torch.equal(t, t.to(torch.bfloat16).float()))
+
+
+class _Adapter:
+    """Per reference model: the step model built from its weights."""
+
+    def __init__(self, model, act: str):
+        from .shipped import MODELED
+
+        self.cfg = config_from_reference(model.cfg)
+        sd = model.state_dict()
+        if act == "fp32":
+            # the dense banks hold bf16 values: an fp32 model runs here only if
+            # its matrices are bf16 values (the reference keeps fp32 AC weights
+            # in that mode, model.py:1183-1196)
+            bad = [k for k, v in sd.items() if k in MODELED and torch.is_tensor(v) and not _bf16_exact(v)]
+            if bad:
+                raise ValueError(f"fp32 compute with weights that are not bf16 values ({bad[0]}, ...): "
+                                 "the dense banks here are bf16")
+        dev = next((v.device for v in sd.values() if torch.is_tensor(v)), None)
+        self.device = dev if dev is not None and dev.type == "cuda" else torch.device("cuda")
+        self.act = act
+        self.step = StepModel(dense_model_from_state(self.cfg, sd, self.device),
+                              device=self.device, act=act, kv="bf16n" if act == "bf16" else "fp32")
 
 
 def _adapter(model) -> _Adapter:
@@ -276,26 +348,62 @@ def _adapter(model) -> _Adapter:
     return ad
 
 
+def _workspace(model, state, attr: str) -> _KVWorkspace:
+    ws = getattr(model, attr, None)
+    if not isinstance(ws, _KVWorkspace) or not ws.serves(state):
+        ws = _KVWorkspace(_adapter(model), state)
+        setattr(model, attr, ws)
+    return ws
+
+
+def prepare_persistent(model, state) -> _KVWorkspace | None:
+    """The W=1 workspace (persistent_step.py:452-588): the cache the state's
+    slots now view.  None when the step cannot serve this state."""
+    if int(state.win) != 1:
+        return None
+    try:
+        return _KVWorkspace(_adapter(model), state)
+    except Exception as exc:  # noqa: BLE001 -- the reference returns None here
+        print(f"[AC incr] altxs workspace unavailable ({exc!r})", file=sys.stderr, flush=True)
+        return None
+
+
+def prepare_mega_encode(model, state) -> _KVWorkspace | None:
+    """The W-window workspace (mega_encode.py:1206-1351)."""
+    if int(state.win) < 2:
+        return None
+    try:
+        return _KVWorkspace(_adapter(model), state)
+    except Exception as exc:  # noqa: BLE001
+        print(f"[AC incr] altxs workspace unavailable ({exc!r})", file=sys.stderr, flush=True)
+        return None
+
+
 def refresh_weights(model) -> None:
-    """Re-read the model's weights (after they were changed in place, e.g. by a
-    retrain); states and their KV caches are kept."""
+    """Re-read the model's weights after an in-place update (e.g. a retrain;
+    ``refresh_persistent_weights`` / ``refresh_encode_weights``,
+    persistent_step.py:591-621); workspaces and their caches are kept."""
     ad = getattr(model, "_altxs_adapter", None)
-    if ad is not None:
-        states = ad.states
-        new = _Adapter(model, "bf16" if ad.step.act_bf16 else "fp32")
-        new.states = {}
-        model._altxs_adapter = new
-        for key, (ref_state, st) in states.items():  # keep the caches: rebuild descriptors only
-            st.model = new.step
-            st._descs.clear()
-            new.states[key] = (ref_state, st)
+    if ad is None:
+        return
+    new = _Adapter(model, ad.act)
+    model._altxs_adapter = new
+    for attr in ("_persist_ws", "_encode_ws"):
+        ws = getattr(model, attr, None)
+        if isinstance(ws, _KVWorkspace):  # same buffers, descriptors rebuilt for the new weights
+            ws.st.model = new.step
+            ws.st._descs.clear()
 
 
-def _try(model, state, flag: str, what: str) -> bool:
+refresh_persistent_weights = refresh_weights
+refresh_encode_weights = refresh_weights
+
+
+def _try(model, state, flag: str, attr: str, what: str) -> bool:
     if getattr(model, flag, False):
         return False
     try:
-        _adapter(model).run(state)
+        _workspace(model, state, attr).run(_adapter(model).step, state)
         return True
     except Exception as exc:  # noqa: BLE001 -- reference contract: log once, disable, fall back
         setattr(model, flag, True)
@@ -304,14 +412,23 @@ def _try(model, state, flag: str, what: str) -> bool:
 
 
 def try_persistent_extend(model, state) -> bool:
-    """The W=1 step into ``state.logits`` / ``state.cand_prev_raw`` from
-    ``state.token``, ``state.pos`` and ``state.prev_raw`` (persistent_step.py:1081)."""
-    return _try(model, state, "_persist_disabled", "altxs step")
+    """The W=1 step (persistent_step.py:1081-1119): ``state.logits`` and
+    ``state.cand_prev_raw`` from ``state.token``, ``state.pos``,
+    ``state.prev_raw`` and the slots' prefix rows ``[0, pos)``; the token's
+    K/V go to the slots' last row for the caller's commit.  False for W != 1
+    (the reference's ``can_persistent``), and after an error (logged once)."""
+    if int(state.win) != 1 or state.token.device.type != "cuda":
+        return False
+    return _try(model, state, "_persist_disabled", "_persist_ws", "altxs step")
 
 
 def try_mega_encode(model, state) -> bool:
-    """The W-token teacher-forced window into ``state`` (mega_encode.py:1693)."""
-    return _try(model, state, "_encode_disabled", "altxs window step")
+    """The W-token teacher-forced window (mega_encode.py:1693-1790), same
+    placement: prefix ``[0, pos)``, window K/V in the last W rows.  False for
+    W < 2 (``can_mega_encode``), and after an error."""
+    if int(state.win) < 2 or state.token.device.type != "cuda":
+        return False
+    return _try(model, state, "_encode_disabled", "_encode_ws", "altxs window step")
 
 
 # ---- shipped codec ------------------------------------------------------------------
@@ -335,29 +452,44 @@ def load_codec(codec_path, *, device, init_state: dict, act: str = "bf16"):
 
 
 # ---- kernel-level helpers ------------------------------------------------------------
-_TILED: dict[int, tuple[int, int, torch.Tensor, _lib.QTensor]] = {}
+# Tiled bf16 copies of dense weights, keyed on where the values live; each entry
+# keeps the weight's storage alive so its address cannot be reused by another
+# tensor while cached, and the cache holds at most _TILED_MAX entries (oldest
+# dropped first).
+_TILED: "OrderedDict[tuple, tuple[int, object, torch.Tensor, _lib.QTensor]]" = OrderedDict()
+_TILED_MAX = 256
 
 
 def _tiled(weight: torch.Tensor) -> _lib.QTensor:
     """Dense [N, K] weight -> bits-16 tiled copy, cached until the weight
-    changes in place (torch's version counter)."""
+    changes in place (torch's version counter).  fp32 weights must hold bf16
+    values (the dense format is bf16)."""
     from .shipped import pack_dense
 
-    key = weight.data_ptr()
+    key = (weight.untyped_storage().data_ptr(), weight.storage_offset(), tuple(weight.shape),
+           tuple(weight.stride()), weight.dtype, weight.device)
     hit = _TILED.get(key)
     ver = weight._version
-    if hit is not None and hit[0] == ver and hit[1] == tuple(weight.shape):
+    if hit is not None and hit[0] == ver:
+        _TILED.move_to_end(key)
         return hit[3]
     n, k = weight.shape
     if n % 16 or k % 256:
         raise ValueError(f"weight [{n}, {k}]: N must be a multiple of 16 and K of 256")
+    if weight.dtype != torch.bfloat16 and not _bf16_exact(weight):
+        raise ValueError("the dense weight format is bf16: this fp32 weight holds values that are not "
+                         "bf16 values")
     tiled = pack_dense(weight.detach().float().contiguous())
     qt = _lib.QTensor(tiled.data_ptr(), tiled.data_ptr(), n, k, 16, 0)
-    _TILED[key] = (ver, (n, k), tiled, qt)
+    _TILED[key] = (ver, weight.untyped_storage(), tiled, qt)
+    _TILED.move_to_end(key)
+    while len(_TILED) > _TILED_MAX:
+        _TILED.popitem(last=False)
     return qt
 
 
 _DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+_RMS_ROUND_ROW, _RMS_ROUND_SCALE = 1, 2  # ALTXS_RMS_ROUND_ROW / ALTXS_RMS_ROUND_SCALE
 
 
 def gemv_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -> None:
@@ -386,8 +518,10 @@ def gemv_vec(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -> None:
 def logits_stage_rows(src: torch.Tensor, weight: torch.Tensor, logit_buf: torch.Tensor, *,
                       eps: float = 1e-6) -> None:
     """Final RMS -> LM projection: ``logit_buf[r] = weight @ rms(src[r])``
-    (ac_gemv.py:562-582); bf16 ``src`` rounds the normalised row to bf16 for
-    the products as the reference's bf16 path does."""
+    (ac_gemv.py:312-359, 562-582) with the reference's rounding points: the
+    rsqrt factor in ``src``'s dtype, the product in ``src``'s dtype, then in
+    the weight's dtype (bf16 ``src``: factor and row rounded to bf16; fp32
+    ``src`` with a bf16 weight: the row rounded to bf16; both fp32: none)."""
     win, d = int(src.shape[0]), int(src.shape[1])
     vocab = int(weight.shape[0])
     if tuple(logit_buf.shape) != (win, vocab) or int(weight.shape[1]) != d:
@@ -396,8 +530,14 @@ def logits_stage_rows(src: torch.Tensor, weight: torch.Tensor, logit_buf: torch.
     x = src if (src.dtype == torch.float32 and src.is_contiguous()) else src.float().contiguous()
     y = logit_buf if (logit_buf.dtype == torch.float32 and logit_buf.is_contiguous()) else \
         torch.empty(win, vocab, dtype=torch.float32, device=src.device)
+    if src.dtype == torch.bfloat16:
+        rounding = _RMS_ROUND_ROW | _RMS_ROUND_SCALE
+    elif src.dtype == torch.float32:
+        rounding = _RMS_ROUND_ROW if weight.dtype == torch.bfloat16 else 0
+    else:
+        raise ValueError("src must be fp32 or bf16")
     rc = _lib.load().altxs_rms_qgemm(ctypes.byref(qt), x.data_ptr(), win, 1.0, float(eps),
-                                     int(src.dtype == torch.bfloat16), y.data_ptr(), _stream(src))
+                                     rounding, y.data_ptr(), _stream(src))
     _lib.check(rc, "altxs_rms_qgemm")
     if y is not logit_buf:
         logit_buf.copy_(y)

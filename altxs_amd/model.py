@@ -71,12 +71,19 @@ class StaticState:
 
     def __init__(self, model: "StepModel", batch: int, win: int, max_len: int,
                  want_probs: bool = True, want_cdf: bool = True, split: bool = False,
-                 persistent: bool = False, rope_len: int | None = None):
+                 persistent: bool = False, rope_len: int | None = None, kv_tail_end: int = 0):
         cfg, dev = model.cfg, model.device
         if max_len % CHUNK:
             raise ValueError(f"max_len must be a multiple of {CHUNK}")
         self.model = model
         self.batch, self.win, self.max_len = int(batch), int(win), int(max_len)
+        # > 0: the window's K/V go to rows kv_tail_end - W + t (the reference's
+        # tail rows) and the caller commits them into the prefix; natural layouts
+        self.kv_tail_end = int(kv_tail_end)
+        if self.kv_tail_end and (model.kv_layout == _lib.KV_BF16
+                                 or not self.win <= self.kv_tail_end <= self.max_len):
+            raise ValueError(f"kv_tail_end={kv_tail_end} needs a natural KV layout and "
+                             f"W <= kv_tail_end <= max_len")
         # length the RoPE table is warmed at (sets the YaRN scale); rows kept = max_len
         self.rope_len = int(rope_len) if rope_len is not None else self.max_len
         B, W, V, D = self.batch, self.win, cfg.vocab_size, cfg.model_dim
@@ -85,7 +92,7 @@ class StaticState:
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
         self.prev_raw = torch.zeros(B, D, dtype=torch.float32, device=dev)
         self.cand_prev_raw = torch.zeros(B, D, dtype=torch.float32, device=dev)
-        kv_dtype = torch.bfloat16 if model.kv_bf16 else torch.float32
+        kv_dtype = torch.float32 if model.kv_layout == _lib.KV_F32 else torch.bfloat16
         self.kv = torch.zeros(model.n_slots, B, 2, cfg.num_kv_heads, self.max_len, cfg.head_dim,
                               dtype=kv_dtype, device=dev)
         self.logits = torch.zeros(R, V, dtype=torch.float32, device=dev)
@@ -162,7 +169,7 @@ class StepModel:
         if act not in ("bf16", "fp32"):
             raise ValueError(act)
         kv = kv or act
-        if kv not in ("bf16", "fp32"):
+        if kv not in ("bf16", "fp32", "bf16n"):
             raise ValueError(kv)
         if cfg.head_dim != 64:
             raise ValueError("head_dim must be 64")
@@ -172,6 +179,9 @@ class StepModel:
         self.cfg = cfg
         self.device = torch.device(device)
         self.act_bf16 = act == "bf16"
+        # "bf16": MFMA-tiled bf16 cache; "bf16n": bf16 in the natural (reference
+        # k_pack) order; "fp32": natural fp32
+        self.kv_layout = {"fp32": _lib.KV_F32, "bf16": _lib.KV_BF16, "bf16n": _lib.KV_BF16_NATURAL}[kv]
         self.kv_bf16 = kv == "bf16"
         self.slots = build_itinerary(cfg)
         self.n_slots = len(self.slots)
@@ -209,13 +219,15 @@ class StepModel:
     def make_static_state(self, max_len: int, device=None, win: int = 1, batch: int = 1,
                           want_probs: bool = True, want_cdf: bool = True,
                           split: bool = False, persistent: bool = False,
-                          rope_len: int | None = None) -> StaticState:
+                          rope_len: int | None = None, kv_tail_end: int = 0) -> StaticState:
         """``split``: run the segments as two groups on two streams (B >= 2).
         ``persistent``: run every slot in one persistent launch (bf16 KV, W | 16).
         ``rope_len``: the length the RoPE table is warmed at (default max_len);
-        the reference engine warms it at its static length (incremental.py:239-242)."""
+        the reference engine warms it at its static length (incremental.py:239-242).
+        ``kv_tail_end``: keep the window's K/V in rows kv_tail_end - W + t, the
+        reference StaticKV's tail (model.py:259-461), for the caller to commit."""
         return StaticState(self, batch, win, max_len, want_probs, want_cdf, split, persistent,
-                           rope_len)
+                           rope_len, kv_tail_end)
 
     def _fill_desc(self, st: StaticState, flags: int) -> _lib.StepDesc:
         cfg = self.cfg
@@ -226,7 +238,8 @@ class StepModel:
         d.n_layers, d.n_slots, d.max_len = cfg.num_layers, self.n_slots, st.max_len
         d.gate_window, d.rope_dims = cfg.gate_window, cfg.rope_dims_eff
         d.lora_rank = cfg.lora_rank if self.lora else 0
-        d.act_bf16, d.kv_bf16 = int(self.act_bf16), int(self.kv_bf16)
+        d.act_bf16, d.kv_bf16 = int(self.act_bf16), int(self.kv_layout)
+        d.kv_tail_end = int(getattr(st, "kv_tail_end", 0))
         f = flags
         if cfg.smear_gate_enabled:
             f |= _lib.F_SMEAR

@@ -121,7 +121,7 @@ def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Te
                 W: int = 1, gate: torch.Tensor | None = None, use_xsa: bool = False,
                 y_bf16: bool = False, ops_bf16: bool = False, tiled: bool = False,
                 err: torch.Tensor | None = None, rows: bool = False,
-                xcd_rows: bool = False) -> torch.Tensor:
+                xcd_rows: bool = False, natural: bool = False, kv_tail_end: int = 0) -> torch.Tensor:
     """q [B*W, H, 64] fp32; k/v [B, Hkv, max_len, 64] (fp32 or bf16); pos [B] int32.
 
     bf16 k/v are given in natural [key][dim] order and tiled here
@@ -132,6 +132,11 @@ def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Te
     decode kernel) instead of the window kernel; the bits are the same.
     ``xcd_rows`` places the one-row kernel's workgroups in 8-row tiles, tile t
     on XCD t % 8 (B*W a multiple of 64; otherwise ignored); the bits are the same.
+    ``natural`` keeps bf16 k/v in their natural order (the VALU kernel reads
+    them; fp32 products of the bf16 values).  ``kv_tail_end`` (natural
+    layouts): window token t's K/V sit in row kv_tail_end - W + t and query t
+    attends to rows [0, pos) and then to those rows (the reference's
+    StaticKV tail, model.py:259-461).
     """
     from .codec import tile_kv
 
@@ -140,13 +145,15 @@ def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Te
     B, Hkv, max_len, hd = k.shape
     if v.shape != k.shape or v.dtype != k.dtype or not (k.is_contiguous() and v.is_contiguous()):
         raise ValueError("k and v must be contiguous with equal shape/dtype")
-    if k.dtype == torch.bfloat16 and not tiled:
+    if k.dtype == torch.bfloat16 and not tiled and not natural:
         k = tile_kv(k, "k").contiguous()
         v = tile_kv(v, "v").contiguous()
     H = q.shape[1]
     a = _lib.AttnArgs()
     a.B, a.W, a.H, a.Hkv, a.head_dim, a.max_len = B, W, H, Hkv, hd, max_len
-    a.kv_bf16 = int(k.dtype == torch.bfloat16)
+    a.kv_bf16 = (_lib.KV_F32 if k.dtype != torch.bfloat16 else
+                 _lib.KV_BF16_NATURAL if natural else _lib.KV_BF16)
+    a.kv_tail_end = int(kv_tail_end)
     a.y_bf16 = int(y_bf16)
     a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
     a.kv_seg_stride = Hkv * max_len * hd

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define ALTXS_ABI_VERSION 5
+#define ALTXS_ABI_VERSION 6
 
 enum {
   ALTXS_OK = 0,
@@ -72,6 +72,11 @@ typedef struct AltxsQTensor {
 int32_t altxs_scale_cum(const float *probs, int64_t rows, int64_t V, uint32_t *cum,
                         altxs_stream_t stream);
 
+/* The same tables from float64 probabilities (the reference's _scale_cum_np
+ * converts its input to float64, arithmetic_coder_lm.py:58-60). */
+int32_t altxs_scale_cum_f64(const double *probs, int64_t rows, int64_t V, uint32_t *cum,
+                            altxs_stream_t stream);
+
 #define ALTXS_CDF_RENORM 1 /* p /= sum(p) after the softmax (compress.py:78-83) */
 
 /*
@@ -114,18 +119,29 @@ int32_t altxs_qgemm_stream(const AltxsQTensor *w, int64_t count, int64_t codes_s
  * y[rows, N] = (RMSNorm(x[rows, K]) * ln_scale) . W^T: the step's normalised
  * prologue (x fp32, eps added to the mean square, one fixed reduction order
  * per row) in front of the dequant GEMM; bits in {2,3,4,6,16}, K in {256,
- * 512}.  act_bf16 = 1 rounds the normalised row to bf16 for the MFMAs (the
- * reference's bf16 path), 0 keeps it fp32-faithful.  Replaces
- * logits_stage_rows(src, weight, logit_buf) (src/xsa_ttt/ac_gemv.py:562-582).
+ * 512}.  act_bf16 holds rounding flags: ALTXS_RMS_ROUND_ROW rounds the
+ * normalised row to bf16 for the MFMAs (a bf16 weight, the reference's
+ * `.to(W.dtype)`), ALTXS_RMS_ROUND_SCALE first rounds the rsqrt factor to
+ * bf16 (a bf16 source row: the reference's `.to(src.dtype)` of the scale);
+ * 0 keeps the row fp32-faithful.  Replaces logits_stage_rows(src, weight,
+ * logit_buf) (src/xsa_ttt/ac_gemv.py:312-359, 562-582).
  */
+#define ALTXS_RMS_ROUND_ROW 1
+#define ALTXS_RMS_ROUND_SCALE 2
 int32_t altxs_rms_qgemm(const AltxsQTensor *w, const float *x, int64_t rows, float ln_scale,
                         float eps, int32_t act_bf16, float *y, altxs_stream_t stream);
 
 /*
  * KV cache layout.  Per (segment, kv head) the cache holds max_len keys of
- * head_dim = 64 in 64-key tiles (ALTXS_KV_TILE); max_len % 64 == 0.
- *   fp32 cache: natural order, element (key, d) at key*64 + d.
- *   bf16 cache: each 4096-element tile is stored in MFMA operand order so one
+ * head_dim = 64 in 64-key tiles (ALTXS_KV_TILE); max_len % 64 == 0.  The
+ * kv_bf16 field of the descriptors selects one of three layouts:
+ *   ALTXS_KV_F32 (0), fp32 cache: natural order, element (key, d) at key*64 + d.
+ *   ALTXS_KV_BF16_NATURAL (2), bf16 cache in the same natural order: the
+ *   reference's own packed layout k_pack[slot][kv_head][max_len][head_dim]
+ *   (src/xsa_ttt/persistent_step.py:472-479), so a reference StaticKV can be a
+ *   view of it.  Attention reads it with the VALU kernel (fp32 products of
+ *   the bf16 values).
+ *   ALTXS_KV_BF16 (1), bf16 cache: each 4096-element tile is stored in MFMA operand order so one
  *   16-byte load per lane feeds v_mfma_f32_16x16x32_bf16.  For key kt = key % 64
  *   of tile key / 64 and dim d (tile base + offset):
  *     K: ((((kt>>4)*2 + (d>>5))*4 + ((d>>3)&3))*16 + (kt&15))*8 + (d&7)
@@ -134,6 +150,20 @@ int32_t altxs_rms_qgemm(const AltxsQTensor *w, const float *x, int64_t rows, flo
  *   altxs_amd.codec.tile_kv() converts a natural [.., max_len, 64] tensor.
  */
 #define ALTXS_KV_TILE 64
+enum { ALTXS_KV_F32 = 0, ALTXS_KV_BF16 = 1, ALTXS_KV_BF16_NATURAL = 2 };
+
+/*
+ * Tail placement (kv_tail_end > 0, natural layouts only): the reference's
+ * StaticState keeps a W-token window's K/V in the last W rows of its buffers
+ * and commits them into the prefix afterwards (src/xsa_ttt/model.py:259-461:
+ * StaticKV, commit_window; run_split_attn's tail_at_pos = False,
+ * split_attn.py:341-425).  With kv_tail_end = E the window's token t has its
+ * K/V in row E - W + t; query row t at position p = pos + t attends to the
+ * prefix rows [0, pos) and then the window rows E - W .. E - W + t, in that
+ * key order (the order of keys 0 .. p, so a committed row gives the same
+ * result).  pos must not exceed E - W (flagged as ALTXS_EDEV_POS).
+ * kv_tail_end = 0: the window's K/V sit at their own positions pos + t.
+ */
 
 /* AltxsAttnArgs.flags */
 #define ALTXS_ATTN_OPS_BF16 1 /* bf16 cache: round q and the softmax weights to
@@ -163,7 +193,7 @@ int32_t altxs_rms_qgemm(const AltxsQTensor *w, const float *x, int64_t rows, flo
  */
 typedef struct AltxsAttnArgs {
   int32_t B, W, H, Hkv, head_dim, max_len;
-  int32_t kv_bf16;  /* KV element type: 0 fp32, 1 bf16 */
+  int32_t kv_bf16;  /* KV layout: ALTXS_KV_F32, ALTXS_KV_BF16 or ALTXS_KV_BF16_NATURAL */
   int32_t y_bf16;   /* output element type: 0 fp32, 1 bf16 */
   const float *q;   /* [B*W, H, head_dim] fp32 */
   const void *k;    /* [B, Hkv, max_len, head_dim] in the cache layout above,
@@ -174,6 +204,8 @@ typedef struct AltxsAttnArgs {
   const float *gate;     /* [B*W, H] multiplier (sparse attention gate) or NULL */
   int32_t use_xsa;       /* subtract the current value direction (model.py:760-768) */
   int32_t flags;         /* ALTXS_ATTN_* */
+  int32_t kv_tail_end;   /* 0, or tail placement (above; natural layouts) */
+  int32_t reserved;
   void *y;               /* [B*W, H*head_dim] */
   int32_t *err;          /* device error word or NULL */
 } AltxsAttnArgs;
@@ -237,7 +269,9 @@ typedef struct AltxsStepDesc {
   int32_t B, W, D, H, Hkv, head_dim, F, V;
   int32_t n_layers, n_slots, max_len, gate_window, rope_dims, lora_rank;
   int32_t act_bf16; /* 0: fp32 activations (3-way split MFMA), 1: bf16 */
-  int32_t kv_bf16;  /* 0: fp32 KV cache, 1: bf16 */
+  int32_t kv_bf16;  /* KV layout: ALTXS_KV_F32, ALTXS_KV_BF16 or ALTXS_KV_BF16_NATURAL */
+  int32_t kv_tail_end; /* 0, or tail placement of the window's K/V (above; natural
+                          layouts, per-stage launches only) */
   int32_t flags;    /* ALTXS_F_* */
   float norm_eps, gate_scale, logit_softcap;
   AltxsLayer layers[ALTXS_MAX_LAYERS];
@@ -310,7 +344,8 @@ int32_t altxs_step_plan_build(const AltxsStepDesc *d, void *plan_host, void *pla
  * One W-token step for B independent segments: embedding (+smear), every slot
  * (QKV + QK-RMS + RoPE + KV write, attention, out-projection + residual,
  * RMSNorm/MLP), final norm, LM head + softcap, softmax and integer CDFs.
- * K/V rows are written at pos[b] + t.  W = 1 is the decode row; W > 1 is the
+ * K/V rows are written at pos[b] + t (or in the tail rows, kv_tail_end).
+ * W = 1 is the decode row; W > 1 is the
  * teacher-forced encode window; per-row results are identical for the same
  * prefix.  Replaces try_persistent_extend(model, state)
  * (src/xsa_ttt/persistent_step.py:1081), try_mega_encode(model, state)

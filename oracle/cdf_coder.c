@@ -10,6 +10,7 @@
  *   oracle_scale_cum   <- _scale_cum_np      src/model/arithmetic_coder_lm.py:49-64
  *                         f_i = max(1, floor(double(p_i) * 1e6 + 0.5)), C_0 = 0,
  *                         C_{i+1} = C_i + f_i, total = C_V.
+ *   oracle_scale_cum_f64  the same on float64 rows
  *   oracle_wnc_encode  <- encode_with_probs  src/model/arithmetic_coder_lm.py:140-195
  *                         (+ _renorm_encode 90-112, _pack_bits 115-128)
  *   oracle_wnc_decode  <- decode_with_probs  src/model/arithmetic_coder_lm.py:198-288
@@ -49,6 +50,29 @@ void oracle_scale_cum_rows(const float *probs, int64_t rows, int64_t V,
                            int64_t *cum) {
   for (int64_t r = 0; r < rows; ++r)
     oracle_scale_cum(probs + r * V, V, cum + r * (V + 1));
+}
+
+/* The same rule on float64 probabilities (the reference converts its input
+ * to float64 first, arithmetic_coder_lm.py:58-60).  Here the two double
+ * roundings are not exact in general. */
+int64_t oracle_scale_cum_f64(const double *probs, int64_t V, int64_t *cum) {
+  int64_t acc = 0;
+  cum[0] = 0;
+  for (int64_t i = 0; i < V; ++i) {
+    double t = probs[i] * 1000000.0;
+    t = t + 0.5;
+    double f = floor(t);
+    int64_t v = (f >= 1.0) ? (int64_t)f : 1; /* np.maximum(1, ...); NaN -> 1 */
+    acc += v;
+    cum[i + 1] = acc;
+  }
+  return acc;
+}
+
+void oracle_scale_cum_rows_f64(const double *probs, int64_t rows, int64_t V,
+                               int64_t *cum) {
+  for (int64_t r = 0; r < rows; ++r)
+    oracle_scale_cum_f64(probs + r * V, V, cum + r * (V + 1));
 }
 
 typedef struct {

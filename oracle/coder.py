@@ -4,7 +4,9 @@
   Pinned by closed-form known answers (uniform rows: V=256 -> f=3906,
   total 999,936; V=4096 -> 244, 999,424; V=16384 -> 61, 999,424; p=0 -> 1),
   by exact-rational brute force around every rounding boundary (tests), and by
-  numpy's own evaluation of the same expression.
+  numpy's own evaluation of the same expression.  :func:`scale_cum_f64`
+  is the rule on float64 rows, pinned by exact-rational emulation of its two
+  double roundings around every boundary and by numpy's float64 evaluation.
 * :func:`wnc_encode` / :func:`wnc_decode` restate ``encode_with_probs`` /
   ``decode_with_probs`` (arithmetic_coder_lm.py:140-288).  Pinned by
   round-trip identity and by byte equality with bitstreams written by the
@@ -41,6 +43,8 @@ def lib():
         L.oracle_scale_cum.argtypes = [p, i64, p]
         L.oracle_scale_cum_rows.restype = None
         L.oracle_scale_cum_rows.argtypes = [p, i64, i64, p]
+        L.oracle_scale_cum_rows_f64.restype = None
+        L.oracle_scale_cum_rows_f64.argtypes = [p, i64, i64, p]
         L.oracle_wnc_encode.restype = i64
         L.oracle_wnc_encode.argtypes = [p, i64, p, i64, p, i64]
         L.oracle_wnc_decode.restype = ctypes.c_int
@@ -60,6 +64,16 @@ def scale_cum(probs: np.ndarray) -> np.ndarray:
     rows = p.reshape(-1, V)
     out = np.empty((rows.shape[0], V + 1), dtype=np.int64)
     lib().oracle_scale_cum_rows(_ptr(rows), rows.shape[0], V, _ptr(out))
+    return out.reshape(p.shape[:-1] + (V + 1,))
+
+
+def scale_cum_f64(probs: np.ndarray) -> np.ndarray:
+    """probs float64 [..., V] -> cum int64 [..., V+1] (the rule on float64 rows)."""
+    p = np.ascontiguousarray(probs, dtype=np.float64)
+    V = p.shape[-1]
+    rows = p.reshape(-1, V)
+    out = np.empty((rows.shape[0], V + 1), dtype=np.int64)
+    lib().oracle_scale_cum_rows_f64(_ptr(rows), rows.shape[0], V, _ptr(out))
     return out.reshape(p.shape[:-1] + (V + 1,))
 
 

@@ -69,6 +69,36 @@ def test_rounding_boundaries_exact():
     assert not np.array_equal(_float32_rule(p), want)
 
 
+def test_f64_rule_rounding_boundaries():
+    """float64 rows: doubles within +-8 ULP of (k - 1/2) * 1e-6 and of the
+    doubles whose product lands on a half, against exact rationals of the two
+    double roundings (which are not exact here, unlike float32 input)."""
+    ks = list(range(1, 3000)) + list(range(10_000, 1_000_001, 7919))
+    vals = []
+    for k in ks:
+        for base in ((k - 0.5) * 1e-6, (k - 0.5) / 1e6):
+            v = np.float64(base)
+            for _ in range(8):
+                v = np.nextafter(v, 0.0)
+            for _ in range(17):
+                vals.append(float(v))
+                v = np.nextafter(v, 1.0)
+    p = np.array(vals, np.float64)
+    got = np.diff(coder.scale_cum_f64(p[None])[0])
+    want = np.array([_two_round(x) for x in vals], np.int64)
+    assert np.array_equal(got, want)
+    # numpy's own evaluation of the reference expression
+    assert np.array_equal(got, np.maximum(1, np.floor(p * 1_000_000.0 + 0.5).astype(np.int64)))
+    # where the double roundings matter, the closed form differs (the check can fail)
+    assert any(_two_round(x) != _exact(x) for x in vals)
+
+
+def test_f64_rule_equals_f32_rule_on_float32_values():
+    rng = np.random.default_rng(5)
+    p = (rng.random((3, 4096)) ** 3).astype(np.float32)
+    assert np.array_equal(coder.scale_cum_f64(p.astype(np.float64)), coder.scale_cum(p))
+
+
 def test_matches_reference_tables(golden_dir):
     g = np.load(os.path.join(golden_dir, "coder_ref.npz"))
     assert np.array_equal(coder.scale_cum(g["a_rows"]), g["a_cum"])

@@ -7,7 +7,8 @@ row is ``_softmax_np`` (fp32 softmax, then ``p /= p.sum()``, compress.py:
 stream start; later rows are the softmax of each window's logits.  The
 fixture tests/golden/engine_rows.npz holds rows the reference's own
 ``StaticACEngine`` produced on its CPU path ("tiny" weights, W=16, block 64,
-retrain every 64, so the engine's static length -- and RoPE table -- is 128).
+retrain every 64, so the engine's static length -- and RoPE table -- is 128);
+engine_rows_bf16w.npz the same with the weight matrices rounded to bf16.
 """
 
 from __future__ import annotations
@@ -21,6 +22,8 @@ import torch
 from altxs_amd import synth
 from altxs_amd.config import make_config
 from oracle import model_ref as mr
+
+from .refshape import bf16_banks
 
 
 @pytest.fixture(scope="module")
@@ -37,15 +40,26 @@ def test_engine_length_rule(eng):
     assert mr.engine_max_len(64, 100, 16) == 64 + 112
 
 
+@pytest.mark.parametrize("fixture", ["engine_rows.npz", "engine_rows_bf16w.npz"])
 @pytest.mark.parametrize("key,start", [("rows_start", 0), ("rows_ctx", 100)])
-def test_segment_rows_match_reference_engine(eng, key, start):
-    z, cfg, sm = eng
+def test_segment_rows_match_reference_engine(eng, golden_dir, fixture, key, start):
+    _, cfg, sm = eng
+    z = np.load(os.path.join(golden_dir, fixture))
     block, win = int(z["block"]), int(z["win"])
-    om = mr.OracleModel(cfg, sm.state_dict(), max_len=int(z["max_len"]))
+    sd = sm.state_dict() if fixture == "engine_rows.npz" else bf16_banks(sm.state_dict())
+    om = mr.OracleModel(cfg, sd, max_len=int(z["max_len"]))
     rows = mr.segment_rows_tf(om, z["arr"], z["arr"][start:start + 64], start, block, win)
     assert np.abs(rows - z[key]).max() < 1e-6
     if start == 0:
         assert np.array_equal(rows[0], np.full(cfg.vocab_size, 1.0 / cfg.vocab_size, np.float32))
+
+
+def test_bf16_bank_fixture_differs_from_fp32_weights(golden_dir):
+    """The two fixtures are different models: rounding the banks to bf16 moves
+    the reference's rows well past the 1e-6 above."""
+    a = np.load(os.path.join(golden_dir, "engine_rows.npz"))["rows_ctx"]
+    b = np.load(os.path.join(golden_dir, "engine_rows_bf16w.npz"))["rows_ctx"]
+    assert np.abs(a - b).max() > 1e-4
 
 
 def test_rope_length_matters(eng):
