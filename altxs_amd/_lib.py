@@ -60,6 +60,7 @@ EXPORTS = (
     "altxs_range_decode",
     "altxs_codec_decode",
     "altxs_pack_dense",
+    "altxs_pack_dense32",
 )
 
 
@@ -195,6 +196,8 @@ def load():
     L.altxs_codec_decode.argtypes = [ctypes.POINTER(CodecGroups), p, p, i64, i64, p, i64, i64, p, p]
     L.altxs_pack_dense.restype = i32
     L.altxs_pack_dense.argtypes = [p, p, i64, i64, i64, p, p]
+    L.altxs_pack_dense32.restype = i32
+    L.altxs_pack_dense32.argtypes = [p, p, i64, i64, i64, p, i64, p]
     v = L.altxs_abi_version()
     if v != ABI_VERSION:
         raise AltxsLibraryError(f"{path}: ABI version {v} != {ABI_VERSION}")

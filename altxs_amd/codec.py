@@ -146,6 +146,30 @@ def pack_dense_tiled(w: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(vals).astype("<u2").view(np.uint8).reshape(-1)
 
 
+def split3_bf16(w: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """fp32 -> three bf16 bit patterns hi, mid, lo with hi + mid + lo == w
+    exactly: hi = bf16(w), mid = bf16(w - hi), lo = bf16(w - hi - mid), where
+    both differences are exact in fp32 and the last one is a bf16 value."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    hi = bf16_bits(w)
+    r1 = w - (hi.astype(np.uint32) << np.uint32(16)).view(np.float32)
+    mid = bf16_bits(r1)
+    r2 = r1 - (mid.astype(np.uint32) << np.uint32(16)).view(np.float32)
+    return hi, mid, bf16_bits(r2)
+
+
+def pack_dense32_tiled(w: np.ndarray) -> np.ndarray:
+    """fp32 [N, K] -> the dense bits-32 bytes: per 16 x 256 block the tiled
+    bytes of the hi, mid and lo planes one after the other."""
+    n, k = w.shape
+    if n % BLOCK_N or k % BLOCK_K:
+        raise ValueError(f"tensor [{n}, {k}] must be a multiple of [{BLOCK_N}, {BLOCK_K}]")
+    order = _lane_order(n, k)  # [blk, lane, 64]
+    planes = [np.ascontiguousarray(p.reshape(-1)[order]).astype("<u2").view(np.uint8).reshape(order.shape[0], -1)
+              for p in split3_bf16(w)]
+    return np.ascontiguousarray(np.stack(planes, axis=1)).reshape(-1)
+
+
 def unpack_dense_tiled(packed: np.ndarray, n: int, k: int) -> np.ndarray:
     """Inverse of :func:`pack_dense_tiled`: fp32 [N, K] of the bf16 values."""
     vals = np.ascontiguousarray(packed, dtype=np.uint8).view("<u2").astype(np.uint32)
@@ -200,6 +224,8 @@ class PackedTensor:
     def dense(self) -> np.ndarray:
         if self.bits == 16:  # codes hold the bf16 bit patterns
             return (self.codes.astype(np.uint32) << np.uint32(16)).view(np.float32)
+        if self.bits == 32:  # codes hold the fp32 bit patterns
+            return self.codes.astype(np.uint32).view(np.float32).copy()
         return dequantize_group64(self.codes, self.scales, self.bits)
 
     @classmethod
@@ -208,6 +234,11 @@ class PackedTensor:
             n = w.shape[0]
             return cls(name, 16, bf16_bits(w), np.zeros((n, 0), np.float16), pack_dense_tiled(w),
                        np.zeros(0, np.float16))
+        if bits == 32:  # dense fp32 weights as three exact bf16 planes
+            n = w.shape[0]
+            w = np.ascontiguousarray(w, dtype=np.float32)
+            return cls(name, 32, w.view(np.uint32).copy(), np.zeros((n, 0), np.float16),
+                       pack_dense32_tiled(w), np.zeros(0, np.float16))
         codes, scales = quantize_group64(w, bits)
         tiled, tsc = pack_tiled(codes, scales, bits)
         return cls(name, bits, codes, scales, tiled, tsc)

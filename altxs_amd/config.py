@@ -34,6 +34,7 @@ class AltxsConfig:
     num_kv_heads: int = 4
     mlp_mult: float = 4.0
     tie_embeddings: bool = True
+    tied_embed_init_std: float = 0.005  # Init(seed) only (model.py:1139-1141)
     logit_softcap: float = 30.0
     asym_logit_rescale: bool = True
     rope_base: float = 1e4
@@ -51,6 +52,7 @@ class AltxsConfig:
     gate_window: int = 12
     sparse_attn_gate_enabled: bool = True
     sparse_attn_gate_scale: float = 0.5
+    sparse_attn_gate_init_std: float = 0.0  # Init(seed) only (model.py:750-756)
     attn_out_gate_enabled: bool = False
     gated_attn_enabled: bool = False
     block_size: int = 2048  # RoPE train_seq_len (model.py:1023)

@@ -114,6 +114,50 @@ __global__ __launch_bounds__(256) void pack_dense_kernel(const float* base, cons
   dst[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
 }
 
+// The same blocks for fp32 weights (bits 32): three bf16 planes hi, mid, lo of
+// w = base + delta (hi = bf16(w), mid = bf16(w - hi), lo = bf16(w - hi - mid)
+// = w - hi - mid exactly), plane p of block blk at (3 * blk + p) * 8192.
+__global__ __launch_bounds__(256) void pack_dense32_kernel(const float* base, const float* delta,
+                                                           int64_t K, int64_t ld, uint8_t* tiled) {
+  const int64_t KB = K >> 8;
+  const int64_t blk = blockIdx.x;
+  const int64_t nb = blk / KB, kb = blk % KB;
+  const int lane = threadIdx.x >> 2, sp = threadIdx.x & 3;
+  const int64_t row = nb * 16 + (lane & 15);
+  uint32_t wv[3][8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int s = 2 * sp + h;
+    const int64_t col = kb * 256 + 32 * s + 8 * (lane >> 4);
+    const float* d = delta + row * ld + col;
+    const float* bs = base ? base + row * ld + col : nullptr;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint16_t part[3][2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float x = d[2 * q + e];
+        if (bs) x = bs[2 * q + e] + x;
+        const uint16_t hi = f32_to_bf16(x);
+        const float r1 = x - bf16_to_f32(hi);
+        const uint16_t mid = f32_to_bf16(r1);
+        const float r2 = r1 - bf16_to_f32(mid);
+        part[0][e] = hi;
+        part[1][e] = mid;
+        part[2][e] = f32_to_bf16(r2);
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p) wv[p][4 * h + q] = (uint32_t)part[p][0] | ((uint32_t)part[p][1] << 16);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    u32x4* dst = (u32x4*)(tiled + (blk * 3 + p) * 8192 + lane * 128 + sp * 32);
+    dst[0] = u32x4{wv[p][0], wv[p][1], wv[p][2], wv[p][3]};
+    dst[1] = u32x4{wv[p][4], wv[p][5], wv[p][6], wv[p][7]};
+  }
+}
+
 }  // namespace
 
 extern "C" int32_t altxs_codec_decode(const AltxsCodecGroups* g, const uint8_t* bits,
@@ -135,6 +179,24 @@ extern "C" int32_t altxs_codec_decode(const AltxsCodecGroups* g, const uint8_t* 
   a.stride_ch = stride_ch; a.stride_el = stride_el; a.out = out; a.err = err;
   hipLaunchKernelGGL(decode_kernel, dim3((unsigned)((width + 255) / 256), (unsigned)n_channels),
                      dim3(256), 0, (hipStream_t)stream, a);
+  ALTXS_CHECK_HIP(hipGetLastError());
+  return ALTXS_OK;
+}
+
+extern "C" int32_t altxs_pack_dense32(const float* base, const float* delta, int64_t N, int64_t K,
+                                      int64_t ld, void* tiled, int64_t tiled_bytes,
+                                      altxs_stream_t stream) {
+  ALTXS_REQUIRE(delta && tiled, "altxs_pack_dense32: null pointer");
+  ALTXS_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0 && ld >= K && ld % 2 == 0,
+                "altxs_pack_dense32: N=%lld K=%lld ld=%lld", (long long)N, (long long)K,
+                (long long)ld);
+  ALTXS_REQUIRE(tiled_bytes >= N * K * 6, "altxs_pack_dense32: tiled holds %lld bytes, %lld needed",
+                (long long)tiled_bytes, (long long)(N * K * 6));
+  ALTXS_REQUIRE(((uintptr_t)tiled & 15) == 0 && ((uintptr_t)delta & 7) == 0 &&
+                    ((uintptr_t)base & 7) == 0,
+                "altxs_pack_dense32: misaligned");
+  hipLaunchKernelGGL(pack_dense32_kernel, dim3((unsigned)(N / 16 * (K / 256))), dim3(256), 0,
+                     (hipStream_t)stream, base, delta, K, ld, (uint8_t*)tiled);
   ALTXS_CHECK_HIP(hipGetLastError());
   return ALTXS_OK;
 }

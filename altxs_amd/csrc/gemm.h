@@ -50,6 +50,15 @@ template <> struct Planes<6> { static constexpr int P0 = 4, P1 = 2; };
 // BITS == 16: dense bf16 weights in the same tiled order (no codes, no scales):
 // a lane's 64 values of a block are 32 words, k-step s in words 4s..4s+3.
 template <> struct Planes<16> { static constexpr int P0 = 16, P1 = 0; };
+// BITS == 32: dense fp32 weights as three bf16 planes w = hi + mid + lo
+// (hi = bf16(w), mid = bf16(w - hi), lo = w - hi - mid, which is a bf16 value:
+// the split is exact), each plane a bits-16 block, the three planes of a
+// block stored one after the other.  The GEMM walks *virtual* blocks
+// v = 3 * kb + plane: one plane in registers at a time, the A slice of block
+// kb applied to each.
+template <> struct Planes<32> { static constexpr int P0 = 16, P1 = 0; };
+// virtual blocks per 16 x 256 block of weights
+template <int BITS> __host__ __device__ constexpr int vpb() { return BITS == 32 ? 3 : 1; }
 
 // A-operand modes
 enum AMode : int { A_F32 = 0, A_BF16 = 1, A_F16 = 2 };
@@ -142,7 +151,8 @@ __device__ __forceinline__ void planes_to6(int bits, uint32_t (&p0)[8], uint32_t
 template <int BITS>
 __device__ __forceinline__ float code_center(int bits) {
   if constexpr (BITS == 0) return 0.5f * (float)((1 << bits) - 1);
-  else return 0.5f * (float)((1 << BITS) - 1);
+  else if constexpr (BITS <= 8) return 0.5f * (float)((1 << BITS) - 1);
+  else return 0.f;  // dense widths carry values, not codes
 }
 
 // 2- and 3-bit codes by table: every value c - center is exact in bf16, so a
@@ -201,7 +211,7 @@ __device__ __forceinline__ float ubyte_f32(uint32_t x) {
 // (planes_to6 already applied).
 template <int BITS>
 __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
-  if constexpr (BITS == 16)
+  if constexpr (BITS == 16 || BITS == 32)
     return __builtin_bit_cast(bf16x8, u32x4{p0[4 * s], p0[4 * s + 1], p0[4 * s + 2], p0[4 * s + 3]});
   if constexpr (BITS == 2 || BITS == 3) {
     static_assert(Planes<BITS>::P0 == 2, "2-bit low plane: k-step s is bits 16 (s & 1) + 2i of p0[s >> 1]");
@@ -303,13 +313,24 @@ struct ADirect {
   int64_t batch_stride;  // elements
 };
 
-// Weight codes + scales of block (nb, kb) for this lane.
+// Weight codes + scales of block (nb, kb) for this lane (BITS == 32: kb is the
+// virtual block 3 * block + plane).
 template <int BITS, int AM, bool ADIRECT>
 __device__ __forceinline__ void load_w(Blk<BITS, AM, ADIRECT>& b, const QT& w, int nb, int kb,
                                        int lane) {
   const int KB = w.K >> 8;
   const size_t bi = (size_t)nb * KB + kb;
-  if constexpr (BITS == 0) {
+  if constexpr (BITS == 32) {
+    const size_t plane = (size_t)(nb * KB) * 3 + kb;  // (block, plane) in storage order
+    const u32x4* a0 = (const u32x4*)(w.codes + plane * (512 * 16)) + lane * 8;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const u32x4 x = a0[v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b.p0[4 * v + i] = x[i];
+    }
+    b.sc[0] = b.sc[1] = 0u;
+  } else if constexpr (BITS == 0) {
     // every element is defined on every path (whole-vector phis), so the block
     // stays in registers; the branches are on the uniform width only
     const int nbits = w.bits;
@@ -393,11 +414,12 @@ __device__ __forceinline__ void load_a(Blk<BITS, AM, ADIRECT>& b, const QT& w, i
   }
 }
 
+// Virtual block kb (= the weight block for every width but 32).
 template <int BITS, int AM, bool ADIRECT>
 __device__ __forceinline__ void load_blk(Blk<BITS, AM, ADIRECT>& b, const QT& w, int nb, int kb,
                                          int lane, const ADirect& ad, int m0, int R, int batch) {
   load_w(b, w, nb, kb, lane);
-  load_a(b, w, kb, lane, ad, m0, R, batch);
+  load_a(b, w, kb / vpb<BITS>(), lane, ad, m0, R, batch);
 }
 
 // Dependency hook of a task: runs after the first tile's weight loads are
@@ -428,12 +450,14 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8& a0, bf16x8& 
   }
 }
 
-// acc += W-block . A-slice (one 16x256 block, 8 MFMA k-steps).
+// acc += W-block . A-slice (one 16x256 block, 8 MFMA k-steps; BITS == 32: one
+// plane of virtual block vb, applied to the A slice of block vb / 3).
 template <int BITS, int AM, bool ADIRECT>
 __device__ __forceinline__ void compute_blk(const Blk<BITS, AM, ADIRECT>& b, const void* As, int K,
-                                            int kb, int lane, f32x4& acc, int bits = BITS) {
+                                            int vb, int lane, f32x4& acc, int bits = BITS) {
+  const int kb = vb / vpb<BITS>();
   float scale[4] = {half_lo(b.sc[0]), half_hi(b.sc[0]), half_lo(b.sc[1]), half_hi(b.sc[1])};
-  if constexpr (BITS == 16) scale[0] = scale[1] = scale[2] = scale[3] = 1.f;  // dense: acc += t
+  if constexpr (BITS == 16 || BITS == 32) scale[0] = scale[1] = scale[2] = scale[3] = 1.f;  // dense: acc += t
   const int row = lane & 15;
   constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
   uint32_t q0[2 * P0], q1[P1 > 0 ? 2 * P1 : 1];
@@ -522,7 +546,8 @@ __device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, i
   const int nbi = wave % NB, ks = wave / NB;
   const int ntiles = (w.N + Cfg::NCOL - 1) / Cfg::NCOL;
   const int KB = w.K >> 8;
-  const int kb0 = ks * (KB / KS), kb1 = kb0 + KB / KS;  // host guarantees KB % KS == 0
+  // virtual blocks (weight blocks, or planes of blocks for BITS == 32) of this K-slice
+  const int kb0 = ks * (KB / KS) * vpb<BITS>(), kb1 = kb0 + KB / KS * vpb<BITS>();  // host: KB % KS == 0
   void* As = smem;
   const size_t a_bytes = STAGE ? (size_t)16 * lds_stride(w.K, AM) * a_esz(AM) : 0;
   float* Cp = (float*)(smem + a_bytes);
@@ -539,8 +564,8 @@ __device__ __forceinline__ void gemm_task(const QT& w, int R, int m0, int nt0, i
   auto issue_a = [&](int nt) {
     if constexpr (ADIRECT) {
       if ((nt * NB + nbi) * 16 < w.N) {
-        if (kb0 < kb1) load_a(b0, w, kb0, lane, ad, m0, R, batch);
-        if (kb0 + 1 < kb1) load_a(b1, w, kb0 + 1, lane, ad, m0, R, batch);
+        if (kb0 < kb1) load_a(b0, w, kb0 / vpb<BITS>(), lane, ad, m0, R, batch);
+        if (kb0 + 1 < kb1) load_a(b1, w, (kb0 + 1) / vpb<BITS>(), lane, ad, m0, R, batch);
       }
     }
   };
@@ -682,6 +707,10 @@ hipError_t launch_gemm_bits(int bits, const QT& w, int R, int batch, int64_t cod
     case 16:
       if constexpr (AM != A_F16)
         return launch_gemm<16, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
+      return hipErrorInvalidValue;
+    case 32:  // fp32 dense weights: the fp32-activation path only
+      if constexpr (AM == A_F32)
+        return launch_gemm<32, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }

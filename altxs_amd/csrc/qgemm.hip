@@ -30,9 +30,10 @@ __global__ __launch_bounds__(64) void dequant_kernel(QT w, float* __restrict__ o
 }
 
 int check_qt(const AltxsQTensor* w, const char* who, bool dense_ok) {
-  ALTXS_REQUIRE(w && w->codes && (w->scales || w->bits == 16), "%s: null tensor", who);
-  ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6 || (dense_ok && w->bits == 16),
-                "%s: bits=%d not in {2,3,4,6%s}", who, w->bits, dense_ok ? ",16" : "");
+  ALTXS_REQUIRE(w && w->codes && (w->scales || w->bits == 16 || w->bits == 32), "%s: null tensor", who);
+  ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6 ||
+                    (dense_ok && (w->bits == 16 || w->bits == 32)),
+                "%s: bits=%d not in {2,3,4,6%s}", who, w->bits, dense_ok ? ",16,32" : "");
   ALTXS_REQUIRE(w->N > 0 && w->N % 16 == 0 && w->N < (1 << 24),
                 "%s: N=%lld must be a positive multiple of 16", who, (long long)w->N);
   ALTXS_REQUIRE(w->K > 0 && w->K % 256 == 0 && w->K <= 8192,
@@ -92,6 +93,7 @@ int32_t gemm_common(const AltxsQTensor* w, int64_t count, int64_t cs, int64_t ss
   if (rc) return rc;
   ALTXS_REQUIRE(x && y, "%s: null x/y", who);
   ALTXS_REQUIRE(w->bits != 16 || xdt != ALTXS_F16, "%s: dense bf16 weights take fp32 or bf16 x", who);
+  ALTXS_REQUIRE(w->bits != 32 || xdt == ALTXS_F32, "%s: dense fp32 weights take fp32 x", who);
   ALTXS_REQUIRE(((uintptr_t)x & 15) == 0, "%s: x must be 16-byte aligned", who);
   ALTXS_REQUIRE(rows >= 1 && rows <= (1 << 20), "%s: rows=%lld out of range", who, (long long)rows);
   ALTXS_REQUIRE(count >= 1 && count <= 65535, "%s: count=%lld out of range", who, (long long)count);

@@ -150,13 +150,15 @@ QT qt_of(const AltxsQTensor& t) {
   return q;
 }
 
-int check_tensor(const AltxsQTensor& t, int64_t N, int64_t K, const char* what, int li) {
-  const bool dense = t.bits == 16;  // bf16 values in the tiled order, no scales
+int check_tensor(const AltxsQTensor& t, int64_t N, int64_t K, const char* what, int li, int act_bf16) {
+  const bool dense = t.bits == 16 || t.bits == 32;  // bf16 / fp32 values in the tiled order, no scales
   ALTXS_REQUIRE(t.codes && (dense || t.scales), "altxs_step: layer %d %s: null tensor", li, what);
   ALTXS_REQUIRE(t.N == N && t.K == K, "altxs_step: layer %d %s: shape [%lld,%lld] != [%lld,%lld]",
                 li, what, (long long)t.N, (long long)t.K, (long long)N, (long long)K);
   ALTXS_REQUIRE(t.bits == 2 || t.bits == 3 || t.bits == 4 || t.bits == 6 || dense,
                 "altxs_step: layer %d %s: bits=%d", li, what, t.bits);
+  ALTXS_REQUIRE(t.bits != 32 || !act_bf16, "altxs_step: layer %d %s: fp32 weights (bits 32) need "
+                "fp32 activations", li, what);
   ALTXS_REQUIRE(((uintptr_t)t.codes & 15) == 0 && ((uintptr_t)t.scales & 7) == 0,
                 "altxs_step: layer %d %s: misaligned", li, what);
   return ALTXS_OK;
@@ -204,10 +206,10 @@ int validate(const AltxsStepDesc* d) {
   for (int l = 0; l < d->n_layers; ++l) {
     const AltxsLayer& L = d->layers[l];
     int rc;
-    if ((rc = check_tensor(L.qkv, d->D + 2 * kvd, d->D, "qkv", l))) return rc;
-    if ((rc = check_tensor(L.o, d->D, d->D, "o", l))) return rc;
-    if ((rc = check_tensor(L.up, d->F, d->D, "up", l))) return rc;
-    if ((rc = check_tensor(L.down, d->D, d->F, "down", l))) return rc;
+    if ((rc = check_tensor(L.qkv, d->D + 2 * kvd, d->D, "qkv", l, d->act_bf16))) return rc;
+    if ((rc = check_tensor(L.o, d->D, d->D, "o", l, d->act_bf16))) return rc;
+    if ((rc = check_tensor(L.up, d->F, d->D, "up", l, d->act_bf16))) return rc;
+    if ((rc = check_tensor(L.down, d->D, d->F, "down", l, d->act_bf16))) return rc;
     ALTXS_REQUIRE(L.resid_mix && L.attn_scale && L.mlp_scale && L.q_gain,
                   "altxs_step: layer %d small params missing", l);
     // read with 16-byte vector loads (embedding and strip epilogues)
@@ -219,7 +221,7 @@ int validate(const AltxsStepDesc* d) {
   ALTXS_REQUIRE((((uintptr_t)d->skip_weights | (uintptr_t)d->skip_gates) & 15) == 0,
                 "altxs_step: skip_weights / skip_gates must be 16-byte aligned");
   int rc;
-  if ((rc = check_tensor(d->emb, d->V, d->D, "emb", -1))) return rc;
+  if ((rc = check_tensor(d->emb, d->V, d->D, "emb", -1, d->act_bf16))) return rc;
   for (int s = 0; s < d->n_slots; ++s) {
     const AltxsSlot& S = d->slots[s];
     ALTXS_REQUIRE(S.layer >= 0 && S.layer < d->n_layers, "altxs_step: slot %d layer", s);
@@ -751,9 +753,11 @@ extern "C" int32_t altxs_rms_qgemm(const AltxsQTensor* w, const float* x, int64_
                                    float eps, int32_t act_bf16, float* y, altxs_stream_t stream) {
   ALTXS_REQUIRE((act_bf16 & ~(ALTXS_RMS_ROUND_ROW | ALTXS_RMS_ROUND_SCALE)) == 0,
                 "altxs_rms_qgemm: unknown rounding flags 0x%x", act_bf16);
-  ALTXS_REQUIRE(w && w->codes && (w->bits == 16 || w->scales), "altxs_rms_qgemm: null tensor");
-  ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6 || w->bits == 16,
+  ALTXS_REQUIRE(w && w->codes && (w->bits == 16 || w->bits == 32 || w->scales), "altxs_rms_qgemm: null tensor");
+  ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6 || w->bits == 16 || w->bits == 32,
                 "altxs_rms_qgemm: bits=%d", w->bits);
+  ALTXS_REQUIRE(w->bits != 32 || !(act_bf16 & ALTXS_RMS_ROUND_ROW),
+                "altxs_rms_qgemm: fp32 weights (bits 32) take an fp32 row");
   ALTXS_REQUIRE(w->N > 0 && w->N % 16 == 0 && w->N < (1 << 24), "altxs_rms_qgemm: N=%lld",
                 (long long)w->N);
   ALTXS_REQUIRE(w->K == 256 || w->K == 512, "altxs_rms_qgemm: K=%lld must be 256 or 512",

@@ -84,9 +84,27 @@ __device__ void dense_run(const QT& w, int n, int run, float (&out)[8]) {
   }
 }
 
+// Dense fp32 rows (bits 32): hi + mid + lo of the three bf16 planes (exact).
+__device__ void dense32_run(const QT& w, int n, int run, float (&out)[8]) {
+  const int KB = w.K >> 8;
+  const int k0 = 8 * run, kb = k0 >> 8, kk = k0 & 255;
+  const int s = kk >> 5, lg = (kk & 31) >> 3;
+  const int L = (n & 15) + 16 * lg;
+  const size_t plane0 = ((size_t)(n >> 4) * KB + kb) * 3;
+  u32x4 x[3];
+#pragma unroll
+  for (int p = 0; p < 3; ++p) x[p] = *((const u32x4*)(w.codes + (plane0 + p) * (512 * 16)) + L * 8 + s);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = (bf16_lo(x[0][i]) + bf16_lo(x[1][i])) + bf16_lo(x[2][i]);
+    out[2 * i + 1] = (bf16_hi(x[0][i]) + bf16_hi(x[1][i])) + bf16_hi(x[2][i]);
+  }
+}
+
 __device__ void dequant_run_bits(int bits, const QT& w, int n, int run, float (&out)[8]) {
   switch (bits) {
     case 16: dense_run(w, n, run, out); break;
+    case 32: dense32_run(w, n, run, out); break;
     case 2: dequant_run<2>(w, n, run, out); break;
     case 3: dequant_run<3>(w, n, run, out); break;
     case 4: dequant_run<4>(w, n, run, out); break;

@@ -26,7 +26,8 @@ library raises).
   ``k_pack`` / ``v_pack`` that ``_rebind_packed_kv`` and ``commit_packed_row``
   use); :func:`refresh_persistent_weights` / :func:`refresh_encode_weights`.
 * :func:`load_codec` <- ``load_codec(codec_path, *, device)``
-  (src/hyperflow_distillation/mixed_bit_delta.py:232-312).
+  (src/hyperflow_distillation/mixed_bit_delta.py:232-312), Init(seed)
+  included (altxs_amd.init_seed).
 * :func:`gemv_rows` / :func:`gemv_vec` / :func:`logits_stage_rows` <-
   src/xsa_ttt/ac_gemv.py:391-420, 562-582.
 
@@ -228,17 +229,18 @@ def config_from_reference(ref_cfg) -> AltxsConfig:
     return AltxsConfig(**{k: v for k, v in src.items() if k in fields})
 
 
-def dense_model_from_state(cfg: AltxsConfig, state: dict, device="cuda") -> SynthModel:
-    """A reference-named state dict -> this build's weights: every matrix as
-    bf16 in the MFMA-tiled order (bits 16, the reference's runtime banks,
-    model.py:1183-1245) packed on the device; small parameters as fp32."""
+def dense_model_from_state(cfg: AltxsConfig, state: dict, device="cuda", bits: int = 16) -> SynthModel:
+    """A reference-named state dict -> this build's weights: every matrix dense
+    in the MFMA-tiled order, packed on the device -- bits 16: bf16, the
+    reference's bf16 runtime banks (model.py:1183-1245); bits 32: the fp32
+    values its fp32 compute mode keeps -- small parameters as fp32."""
     from .shipped import MODELED, pack_dense, split_init, tensor_shapes
 
     init = split_init(cfg, {k: v for k, v in state.items() if k in MODELED}, device)
     packed = {}
     for name, (n, k) in tensor_shapes(cfg).items():
-        tiled = pack_dense(init[name].contiguous())
-        packed[name] = PackedTensor(name, 16, np.zeros((0, 0), np.uint16), np.zeros((0, 0), np.float16),
+        tiled = pack_dense(init[name].contiguous(), bits=bits)
+        packed[name] = PackedTensor(name, bits, np.zeros((0, 0), np.uint16), np.zeros((0, 0), np.float16),
                                     tiled, np.zeros(0, np.float16), nk=(n, k))
     small = {k: torch.as_tensor(v).detach().float().cpu().numpy() for k, v in state.items()
              if k not in MODELED}
@@ -311,31 +313,20 @@ class _KVWorkspace:
         state.cand_prev_raw.view(-1)[:self.d].copy_(st.cand_prev_raw.view(-1))
 
 
-def _bf16_exact(t: torch.Tensor) -> bool:
-    t = t.detach().float()
-    return bool(torch.equal(t, t.to(torch.bfloat16).float()))
-
-
 class _Adapter:
-    """Per reference model: the step model built from its weights."""
+    """Per reference model: the step model built from its weights -- bf16
+    banks and bf16 natural-order KV for a bf16 model; fp32 banks (bits 32) and
+    fp32 KV for an fp32 one, the dtypes the reference computes in
+    (model.py:1183-1196)."""
 
     def __init__(self, model, act: str):
-        from .shipped import MODELED
-
         self.cfg = config_from_reference(model.cfg)
         sd = model.state_dict()
-        if act == "fp32":
-            # the dense banks hold bf16 values: an fp32 model runs here only if
-            # its matrices are bf16 values (the reference keeps fp32 AC weights
-            # in that mode, model.py:1183-1196)
-            bad = [k for k, v in sd.items() if k in MODELED and torch.is_tensor(v) and not _bf16_exact(v)]
-            if bad:
-                raise ValueError(f"fp32 compute with weights that are not bf16 values ({bad[0]}, ...): "
-                                 "the dense banks here are bf16")
         dev = next((v.device for v in sd.values() if torch.is_tensor(v)), None)
         self.device = dev if dev is not None and dev.type == "cuda" else torch.device("cuda")
         self.act = act
-        self.step = StepModel(dense_model_from_state(self.cfg, sd, self.device),
+        bits = 16 if act == "bf16" else 32
+        self.step = StepModel(dense_model_from_state(self.cfg, sd, self.device, bits),
                               device=self.device, act=act, kv="bf16n" if act == "bf16" else "fp32")
 
 
@@ -432,21 +423,32 @@ def try_mega_encode(model, state) -> bool:
 
 
 # ---- shipped codec ------------------------------------------------------------------
-def load_codec(codec_path, *, device, init_state: dict, act: str = "bf16"):
-    """Decode a shipped codec into a step model: (StepModel, meta, small params).
+def load_codec(codec_path, *, device, init_state: dict | None = None, act: str | None = None):
+    """Decode a shipped codec into a step model: (StepModel, meta, small params)
+    (mixed_bit_delta.py:232-312).
 
-    The reference builds Init(seed) itself (``build_model`` after
-    ``enable_deterministic(seed)``, mixed_bit_delta.py:251-262); here it comes
-    in as that model's state dict (``init_state``), and the delta is decoded,
-    added and packed on the device (altxs_codec_decode, altxs_pack_dense)."""
+    Init(seed) is built here as the reference builds it (``enable_deterministic
+    (seed)`` + ``build_model``; :func:`altxs_amd.init_seed.reference_init_state`)
+    unless a state dict is passed in; the delta is decoded on the device, added
+    to Init and packed (altxs_codec_decode, altxs_pack_dense[32]).  ``act``:
+    "bf16" (bf16 banks, the reference's compute dtype with ``use_bf16``, its
+    production setting) or "fp32" (fp32 banks); default from the codec's cfg."""
     import json
 
-    from .shipped import load_shipped
+    from .init_seed import reference_init_state
+    from .shipped import config_from_meta, load_shipped
 
     path = str(codec_path)
     stem = path[:-len(".safetensors")] if path.endswith(".safetensors") else path
-    cfg, weights, small = load_shipped(stem, init_state, device=device)
     meta = json.load(open(stem + ".json", encoding="utf8"))
+    if act is None:
+        act = "bf16" if (meta.get("cfg") or {}).get("use_bf16", False) else "fp32"
+    if act not in ("bf16", "fp32"):
+        raise ValueError(act)
+    if init_state is None:
+        init_state = reference_init_state(config_from_meta(meta), int(meta["seed"]))
+    cfg, weights, small = load_shipped(stem, init_state, device=device,
+                                       bits=16 if act == "bf16" else 32)
     sm = SynthModel(cfg, weights, {k: np.asarray(v, np.float32) for k, v in small.items()})
     return StepModel(sm, device=device, act=act), meta, small
 
@@ -461,9 +463,9 @@ _TILED_MAX = 256
 
 
 def _tiled(weight: torch.Tensor) -> _lib.QTensor:
-    """Dense [N, K] weight -> bits-16 tiled copy, cached until the weight
-    changes in place (torch's version counter).  fp32 weights must hold bf16
-    values (the dense format is bf16)."""
+    """Dense [N, K] weight -> tiled copy (bits 16 for a bf16 weight, bits 32
+    for an fp32 one: its exact value), cached until the weight changes in
+    place (torch's version counter)."""
     from .shipped import pack_dense
 
     key = (weight.untyped_storage().data_ptr(), weight.storage_offset(), tuple(weight.shape),
@@ -476,11 +478,11 @@ def _tiled(weight: torch.Tensor) -> _lib.QTensor:
     n, k = weight.shape
     if n % 16 or k % 256:
         raise ValueError(f"weight [{n}, {k}]: N must be a multiple of 16 and K of 256")
-    if weight.dtype != torch.bfloat16 and not _bf16_exact(weight):
-        raise ValueError("the dense weight format is bf16: this fp32 weight holds values that are not "
-                         "bf16 values")
-    tiled = pack_dense(weight.detach().float().contiguous())
-    qt = _lib.QTensor(tiled.data_ptr(), tiled.data_ptr(), n, k, 16, 0)
+    if weight.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("weights must be bf16 or fp32")
+    bits = 16 if weight.dtype == torch.bfloat16 else 32
+    tiled = pack_dense(weight.detach().float().contiguous(), bits=bits)
+    qt = _lib.QTensor(tiled.data_ptr(), tiled.data_ptr(), n, k, bits, 0)
     _TILED[key] = (ver, weight.untyped_storage(), tiled, qt)
     _TILED.move_to_end(key)
     while len(_TILED) > _TILED_MAX:
@@ -502,6 +504,8 @@ def gemv_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -> None:
     if x.dtype not in _DT or not x.is_contiguous():
         raise ValueError("x must be a contiguous fp32/bf16/fp16 device tensor")
     qt = _tiled(weight)
+    if qt.bits == 32 and x.dtype != torch.float32:  # fp32 weights: fp32 products of the widened x
+        x = x.float()
     y = out if (out.dtype == torch.float32 and out.is_contiguous()) else \
         torch.empty(win, n_out, dtype=torch.float32, device=x.device)
     _lib.check(_lib.load().altxs_qgemm(ctypes.byref(qt), x.data_ptr(), _DT[x.dtype], win, y.data_ptr(),
@@ -531,6 +535,8 @@ def logits_stage_rows(src: torch.Tensor, weight: torch.Tensor, logit_buf: torch.
     y = logit_buf if (logit_buf.dtype == torch.float32 and logit_buf.is_contiguous()) else \
         torch.empty(win, vocab, dtype=torch.float32, device=src.device)
     if src.dtype == torch.bfloat16:
+        if weight.dtype != torch.bfloat16:
+            raise ValueError("a bf16 src row with an fp32 weight is not a reference combination")
         rounding = _RMS_ROUND_ROW | _RMS_ROUND_SCALE
     elif src.dtype == torch.float32:
         rounding = _RMS_ROUND_ROW if weight.dtype == torch.bfloat16 else 0

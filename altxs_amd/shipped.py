@@ -148,25 +148,42 @@ def ctypes_stream(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def pack_dense(delta: torch.Tensor, base: torch.Tensor | None = None) -> torch.Tensor:
-    """bf16(base + delta) in the MFMA-tiled order (uint8 device tensor, bits 16)."""
+def pack_dense(delta: torch.Tensor, base: torch.Tensor | None = None, bits: int = 16) -> torch.Tensor:
+    """base + delta in the MFMA-tiled order (uint8 device tensor): bits 16
+    rounds it to bf16, bits 32 keeps the fp32 value as three exact bf16 planes."""
     n, k = delta.shape
     if delta.dtype != torch.float32 or not delta.is_contiguous():
         raise ValueError("delta must be contiguous fp32 [N, K]")
     if base is not None and (base.shape != delta.shape or base.dtype != torch.float32
                              or not base.is_contiguous()):
         raise ValueError("base must match delta")
-    out = torch.empty(n * k * 2, dtype=torch.uint8, device=delta.device)
+    nbytes = dense_bytes(n, k, bits)
+    out = torch.empty(nbytes, dtype=torch.uint8, device=delta.device)
     L = _lib.load()
-    _lib.check(L.altxs_pack_dense(base.data_ptr() if base is not None else None, delta.data_ptr(),
-                                  n, k, k, out.data_ptr(), ctypes_stream(delta)), "altxs_pack_dense")
+    b = base.data_ptr() if base is not None else None
+    if bits == 16:
+        rc = L.altxs_pack_dense(b, delta.data_ptr(), n, k, k, out.data_ptr(), ctypes_stream(delta))
+    else:
+        rc = L.altxs_pack_dense32(b, delta.data_ptr(), n, k, k, out.data_ptr(), nbytes, ctypes_stream(delta))
+    _lib.check(rc, "altxs_pack_dense")
     return out
 
 
+def dense_bytes(n: int, k: int, bits: int) -> int:
+    """Bytes of a dense [n, k] tensor: bf16 values (bits 16), or three bf16
+    planes of the fp32 values (bits 32)."""
+    if bits == 16:
+        return n * k * 2
+    if bits == 32:
+        return n * k * 6
+    raise ValueError(f"dense bits {bits} not in (16, 32)")
+
+
 def decode_to_dense(cfg: AltxsConfig, banks: dict[str, DeviceBank], width: int,
-                    init: dict[str, torch.Tensor] | None, device) -> dict[str, PackedTensor]:
+                    init: dict[str, torch.Tensor] | None, device, bits: int = 16) -> dict[str, PackedTensor]:
     """Every modeled bank decoded into this build's tensors, Init added, packed
-    as bits-16 weights (PackedTensor with device-resident tiles)."""
+    as dense weights (bits 16: bf16, the reference's bf16 banks; bits 32:
+    fp32; PackedTensor with device-resident tiles)."""
     shapes = tensor_shapes(cfg)
     deltas = {name: torch.zeros(n * k, dtype=torch.float32, device=device) for name, (n, k) in shapes.items()}
     err = torch.zeros(1, dtype=torch.int32, device=device)
@@ -179,8 +196,8 @@ def decode_to_dense(cfg: AltxsConfig, banks: dict[str, DeviceBank], width: int,
     for name, (n, k) in shapes.items():
         d = deltas[name].view(n, k)
         base = init[name] if init is not None else None
-        tiled = pack_dense(d, base)
-        out[name] = PackedTensor(name, 16, np.zeros((0, 0), np.uint16), np.zeros((0, 0), np.float16),
+        tiled = pack_dense(d, base, bits)
+        out[name] = PackedTensor(name, bits, np.zeros((0, 0), np.uint16), np.zeros((0, 0), np.float16),
                                  tiled, np.zeros(0, np.float16), nk=(n, k))
     return out
 
@@ -192,10 +209,12 @@ def config_from_meta(meta: dict) -> AltxsConfig:
 
 
 def load_shipped(codec_path: str, init_state: dict[str, torch.Tensor],
-                 config_from_meta: Callable[[dict], AltxsConfig] = config_from_meta, device="cuda"):
+                 config_from_meta: Callable[[dict], AltxsConfig] = config_from_meta, device="cuda",
+                 bits: int = 16):
     """Read a shipped codec (``<stem>.json`` + ``<stem>.safetensors``, loaded
-    with safetensors: no code runs from the file) and return (cfg, dense bits-16
-    tensors on the device, small params as reference-named numpy arrays)."""
+    with safetensors: no code runs from the file) and return (cfg, dense
+    tensors on the device -- bits 16 or 32, as :func:`decode_to_dense` --,
+    small params as reference-named numpy arrays)."""
     from safetensors.numpy import load_file
 
     stem = codec_path[:-len(".safetensors")] if codec_path.endswith(".safetensors") else codec_path
@@ -226,6 +245,6 @@ def load_shipped(codec_path: str, init_state: dict[str, torch.Tensor],
         scales = {b: state[key("scale", f"b{b}")] for b in (2, 3, 4) if key("scale", f"b{b}") in state}
         banks[name] = DeviceBank(state[key("bits")], packed, books, mode, scales or None, device)
     init = split_init(cfg, init_state, device)
-    weights = decode_to_dense(cfg, banks, width, init, device)
+    weights = decode_to_dense(cfg, banks, width, init, device, bits)
     small = {n: state["small/" + n] for n in meta["small_params"] if "small/" + n in state}
     return cfg, weights, small

@@ -91,15 +91,16 @@ class SynthModel:
 
 
 def make_model(cfg: AltxsConfig, *, seed: int = WEIGHT_SEED, std: float = 0.02,
-               softcap: tuple[float, float] | None = None, dense: bool = False) -> SynthModel:
-    """``dense``: every matrix kept as bf16 (the reference's runtime banks)
-    instead of the mixed-bit packing."""
+               softcap: tuple[float, float] | None = None, dense: bool | int = False) -> SynthModel:
+    """``dense``: every matrix kept dense instead of the mixed-bit packing --
+    True or 16: bf16 (the reference's runtime banks); 32: fp32 (its fp32
+    compute mode)."""
     cfg.validate()
     rng = np.random.default_rng(seed)
     d, kvd, f = cfg.model_dim, cfg.kv_dim, cfg.hidden_dim
     names = tensor_list(cfg)
     if dense:
-        bits = {nm: 16 for nm, _, _ in names}
+        bits = {nm: (32 if dense == 32 else 16) for nm, _, _ in names}
     else:
         bits = allocate_bits([(nm, nn * kk) for nm, nn, kk in names], cfg.bpw_target)
     packed = {}

@@ -53,6 +53,12 @@ const char *altxs_last_error(void);
  * 16-row x 256-column blocks; in each block every lane of a wave owns the
  * codes its v_mfma_f32_16x16x32 B operand needs, split into 4/2/1-bit planes
  * so each lane reads whole 16/8-byte words.  N % 16 == 0, K % 256 == 0.
+ * Dense forms (no codes, scales unused): bits = 16 holds bf16 values in the
+ * same tiled order (N*K*2 bytes); bits = 32 holds fp32 values exactly as three
+ * bf16 planes hi + mid + lo (hi = bf16(w), mid = bf16(w - hi), lo = w - hi -
+ * mid), the three 8 KB planes of each 16 x 256 block stored one after the
+ * other (N*K*6 bytes), for the reference's fp32 compute mode; bits 32 needs
+ * fp32 activations.
  */
 typedef struct AltxsQTensor {
   const void *codes;  /* uint8 planes, N*K*bits/8 bytes */
@@ -469,6 +475,12 @@ int32_t altxs_codec_decode(const AltxsCodecGroups *g, const uint8_t *bits, const
  * 0, K % 256 == 0; row r of base/delta at r*ld). tiled: N*K*2 bytes. */
 int32_t altxs_pack_dense(const float *base, const float *delta, int64_t N, int64_t K, int64_t ld,
                          void *tiled, altxs_stream_t stream);
+
+/* The same for a dense bits = 32 tensor: w = base + delta kept in fp32, as
+ * the three exact bf16 planes (tiled: tiled_bytes >= N*K*6, checked).  The
+ * reference's fp32 compute mode keeps its banks in fp32 (model.py:1183-1196). */
+int32_t altxs_pack_dense32(const float *base, const float *delta, int64_t N, int64_t K, int64_t ld,
+                           void *tiled, int64_t tiled_bytes, altxs_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -26,6 +26,7 @@ semantics, restated here:
 
 from __future__ import annotations
 
+import os
 import types
 
 import numpy as np
@@ -41,6 +42,44 @@ def bf16_banks(sd: dict) -> dict:
     """The weight matrices rounded to bf16 values (engine_rows_bf16w.npz's weights)."""
     return {k: (torch.as_tensor(np.asarray(v)).to(torch.bfloat16).float().numpy() if k in BF16_BANKS
                 else v) for k, v in sd.items()}
+
+
+SHIPPED_STEM = os.path.join("shipped", "mixed_da_bpw3.15_upb1.8")
+
+
+def student_state_dict(golden_dir: str, *, round_banks: bool = False):
+    """(cfg, meta, reference-named fp32 state) of the shipped student: the
+    restated Init(seed) plus the delta the oracle's codec decodes from the
+    copy of the asset in tests/golden/shipped/ (``load_codec``,
+    mixed_bit_delta.py:232-312); ``round_banks``: the banks rounded to bf16
+    values (the reference's bf16 runtime banks, model.py:1183-1245)."""
+    import json
+
+    from safetensors.numpy import load_file
+
+    from altxs_amd.init_seed import reference_init_state
+    from altxs_amd.shipped import MODELED, config_from_meta
+    from oracle import codec_ref
+
+    meta = json.load(open(os.path.join(golden_dir, SHIPPED_STEM + ".json"), encoding="utf8"))
+    cfg = config_from_meta(meta)
+    state = load_file(os.path.join(golden_dir, SHIPPED_STEM + ".safetensors"))
+    sd = {k: v.numpy() for k, v in reference_init_state(cfg, int(meta["seed"])).items()}
+    L, width = int(meta["n_layers"]), cfg.model_dim
+    for name in MODELED:
+        key = lambda kind, *rest: "/".join((kind, name) + rest)  # noqa: E731
+        bits = state[key("bits")]
+        packed = {b: state[key("packed", f"b{b}")] for b in (2, 3, 4)}
+        books = {b: state[key("codebook", f"b{b}")] for b in (2, 3, 4) if key("codebook", f"b{b}") in state}
+        scales = {b: state[key("scale", f"b{b}")] for b in (2, 3, 4) if key("scale", f"b{b}") in state}
+        ch = codec_ref.dequantize_channels(bits, books, packed, channel_width=width,
+                                           mode=str(meta["codebook_mode"]), scales=scales or None)
+        sd[name] = sd[name] + codec_ref.from_channels(name, ch, meta["layouts"][name]["shape"], L)
+    for n in meta["small_params"]:
+        sd[n] = state["small/" + n]
+    if round_banks:
+        sd = bf16_banks(sd)
+    return cfg, meta, sd
 
 
 class RefStaticKV:

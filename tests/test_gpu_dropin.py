@@ -14,9 +14,9 @@ arguments, checked against the oracle and the reference's own vectors.
   commits): the slots become views of the step's cache; logits within 2e-4
   of the fp32 oracle, windows equal to rows bit for bit; the engine's own
   flow (prefill into the slots, rebind, row-state sync, windows and rows)
-  within 2e-5 of rows the reference's StaticACEngine wrote; False plus a
-  sticky disable on a broken state or on fp32 weights the bf16 banks would
-  round;
+  within 2e-5 of rows the reference's StaticACEngine wrote (fp32 weights, or
+  bf16-valued ones); fp32 models on fp32 banks; False plus a sticky disable
+  on a broken state;
 * ``gemv_rows`` / ``logits_stage_rows`` against fp64 products.
 """
 
@@ -202,29 +202,33 @@ def test_try_persistent_extend_shares_the_state_kv():
     assert model._persist_disabled and not dropin.try_persistent_extend(model, st)
 
 
-def _engine(bf16: bool, golden_dir):
+def _engine(bf16: bool, golden_dir, fixture: str = "engine_rows_bf16w.npz"):
     from .refshape import RefEngine
 
-    z = np.load(os.path.join(golden_dir, "engine_rows_bf16w.npz"))
+    z = np.load(os.path.join(golden_dir, fixture))
     cfg, model, sd = _ref_model("tiny", bf16=bf16, std=float(z["std"]),
-                                softcap=tuple(z["softcap"].tolist()))
+                                softcap=tuple(z["softcap"].tolist()),
+                                round_banks=fixture == "engine_rows_bf16w.npz")
     eng = RefEngine(model, cfg, sd, win=int(z["win"]), block=int(z["block"]), every=int(z["every"]))
     assert eng.max_len == int(z["max_len"])
     return z, eng
 
 
+@pytest.mark.parametrize("fixture", ["engine_rows.npz", "engine_rows_bf16w.npz"])
 @pytest.mark.parametrize("key,start", [("rows_ctx", 100), ("rows_start", 0)])
-def test_engine_flow_matches_reference_engine(golden_dir, key, start):
+def test_engine_flow_matches_reference_engine(golden_dir, fixture, key, start):
     """The engine's own flow through the drop-in (reset_segment's eager prefill
     into the slots, _rebind_packed_kv, W=16 windows through try_mega_encode
     with commit_window, the row state synced from the prefix and stepped
-    through try_persistent_extend): rows within 2e-5 of the rows the
-    reference's StaticACEngine wrote on the same weights, and the window rows
-    equal the decode rows bit for bit (encode/decode lockstep)."""
+    through try_persistent_extend) on an fp32 model -- its fp32 weights
+    (engine_rows.npz) or the same rounded to bf16 values (_bf16w): rows within
+    2e-5 of the rows the reference's StaticACEngine wrote on those weights,
+    and the window rows equal the decode rows bit for bit (encode/decode
+    lockstep)."""
     from oracle import coder
 
-    _log(f"dropin engine flow {key} (tiny, fp32)")
-    z, eng = _engine(False, golden_dir)
+    _log(f"dropin engine flow {fixture} {key} (tiny, fp32)")
+    z, eng = _engine(False, golden_dir, fixture)
     arr, seg = z["arr"], z["arr"][start:start + 64]
     enc = eng.segment_rows_tf(arr, seg, start)
     err = float(np.abs(enc - z[key]).max())
@@ -254,17 +258,28 @@ def test_engine_flow_bf16_lockstep(golden_dir):
     assert eng.model._encode_ws.k_pack.dtype == torch.bfloat16
 
 
-def test_fp32_model_with_fp32_weights_is_refused():
-    """An fp32 model whose matrices are not bf16 values: the step would round
-    them (the dense banks are bf16), so it declines like a tier that cannot
-    run -- False, logged, disabled."""
-    from altxs_amd import dropin
+def test_fp32_model_keeps_fp32_weights():
+    """An fp32 model whose matrices are not bf16 values runs on fp32 banks
+    (bits 32): logits within 2e-4 of the fp32 oracle on the same weights."""
+    from altxs_amd import synth
+    from oracle.model_ref import OracleModel
 
-    _log("dropin refuses fp32 weights that are not bf16 values")
-    cfg, model, _ = _ref_model("tiny", bf16=False, round_banks=False)
+    _log("dropin fp32 model, fp32 weights")
+    cfg, model, sd = _ref_model("tiny", bf16=False, round_banks=False)
     st = model.make_static_state(256, "cuda", win=1)
-    assert not dropin.try_persistent_extend(model, st)
-    assert model._persist_disabled
+    toks = synth.zipf_tokens(cfg.vocab_size, (12,), seed=3)
+    rows = []
+    for t, tk in enumerate(toks):
+        st.token.fill_(int(tk))
+        st.pos.fill_(t)
+        model.static_extend_fused(st)
+        rows.append(st.logits[0, 0].cpu().clone())
+        st.commit_window(t)
+        st.prev_raw.copy_(st.cand_prev_raw)
+    assert all(q.bits == 32 for q in model._altxs_adapter.step.qt.values())
+    err = float(np.abs(torch.stack(rows).numpy() - OracleModel(cfg, sd, max_len=256).decode_rows(toks).numpy()).max())
+    _log(f"max |dlogit| = {err:.3e}")
+    assert err < 2e-4, err
 
 
 def test_gemv_rows_and_logits_stage_rows():

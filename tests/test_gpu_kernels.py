@@ -122,6 +122,34 @@ def test_qgemm_against_fp32_matmul(bits, shape, B, xdt):
     assert err < 1e-5 * max(1.0, ref.abs().max().item()) * math.sqrt(k)
 
 
+@pytest.mark.parametrize("shape", [(512, 2048), (2048, 512), (16, 256)])
+@pytest.mark.parametrize("B", [1, 5, 64])
+def test_qgemm_dense_fp32_weights(shape, B):
+    """bits 32 (fp32 weights as three exact bf16 planes) with fp32 x: the
+    products of an fp32 matmul to ~2^-24 relative per term; bits 16 of the
+    same weights misses that bound (the planes matter); bf16 or fp16 x is
+    refused."""
+    from altxs_amd import ops
+    from altxs_amd.codec import PackedTensor
+
+    _log(f"qgemm bits=32 shape={shape} B={B}")
+    n, k = shape
+    rng = np.random.default_rng(40 + B)
+    w32 = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    x32 = torch.from_numpy(rng.standard_normal((B, k)).astype(np.float32))
+    ref = x32.double() @ torch.from_numpy(w32).double().T
+    bound = 1e-6 * math.sqrt(k) * max(1.0, ref.abs().max().item())
+    w = ops.DeviceQTensor(PackedTensor.from_dense("w", w32, 32))
+    y = ops.qgemm(w, x32.to(DEV).contiguous()).cpu().double()
+    err = (y - ref).abs().max().item()
+    assert err < bound, (err, bound)
+    w16 = ops.DeviceQTensor(PackedTensor.from_dense("w", w32, 16))
+    y16 = ops.qgemm(w16, x32.to(DEV).contiguous()).cpu().double()
+    assert (y16 - ref).abs().max().item() > 10 * bound
+    with pytest.raises(RuntimeError):
+        ops.qgemm(w, x32.to(torch.bfloat16).to(DEV).contiguous())
+
+
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("shape", [(2048, 512), (512, 2048)])
 @pytest.mark.parametrize("bits", [2, 3, 4, 6])

@@ -14,7 +14,10 @@ altxs_pack_dense) and the dense bf16 step it feeds.
   rows, tests/golden/shipped_slice.npz) decode on the device to exactly the
   values the reference's own decoder produced from the whole bank, and the
   five codebook modes decode to the reference's outputs on its vectors
-  (tests/golden/codec_modes.npz).  (The asset itself is not on the GPU box.)
+  (tests/golden/codec_modes.npz);
+* the whole asset (a copy in tests/golden/shipped/) through
+  ``dropin.load_codec(path, device=...)`` with Init(seed) built here: the
+  student's logits against the ones the reference's load_codec model wrote.
 """
 
 from __future__ import annotations
@@ -116,6 +119,11 @@ def test_pack_dense_matches_host_packer():
     got = shipped.pack_dense(torch.from_numpy(delta).cuda(), torch.from_numpy(base).cuda())
     want = codec.pack_dense_tiled(base + delta)
     assert np.array_equal(got.cpu().numpy(), want)
+    got32 = shipped.pack_dense(torch.from_numpy(delta).cuda(), torch.from_numpy(base).cuda(), bits=32)
+    assert np.array_equal(got32.cpu().numpy(), codec.pack_dense32_tiled(base + delta))
+    hi, mid, lo = codec.split3_bf16(base + delta)  # the planes sum back to the fp32 value exactly
+    planes = [(p.astype(np.uint32) << np.uint32(16)).view(np.float32) for p in (hi, mid, lo)]
+    assert np.array_equal((planes[0] + planes[1]) + planes[2], base + delta)
     got0 = shipped.pack_dense(torch.from_numpy(delta).cuda())
     assert np.array_equal(got0.cpu().numpy(), codec.pack_dense_tiled(delta))
 
@@ -189,16 +197,73 @@ def test_shipped_codec_end_to_end(tmp_path):
     err = np.abs(got - want).max()
     _log(f"max |dlogit| = {err:.3e}")
     assert err < 2e-4, err
-    # the reference-named loader gives the same step model
+    # the reference-named loader in the fp32 mode keeps Init + delta in fp32
+    # (bits-32 banks): the oracle on the unrounded sum
     from altxs_amd import dropin
 
     model2, meta2, _ = dropin.load_codec(stem + ".safetensors", device="cuda", init_state=init, act="fp32")
     assert meta2["codebook_mode"] == "lloyd"
+    assert all(model2.qt[n].bits == 32 for n in model2.qt)
     st2 = model2.make_static_state(256, win=1, batch=2)
+    got2 = []
     for t in range(toks.shape[1]):
         st2.token.copy_(torch.from_numpy(toks[:, t:t + 1]))
         model2.step(st2, commit=True)
-        assert np.array_equal(st2.logits.cpu().numpy(), got[:, t])
+        got2.append(st2.logits.cpu().numpy().copy())
+    st2.check_errors()
+    sd32 = dict(sm0.small)
+    sd32.update({n: init[n] + delta[n] for n in shapes})
+    om32 = OracleModel(cfg, sd32, max_len=256)
+    want32 = np.stack([om32.decode_rows(t).numpy() for t in toks.astype(np.int64)])
+    err32 = np.abs(np.stack(got2, 1) - want32).max()
+    _log(f"fp32 banks: max |dlogit| = {err32:.3e}")
+    assert err32 < 2e-4, err32
+
+
+def test_real_student_decodes_whole_asset(golden_dir):
+    """The reference's shipped codec (tests/golden/shipped/, its
+    weights/mixed_da_bpw3.15_upb1.8.*) through ``dropin.load_codec(path,
+    device=...)``: Init(seed) restated, the whole delta decoded and added on
+    the device, the 17-slot student (GQA, depth loops, parallel lanes, XSA,
+    gates) stepped W=1 from the stream start.
+    * fp32 banks: logits within 2e-3 of the fp32 logits the reference's own
+      load_codec model wrote (tests/golden/shipped_full.npz);
+    * bf16 banks and bf16 activations (the reference's production dtypes,
+      model.py:1183-1245, compress.py:58-61): no farther from the fp32
+      reference logits than the reference's own eager step under its bf16
+      autocast policy is (rows_w1_autocast_bf16, written by the reference:
+      0.52 max, 0.083 mean on this student), in max and in mean."""
+    import os
+
+    from altxs_amd import dropin
+    from oracle import coder
+
+    z = np.load(os.path.join(golden_dir, "shipped_full.npz"))
+    path = os.path.join(golden_dir, "shipped", "mixed_da_bpw3.15_upb1.8.safetensors")
+    toks = z["tokens"].astype(np.int32)
+    ref = z["rows_w1"]
+    ref_bf16 = np.abs(z["rows_w1_autocast_bf16"] - ref)
+    for act in ("fp32", "bf16"):
+        _log(f"real student, {act} banks")
+        model, meta, small = dropin.load_codec(path, device="cuda", act=act)
+        assert model.n_slots == 17 and model.cfg.vocab_size == 256
+        st = model.make_static_state(int(z["max_len"]), win=1, batch=1)
+        rows, cums = [], []
+        for t in range(toks.size):
+            st.token.fill_(int(toks[t]))
+            model.step(st, commit=True)
+            rows.append(st.logits[0].cpu().numpy().copy())
+            cums.append(st.cum[0].cpu().numpy().copy())
+        st.check_errors()
+        d = np.abs(np.stack(rows) - ref)
+        _log(f"{act}: max |dlogit| = {d.max():.3e}, mean {d.mean():.3e} (reference bf16 autocast: "
+             f"{ref_bf16.max():.3e}, {ref_bf16.mean():.3e}; logits up to {np.abs(ref).max():.1f})")
+        if act == "fp32":
+            assert d.max() < 2e-3, d.max()
+        else:
+            assert d.max() <= ref_bf16.max() and d.mean() <= ref_bf16.mean(), (d.max(), d.mean())
+        # the last row's table is the rule applied to the device probabilities
+        assert np.array_equal(cums[-1].astype(np.int64), coder.scale_cum(st.probs[0].cpu().numpy()[None])[0])
 
 
 def _decode_on_device(bits, packed, books, mode, width, scales=None):

@@ -10,6 +10,7 @@ import os
 import re
 import subprocess
 
+import numpy as np
 import pytest
 
 from altxs_amd import _lib
@@ -49,6 +50,22 @@ def test_bad_arguments_return_errors_without_gpu():
     assert L.altxs_codec_decode(None, None, None, 1, 512, None, 512, 1, None, None) == -1
     assert L.altxs_pack_dense(None, None, 16, 256, 256, None, None) == -1
     assert b"altxs_pack_dense" in L.altxs_last_error()
+    # a bits-32 buffer smaller than N*K*6 bytes is refused before any launch
+    fake = ctypes.c_void_p(1 << 20)
+    assert L.altxs_pack_dense32(None, fake, 16, 256, 256, fake, 16 * 256 * 4, None) == -1
+    assert b"bytes" in L.altxs_last_error()
+
+
+def test_dense_sizes():
+    from altxs_amd import codec, shipped
+
+    assert shipped.dense_bytes(48, 768, 16) == 48 * 768 * 2
+    assert shipped.dense_bytes(48, 768, 32) == 48 * 768 * 6
+    w = np.zeros((48, 768), np.float32)
+    assert codec.pack_dense32_tiled(w).size == shipped.dense_bytes(48, 768, 32)
+    assert codec.pack_dense_tiled(w).size == shipped.dense_bytes(48, 768, 16)
+    with pytest.raises(ValueError):
+        shipped.dense_bytes(48, 768, 8)
 
 
 def test_struct_layout_matches_header(tmp_path):
