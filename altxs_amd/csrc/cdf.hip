@@ -15,6 +15,8 @@ namespace {
 
 constexpr int CDF_THREADS = 1024;
 constexpr int CDF_WAVES = CDF_THREADS / WAVE;
+// Renormalised rows stage the row in LDS for numpy's summation order (64 KB).
+constexpr int kRenormMaxV = 16384;
 
 __device__ __forceinline__ uint32_t scale_count(float p) {
   double t = __dmul_rn((double)p, 1000000.0);
@@ -78,6 +80,70 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* wred) 
   return base + incl - v;
 }
 
+// numpy's float32 add-reduce of a contiguous row, which the reference's
+// renormalisation uses (``p /= float(p.sum())``, compress.py:64-85): the row
+// is summed in chunks of NPY_BUFSIZE = 8192 elements, accumulated in order
+// from 0, each chunk by numpy's pairwise_sum -- blocks of at most 128
+// elements summed into 8 interleaved accumulators combined as
+// ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) plus the tail in order, larger ranges
+// split at half the length rounded down to a multiple of 8, the two halves
+// added.  One thread, from LDS (the row is summed once per context reset).
+constexpr int kNpyBuf = 8192, kNpyBlock = 128;
+
+__device__ float np_leaf_sum(const float* a, int n) {
+  if (n < 8) {
+    float r = 0.f;
+    for (int i = 0; i < n; ++i) r += a[i];
+    return r;
+  }
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = a[j];
+  int i = 8;
+  for (; i < n - (n % 8); i += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+  }
+  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; ++i) res += a[i];
+  return res;
+}
+
+__device__ float np_pairwise_sum(const float* a, int n) {
+  struct Frame { int off, n, stage; float left; };
+  Frame st[16];  // depth <= log2(8192 / 128) + 1
+  int sp = 0;
+  float ret = 0.f;
+  st[sp++] = Frame{0, n, 0, 0.f};
+  while (sp > 0) {
+    Frame& f = st[sp - 1];
+    if (f.n <= kNpyBlock) {
+      ret = np_leaf_sum(a + f.off, f.n);
+      --sp;
+      continue;
+    }
+    const int n2 = f.n / 2 - (f.n / 2) % 8;
+    if (f.stage == 0) {
+      f.stage = 1;
+      st[sp++] = Frame{f.off, n2, 0, 0.f};
+    } else if (f.stage == 1) {
+      f.left = ret;
+      f.stage = 2;
+      st[sp++] = Frame{f.off + n2, f.n - n2, 0, 0.f};
+    } else {
+      ret = f.left + ret;
+      --sp;
+    }
+  }
+  return ret;
+}
+
+__device__ float np_sum(const float* a, int n) {
+  float acc = 0.f;
+  for (int k = 0; k < n; k += kNpyBuf) acc += np_pairwise_sum(a + k, n - k < kNpyBuf ? n - k : kNpyBuf);
+  return acc;
+}
+
 template <int EPT, bool FROM_LOGITS>
 __global__ __launch_bounds__(CDF_THREADS) void cdf_kernel(const float* __restrict__ in,
                                                            int V, int flags,
@@ -85,6 +151,7 @@ __global__ __launch_bounds__(CDF_THREADS) void cdf_kernel(const float* __restric
                                                            uint32_t* __restrict__ cum) {
   __shared__ float red[CDF_WAVES];
   __shared__ uint32_t wred[CDF_WAVES];
+  extern __shared__ float row_lds[];  // [V] with ALTXS_CDF_RENORM
   const int64_t row = blockIdx.x;
   const float* x = in + row * (int64_t)V;
   const int base = threadIdx.x * EPT;
@@ -109,13 +176,22 @@ __global__ __launch_bounds__(CDF_THREADS) void cdf_kernel(const float* __restric
     s = block_sum(s, red);
 #pragma unroll
     for (int i = 0; i < EPT; ++i) v[i] = v[i] / s;
-    if (flags & ALTXS_CDF_RENORM) {
-      float s2 = 0.f;
+    if (flags & ALTXS_CDF_RENORM) {  // p /= float(p.sum()) with numpy's sum (compress.py:78-83)
 #pragma unroll
-      for (int i = 0; i < EPT; ++i) s2 += v[i];
-      s2 = block_sum(s2, red);
+      for (int i = 0; i < EPT; ++i)
+        if (base + i < V) row_lds[base + i] = v[i];
+      __syncthreads();
+      if (threadIdx.x == 0) red[0] = np_sum(row_lds, V);
+      __syncthreads();
+      const float s2 = red[0];
+      if (!(s2 > 0.f) || s2 == INFINITY) {  // non-positive or non-finite sum: the uniform row
+        const float u = 1.0f / (float)V;
 #pragma unroll
-      for (int i = 0; i < EPT; ++i) v[i] = v[i] / s2;
+        for (int i = 0; i < EPT; ++i) v[i] = u;
+      } else {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) v[i] = v[i] / s2;
+      }
     }
     if (probs) {
       float* po = probs + row * (int64_t)V;
@@ -373,11 +449,14 @@ hipError_t launch_cdf(const float* in, int64_t rows, int V, int flags, float* pr
                       uint32_t* cum, hipStream_t s) {
   const int ept = (V + CDF_THREADS - 1) / CDF_THREADS;
   dim3 grid((unsigned)rows), block(CDF_THREADS);
-#define CDF_CASE(E)                                                                   \
-  if (ept <= E) {                                                                     \
-    hipLaunchKernelGGL((cdf_kernel<E, FROM_LOGITS>), grid, block, 0, s, in, V, flags, \
-                       probs, cum);                                                   \
-    return hipGetLastError();                                                         \
+  const bool renorm = FROM_LOGITS && (flags & ALTXS_CDF_RENORM);
+  if (renorm && V > kRenormMaxV) return hipErrorInvalidValue;
+  const size_t lds = renorm ? (size_t)V * sizeof(float) : 0;
+#define CDF_CASE(E)                                                                     \
+  if (ept <= E) {                                                                       \
+    hipLaunchKernelGGL((cdf_kernel<E, FROM_LOGITS>), grid, block, lds, s, in, V, flags, \
+                       probs, cum);                                                     \
+    return hipGetLastError();                                                           \
   }
   CDF_CASE(1) CDF_CASE(2) CDF_CASE(4) CDF_CASE(8) CDF_CASE(16) CDF_CASE(32) CDF_CASE(64)
 #undef CDF_CASE
@@ -465,6 +544,8 @@ extern "C" int32_t altxs_softmax_cdf(const float* logits, int64_t rows, int64_t 
   ALTXS_REQUIRE(logits, "altxs_softmax_cdf: null logits");
   ALTXS_REQUIRE(V >= 1 && V <= 65536, "altxs_softmax_cdf: V=%lld outside [1, 65536]",
                 (long long)V);
+  ALTXS_REQUIRE(!(flags & ALTXS_CDF_RENORM) || V <= kRenormMaxV,
+                "altxs_softmax_cdf: renormalised rows need V <= %d", kRenormMaxV);
   ALTXS_REQUIRE(rows >= 0 && rows < (1ll << 31), "altxs_softmax_cdf: bad rows");
   ALTXS_CHECK_HIP(altxs_launch_cdf(logits, rows, (int)V, flags, true, probs, cum,
                                    (hipStream_t)stream));

@@ -201,6 +201,8 @@ int validate(const AltxsStepDesc* d) {
   if (d->aux_stream) ALTXS_REQUIRE(d->sync_events, "altxs_step: aux_stream needs sync_events");
   if (d->flags & ALTXS_F_SMEAR)
     ALTXS_REQUIRE(d->smear_w && d->smear_lambda, "altxs_step: smear params missing");
+  if (d->flags & ALTXS_F_RENORM)
+    ALTXS_REQUIRE(d->V <= 16384, "altxs_step: renormalised rows need V <= 16384 (V=%d)", d->V);
   if (d->flags & ALTXS_F_ASYM_SOFTCAP) ALTXS_REQUIRE(d->softcap_pn, "altxs_step: softcap_pn missing");
   const int kvd = d->Hkv * HD;
   for (int l = 0; l < d->n_layers; ++l) {

@@ -83,7 +83,11 @@ int32_t altxs_scale_cum(const float *probs, int64_t rows, int64_t V, uint32_t *c
 int32_t altxs_scale_cum_f64(const double *probs, int64_t rows, int64_t V, uint32_t *cum,
                             altxs_stream_t stream);
 
-#define ALTXS_CDF_RENORM 1 /* p /= sum(p) after the softmax (compress.py:78-83) */
+#define ALTXS_CDF_RENORM 1 /* p /= sum(p) after the softmax, the sum in numpy's float32
+                              order (pairwise blocks of 128, 8192-element chunks) as the
+                              reference's _softmax_np computes it (compress.py:64-85);
+                              a non-positive or non-finite sum gives the uniform row;
+                              V <= 16384 */
 
 /*
  * Deterministic softmax + CDF: probs = softmax(logits) in fp32 with a fixed
@@ -229,7 +233,7 @@ enum {
   ALTXS_F_SKIP_GATES = 1 << 2,  /* gated U-Net skips (model.py:1275-1291) */
   ALTXS_F_ASYM_SOFTCAP = 1 << 3,/* asymmetric tanh softcap (model.py:1478-1493) */
   ALTXS_F_COMMIT = 1 << 4,      /* after the step: pos += W, prev_raw = last raw */
-  ALTXS_F_RENORM = 1 << 5,      /* renormalise probs before the CDF */
+  ALTXS_F_RENORM = 1 << 5,      /* renormalise probs before the CDF (ALTXS_CDF_RENORM; V <= 16384) */
   ALTXS_F_FINAL_ATTN = 1 << 6,  /* parallel_final_lane = "attn" (default mean) */
   ALTXS_F_FINAL_MLP = 1 << 7,   /* parallel_final_lane = "mlp" */
 };

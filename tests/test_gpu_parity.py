@@ -14,7 +14,8 @@
   2048 cfg3 symbols;
 * the probability engine against rows the reference's own StaticACEngine
   wrote (tests/golden/engine_rows.npz): carry by the renormalised softmax,
-  RoPE warmed at the engine length (YaRN), windows after a context.
+  RoPE warmed at the engine length (YaRN), windows after a context; the
+  carry is numpy's renormalisation of the step's softmax, bit for bit.
 """
 
 from __future__ import annotations
@@ -206,3 +207,45 @@ def test_engine_rows_match_reference_engine(golden_dir):
         assert abs(ib - rb) / rb < 1e-4, (key, ib, rb)
         if start == 0:
             assert np.array_equal(cum[0, 0], coder.scale_cum(ref[:1])[0])
+
+
+def test_engine_carry_follows_reference_rule(golden_dir):
+    """The context carry (reset_segment, incremental.py:878-886) is
+    ``_softmax_np`` of the context's last logits (compress.py:64-85): the
+    softmax, then ``p /= float(p.sum())`` with numpy's own float32 sum.  The
+    engine's carry probabilities equal, bit for bit, numpy's renormalisation
+    (run here by numpy itself) of the step's softmax of those logits, and the
+    carry table is the count rule of them."""
+    from altxs_amd import ops, synth
+    from altxs_amd.config import make_config
+    from altxs_amd.engine import StaticACEngine
+    from altxs_amd.model import StepModel
+    from oracle import coder
+
+    _log("engine carry = numpy renormalisation of the softmax")
+    z = np.load(os.path.join(golden_dir, "engine_rows.npz"))
+    for profile, act in (("tiny", "fp32"), ("cfg3", "bf16")):
+        cfg = make_config(profile, online_retrain_every=int(z["every"]))
+        sm = synth.make_model(cfg, std=float(z["std"]) if profile == "tiny" else 0.02,
+                              softcap=tuple(z["softcap"].tolist()) if profile == "tiny" else (30.0, 24.0))
+        model = StepModel(sm, act=act)
+        eng = StaticACEngine(model, batch=2, win=int(z["win"]), block=int(z["block"]), want_probs=True)
+        arr = synth.zipf_tokens(cfg.vocab_size, (300,), seed=31)
+        arr2 = synth.zipf_tokens(cfg.vocab_size, (300,), seed=32)
+        eng.reset_segment([arr, arr2], [100, 100])
+        w = int(z["win"])  # the 64-token context is four full windows
+        V = cfg.vocab_size
+        lg = eng.st.logits[:2 * w].view(2, w, V)[:, w - 1].contiguous()
+        p, _ = ops.softmax_cdf(lg)
+        p = p.cpu().numpy()
+        for b in range(2):
+            row = p[b].copy()
+            row /= float(row.sum())  # _softmax_np's renormalisation, by numpy
+            assert np.array_equal(eng.carry_probs[b].cpu().numpy(), row), (profile, b)
+            assert np.array_equal(eng.carry_row_dev()[b].cpu().numpy().astype(np.int64),
+                                  coder.scale_cum(row[None])[0]), (profile, b)
+        # the sum order matters: a plain left-to-right fp32 sum moves some rows
+        seq = [np.float32(0)]
+        for x in p[0]:
+            seq[0] = np.float32(seq[0] + x)
+        _log(f"{profile}: numpy sum {float(p[0].sum())!r}, sequential {float(seq[0])!r}")
