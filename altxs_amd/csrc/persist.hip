@@ -292,6 +292,13 @@ __global__ __launch_bounds__(kThreads, ALTXS_PERSIST_MINW) void roles_kernel(con
 #endif
       if (valid) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        // The release writes the XCD's L2 back (buffer_wbl2 sc1); the counter
+        // may only move once that write-back has completed, or a consumer on
+        // another XCD can read stale data from memory.  The compiled fence
+        // was followed by no vmcnt wait before the atomic (the assembly of
+        // this kernel showed buffer_wbl2 directly followed by the
+        // flat_atomic_add), so the wait is spelled out here.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         atomicAdd(a.done + ((int64_t)s * a.nrt + m) * a.ctr_stride + st, 1);
       }
       s_task = atomicAdd(q, 1);
