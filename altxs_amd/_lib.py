@@ -46,6 +46,8 @@ EXPORTS = (
     "altxs_dequant",
     "altxs_qgemm",
     "altxs_qgemm_stream",
+    "altxs_qgemv",
+    "altxs_qgemv_stream",
     "altxs_rms_qgemm",
     "altxs_decode_attn",
     "altxs_step_workspace_bytes",
@@ -168,6 +170,10 @@ def load():
     L.altxs_qgemm.argtypes = [ctypes.POINTER(QTensor), p, i32, i64, p, p]
     L.altxs_qgemm_stream.restype = i32
     L.altxs_qgemm_stream.argtypes = [ctypes.POINTER(QTensor), i64, i64, i64, p, i32, i64, p, p]
+    L.altxs_qgemv.restype = i32
+    L.altxs_qgemv.argtypes = [ctypes.POINTER(QTensor), p, i32, i64, p, p]
+    L.altxs_qgemv_stream.restype = i32
+    L.altxs_qgemv_stream.argtypes = [ctypes.POINTER(QTensor), i64, i64, i64, p, i32, i64, p, p]
     L.altxs_rms_qgemm.restype = i32
     L.altxs_rms_qgemm.argtypes = [ctypes.POINTER(QTensor), p, i64, ctypes.c_float, ctypes.c_float, i32, p, p]
     L.altxs_decode_attn.restype = i32

@@ -31,6 +31,7 @@ struct AttnP {
   int32_t* err;
   int xcd_rows;  // one-row kernel: rows in tiles of 8, tile t on XCD t % 8
   int kv_tail = -1;  // natural layouts: first row of the window's K/V (-1: at pos + t)
+  int helpers = 0;   // small MHA decode launches: prefetch workgroups per (row, kv head)
 };
 
 // Row of the cache that holds key j of a query of segment b whose window starts

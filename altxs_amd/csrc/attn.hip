@@ -38,9 +38,67 @@ using namespace altxs_attn;
 
 namespace {
 
-template <int G, int NP, int YBF16>
+// Decode launches with fewer (row, kv head) workgroups than this take the
+// two-tiles-in-flight MHA variant (the chip has 256 CUs), with prefetch
+// workgroups beside them (attn_prefetch_task).
+constexpr unsigned kAttnSmallGrid = 256;
+
+// Prefetch workgroup h (of a.helpers) of (row, kv head) pair c in a small
+// decode launch: it touches one word of every 128-byte line of the pair's K
+// and V tiles h, h + helpers, ... (both halves of the workgroup interleave
+// tiles), all loads in flight at once, so the lines are in the L2 before the
+// pair's compute waves reach them.  Pair c's compute workgroup has id c and
+// helper h id (h + 1) * pairs + c; workgroups are dealt to the 8 XCDs
+// round-robin by id, so with pairs % 8 == 0 both share an XCD and its L2
+// (otherwise the lines still come from the memory-side cache).  Reads only:
+// the results are the compute workgroups' alone.
+// ESZ: bytes per cache element (2: bf16, tiled or natural; 4: fp32).  In
+// every layout tile T of a (segment, kv head) is TILE x HD consecutive
+// elements (keys 64T .. 64T + 63); with a tail placement the window's rows
+// are not prefetched (one row per query at W = 1).
+template <int ESZ>
+__device__ __forceinline__ void attn_prefetch_task(const AttnP& a, int c, int h) {
+  constexpr int kLines = TILE * HD * ESZ / 128;  // 128-byte lines per K (or V) tile
+  constexpr int kGroups = ATT_THREADS / (2 * kLines);  // tiles one pass touches
+  static_assert(kGroups >= 1 && ATT_THREADS % (2 * kLines) == 0, "one K and one V tile per thread group");
+  const int r = c / a.Hkv, g = c % a.Hkv, b = r / a.W;
+  int p = a.pos[b] + r % a.W;
+  p = p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p);  // the compute task flags it
+  const int ntiles = p / TILE + 1;
+  const int grp = threadIdx.x / (2 * kLines), li = threadIdx.x % (2 * kLines);
+  const int64_t off = ((int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD) * ESZ;
+  const char* base = (const char*)(li < kLines ? a.k : a.v) + off + (li % kLines) * 128;
+  const int step = kGroups * a.helpers;
+  uint32_t acc = 0;
+  for (int T0 = h + a.helpers * grp; T0 < ntiles; T0 += 8 * step) {
+    uint32_t x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {  // unconditional: a tile past the end re-reads the last one
+      const int T = min(T0 + u * step, ntiles - 1);
+      x[u] = *(const uint32_t*)(base + (int64_t)T * (TILE * HD * ESZ));
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += x[u];
+  }
+  asm volatile("" ::"v"(acc));  // keeps the loads
+}
+
+// Helpers per (row, kv head) pair of a launch of `pairs` workgroups (0: none).
+inline int attn_helpers(unsigned pairs) {
+  return pairs < kAttnSmallGrid ? (int)(kAttnSmallGrid / pairs < 16 ? kAttnSmallGrid / pairs : 16) : 0;
+}
+
+template <int G, int NP, int YBF16, int PF>
 __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
+  if constexpr (G == 1 && PF == 1) {
+    const int pairs = a.B * a.W * a.Hkv;
+    if (a.helpers > 0 && (int)blockIdx.x >= pairs) {
+      const int id = blockIdx.x - pairs;
+      attn_prefetch_task<2>(a, id % pairs, id / pairs);
+      return;
+    }
+  }
   int r = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
   if (a.xcd_rows) {  // row tile t (8 rows x Hkv heads) on XCD t % 8
     int t, j;
@@ -48,8 +106,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
     r = 8 * t + j / a.Hkv;
     g = j % a.Hkv;
   }
-  // GQA launches have G times fewer workgroups: keep two tiles per wave in flight
-  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : ALTXS_ATT_PF)>(a, r, g, sm);
+  // GQA launches have G times fewer workgroups, and small launches (PF = 1)
+  // too few to cover the load latency: keep two tiles per wave in flight
+  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : PF)>(a, r, g, sm);
 }
 
 // Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
@@ -114,6 +173,14 @@ __device__ __forceinline__ float load1(const KVT* base, int64_t row, int d) {
 template <int G, int YBF16, class KVT>
 __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
+  {
+    const int pairs = a.B * a.W * a.Hkv;
+    if (a.helpers > 0 && (int)blockIdx.x >= pairs) {
+      const int id = blockIdx.x - pairs;
+      attn_prefetch_task<(int)sizeof(KVT)>(a, id % pairs, id / pairs);
+      return;
+    }
+  }
   int r = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
   if (a.xcd_rows) {  // row tile (8 rows x Hkv heads) tt on XCD tt % 8
     int tt, j;
@@ -233,16 +300,37 @@ hipError_t launch_y(const AttnP& p, int group, int kv_layout, bool ops_bf16, boo
 #undef WIN_GO
   }
   if (kv_bf16) {
-    if (ops_bf16) {
-      if (group == 1) ATT_GO((attn_mfma_kernel<1, 1, YBF16>));
-      if (group == 2) ATT_GO((attn_mfma_kernel<2, 1, YBF16>));
-      if (group == 4) ATT_GO((attn_mfma_kernel<4, 1, YBF16>));
-    } else {
-      if (group == 1) ATT_GO((attn_mfma_kernel<1, 3, YBF16>));
-      if (group == 2) ATT_GO((attn_mfma_kernel<2, 3, YBF16>));
-      if (group == 4) ATT_GO((attn_mfma_kernel<4, 3, YBF16>));
+    // Fewer workgroups than CUs (small batches, B = 1 above all): each wave's
+    // tiles are a dependent chain of HBM round trips that nothing else hides,
+    // so the MHA kernel keeps its next tile's loads in flight as well (the
+    // same arithmetic in the same order: the same bits).
+    if (group == 1 && grid.x < kAttnSmallGrid && !p.xcd_rows) {
+      AttnP ph = p;
+      ph.helpers = attn_helpers(grid.x);
+      const dim3 hgrid(grid.x * (1 + ph.helpers));
+      if (ops_bf16) hipLaunchKernelGGL((attn_mfma_kernel<1, 1, YBF16, 1>), hgrid, block, 0, s, ph);
+      else hipLaunchKernelGGL((attn_mfma_kernel<1, 3, YBF16, 1>), hgrid, block, 0, s, ph);
+      return hipGetLastError();
     }
-  } else if (kv_layout == ALTXS_KV_BF16_NATURAL) {
+    if (ops_bf16) {
+      if (group == 1) ATT_GO((attn_mfma_kernel<1, 1, YBF16, ALTXS_ATT_PF>));
+      if (group == 2) ATT_GO((attn_mfma_kernel<2, 1, YBF16, 1>));
+      if (group == 4) ATT_GO((attn_mfma_kernel<4, 1, YBF16, 1>));
+    } else {
+      if (group == 1) ATT_GO((attn_mfma_kernel<1, 3, YBF16, ALTXS_ATT_PF>));
+      if (group == 2) ATT_GO((attn_mfma_kernel<2, 3, YBF16, 1>));
+      if (group == 4) ATT_GO((attn_mfma_kernel<4, 3, YBF16, 1>));
+    }
+    return hipErrorInvalidValue;
+  }
+  // natural layouts: prefetch workgroups beside small launches as above
+  AttnP ph = p;
+  ph.helpers = p.xcd_rows ? 0 : attn_helpers(grid.x);
+  grid.x *= 1 + ph.helpers;
+#undef ATT_GO
+#define ATT_GO(K) \
+  do { hipLaunchKernelGGL(K, grid, block, 0, s, ph); return hipGetLastError(); } while (0)
+  if (kv_layout == ALTXS_KV_BF16_NATURAL) {
     if (group == 1) ATT_GO((attn_valu_kernel<1, YBF16, uint16_t>));
     if (group == 2) ATT_GO((attn_valu_kernel<2, YBF16, uint16_t>));
     if (group == 4) ATT_GO((attn_valu_kernel<4, YBF16, uint16_t>));

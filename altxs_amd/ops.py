@@ -117,6 +117,35 @@ def qgemm_stream(codes: torch.Tensor, scales: torch.Tensor, count: int, N: int, 
     return out
 
 
+def qgemv(w: DeviceQTensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[rows, N] = x[rows, K] . W^T for 1..4 fp16/bf16 rows, each row on its
+    own (VALU dot arithmetic; a row's bits depend on that row alone)."""
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"x dtype {x.dtype} not supported (fp16 or bf16)")
+    if not x.is_cuda or not x.is_contiguous() or x.shape[-1] != w.K:
+        raise ValueError("x must be a contiguous device tensor [..., K]")
+    rows = x.numel() // w.K
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (w.N,), dtype=torch.float32, device=x.device)
+    _need(out, torch.float32, "out")
+    rc = _lib.load().altxs_qgemv(ctypes.byref(w.qt), x.data_ptr(), _DT[x.dtype], rows,
+                                 out.data_ptr(), _s(x))
+    _lib.check(rc, "altxs_qgemv")
+    return out
+
+
+def qgemv_stream(codes: torch.Tensor, scales: torch.Tensor, count: int, N: int, K: int, bits: int,
+                 codes_stride: int, scales_stride: int, x: torch.Tensor,
+                 out: torch.Tensor) -> torch.Tensor:
+    """:func:`qgemv` over ``count`` packed tensors at fixed byte strides."""
+    qt = _lib.QTensor(codes.data_ptr(), scales.data_ptr(), N, K, bits, 0)
+    rows = x.numel() // K
+    rc = _lib.load().altxs_qgemv_stream(ctypes.byref(qt), count, codes_stride, scales_stride,
+                                        x.data_ptr(), _DT[x.dtype], rows, out.data_ptr(), _s(x))
+    _lib.check(rc, "altxs_qgemv_stream")
+    return out
+
+
 def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor, *,
                 W: int = 1, gate: torch.Tensor | None = None, use_xsa: bool = False,
                 y_bf16: bool = False, ops_bf16: bool = False, tiled: bool = False,

@@ -269,12 +269,14 @@ def cfg2_bench(a) -> int:
     and random fp16 group-64 scales), fp16 activations ~N(0, 1), B = 1 and 64
     rows.  One matrix is at most 0.8 MB and would sit in the 256 MB Infinity
     Cache, so the HBM figure streams >= 2 GB of distinct matrices through one
-    ``altxs_qgemm_stream`` launch (each matrix's y written to its own rows);
-    algorithmic bytes per launch = codes + scales + y of every matrix + x
-    once.  The single-call latency is ``altxs_qgemm`` on one matrix, replayed
-    from a HIP graph (cache-resident, launch included).  MFMA figures count
-    the useful 2*N*K*B flops against the dense fp16 peak (2.5 PFLOP/s); at
-    B = 1 the 16-row MFMA tiles carry 15 empty rows."""
+    ``altxs_qgemv_stream`` / ``altxs_qgemm_stream`` launch (each matrix's y
+    written to its own rows); algorithmic bytes per launch = codes + scales +
+    y of every matrix + x once.  B = 1 runs both the row GEMV (altxs_qgemv:
+    VALU dot arithmetic, the batch-1 kernel; ``value`` is its mean) and the
+    16-row MFMA tiles of altxs_qgemm (15 empty rows, for comparison); B = 64
+    runs altxs_qgemm.  The single-call latency is one matrix, replayed from a
+    HIP graph (cache-resident, launch included).  MFMA figures count the
+    useful 2*N*K*B flops against the dense fp16 peak (2.5 PFLOP/s)."""
     import ctypes
 
     import numpy as np
@@ -296,12 +298,14 @@ def cfg2_bench(a) -> int:
             codes = torch.randint(0, 256, (count * cs,), dtype=torch.uint8, device="cuda", generator=g)
             scales = (torch.rand(count * ss // 2, device="cuda", generator=g) * 0.05 + 0.001).half()
             qt = _lib.QTensor(codes.data_ptr(), scales.data_ptr(), N, K, bits, 0)
-            for B in (1, 64):
+            for api, B in (("qgemv", 1), ("qgemm", 1), ("qgemm", 64)):
                 x = torch.randn(B, K, device="cuda", generator=g).half()
                 y = torch.empty(count, B, N, dtype=torch.float32, device="cuda")
-                run = lambda: _lib.check(L.altxs_qgemm_stream(  # noqa: E731
+                fn_stream = L.altxs_qgemv_stream if api == "qgemv" else L.altxs_qgemm_stream
+                fn_one = L.altxs_qgemv if api == "qgemv" else L.altxs_qgemm
+                run = lambda: _lib.check(fn_stream(  # noqa: E731
                     ctypes.byref(qt), count, cs, ss, x.data_ptr(), _lib.F16, B, y.data_ptr(), stream()),
-                    "altxs_qgemm_stream")
+                    f"altxs_{api}_stream")
                 run()
                 torch.cuda.synchronize()
                 # spot check: the first and last matrix against dequant + fp64 matmul
@@ -312,7 +316,8 @@ def cfg2_bench(a) -> int:
                     ref = x.double() @ w.double().T
                     err = (y[i].double() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
                     if err > 1e-3:
-                        raise RuntimeError(f"cfg2 check failed: [{N},{K}] b={bits} B={B} matrix {i}: {err:.2e}")
+                        raise RuntimeError(f"cfg2 check failed: {api} [{N},{K}] b={bits} B={B} matrix {i}: "
+                                           f"{err:.2e}")
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 reps = 5
                 e0.record()
@@ -325,8 +330,8 @@ def cfg2_bench(a) -> int:
                 flops = 2.0 * N * K * B * count
                 # single call on one matrix, from a graph of 50 calls
                 y1 = torch.empty(B, N, dtype=torch.float32, device="cuda")
-                one = lambda: L.altxs_qgemm(ctypes.byref(qt), x.data_ptr(), _lib.F16, B,  # noqa: E731
-                                            y1.data_ptr(), stream())
+                one = lambda: fn_one(ctypes.byref(qt), x.data_ptr(), _lib.F16, B,  # noqa: E731
+                                     y1.data_ptr(), stream())
                 one()
                 torch.cuda.synchronize()
                 gr = torch.cuda.CUDAGraph()
@@ -340,21 +345,22 @@ def cfg2_bench(a) -> int:
                 e1.record()
                 torch.cuda.synchronize()
                 us1 = e0.elapsed_time(e1) / 50 * 1e3
-                r = {"N": N, "K": K, "bits": bits, "B": B, "matrices": count,
+                r = {"api": api, "N": N, "K": K, "bits": bits, "B": B, "matrices": count,
                      "stream_bytes": int(nbytes), "ms_per_launch": round(ms, 4),
                      "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                      "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
                      "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4),
                      "single_call_us": round(us1, 2)}
-                log(f"[{N},{K}] b={bits} B={B}: {count} matrices, {ms:.3f} ms, {r['GBps']:.0f} GB/s "
+                log(f"{api} [{N},{K}] b={bits} B={B}: {count} matrices, {ms:.3f} ms, {r['GBps']:.0f} GB/s "
                     f"({100 * r['hbm_frac']:.1f}% HBM), {r['TFLOPs']:.1f} TFLOP/s; single call {us1:.2f} us")
                 results.append(r)
                 del y, y1, gr
             del codes, scales
             torch.cuda.empty_cache()
-    b1 = [r for r in results if r["B"] == 1]
+    b1 = [r for r in results if r["B"] == 1 and r["api"] == "qgemv"]
     value = float(np.mean([r["GBps"] for r in b1]))
+    mfma_b1 = float(np.mean([r["GBps"] for r in results if r["B"] == 1 and r["api"] == "qgemm"]))
     out = {
         "metric": "cfg2 fused dequant-GEMV HBM throughput (B=1, >=2 GB of distinct packed matrices, "
                   "mean over 512x2048 / 2048x512 and 2/3/4/6 bits)",
@@ -363,9 +369,10 @@ def cfg2_bench(a) -> int:
         "data": "synthetic",
         "config": {"workload": "cfg2: packed group-64 weights, fp16 scales, fp16 activations, B in {1, 64}",
                    "stream_gb": a.cfg2_gb},
-        "roofline": {"kernel": "gemm_kernel (altxs_qgemm_stream), B=1", "bound": "hbm",
+        "roofline": {"kernel": "qgemv_kernel (altxs_qgemv_stream), B=1", "bound": "hbm",
                      "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+        "mfma_tile_b1_GBps": round(mfma_b1, 1),
         "results": results,
     }
     print(json.dumps(out), flush=True)

@@ -126,6 +126,26 @@ int32_t altxs_qgemm_stream(const AltxsQTensor *w, int64_t count, int64_t codes_s
                            int64_t rows, float *y, altxs_stream_t stream);
 
 /*
+ * y[rows, N] = x[rows, K] . W^T for 1 <= rows <= 4, each row on its own: the
+ * row-independent GEMV of the reference's `_gemv_row_tiles` / gemv_rows
+ * (src/xsa_ttt/ac_gemv.py:26-58, 391-425: one program per row and column
+ * tile), on packed weights (bits in {2,3,4,6}) with fp16 or bf16 x.  VALU
+ * arithmetic (each code decoded once into a 16-bit pair, one v_dot2 per pair
+ * and row, fp32 accumulation, group centre taken out with the group's sum of
+ * x), so its bits are not altxs_qgemm's; a row's result depends on that row
+ * alone.  For the bandwidth-bound batch-1 regime: each weight is decoded once
+ * for all rows and with ~1-2 VALU instructions.
+ */
+int32_t altxs_qgemv(const AltxsQTensor *w, const void *x, int32_t x_dtype, int64_t rows,
+                    float *y, altxs_stream_t stream);
+
+/* altxs_qgemv over `count` tensors at fixed byte strides (as
+ * altxs_qgemm_stream); y is [count, rows, N]. */
+int32_t altxs_qgemv_stream(const AltxsQTensor *w, int64_t count, int64_t codes_stride,
+                           int64_t scales_stride, const void *x, int32_t x_dtype,
+                           int64_t rows, float *y, altxs_stream_t stream);
+
+/*
  * y[rows, N] = (RMSNorm(x[rows, K]) * ln_scale) . W^T: the step's normalised
  * prologue (x fp32, eps added to the mean square, one fixed reduction order
  * per row) in front of the dequant GEMM; bits in {2,3,4,6,16}, K in {256,

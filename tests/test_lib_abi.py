@@ -54,6 +54,16 @@ def test_bad_arguments_return_errors_without_gpu():
     fake = ctypes.c_void_p(1 << 20)
     assert L.altxs_pack_dense32(None, fake, 16, 256, 256, fake, 16 * 256 * 4, None) == -1
     assert b"bytes" in L.altxs_last_error()
+    # the row GEMV takes 1..4 fp16/bf16 rows of packed (not dense) weights
+    qt = _lib.QTensor(1 << 20, 1 << 20, 512, 2048, 4, 0)
+    for rows, xdt, bits, what in ((5, _lib.F16, 4, b"rows"), (0, _lib.F16, 4, b"rows"),
+                                  (1, _lib.F32, 4, b"fp16 or bf16"), (1, _lib.F16, 16, b"bits")):
+        qt.bits = bits
+        assert L.altxs_qgemv(ctypes.byref(qt), fake, xdt, rows, fake, None) == -1
+        assert what in L.altxs_last_error(), L.altxs_last_error()
+    qt.bits = 4
+    assert L.altxs_qgemv_stream(ctypes.byref(qt), 2, 512 * 1024, 16, fake, _lib.F16, 1, fake, None) == -1
+    assert b"strides" in L.altxs_last_error()
 
 
 def test_dense_sizes():
