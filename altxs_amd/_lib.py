@@ -12,7 +12,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libaltxs_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MAX_LAYERS = 32
 MAX_SLOTS = 64
@@ -44,6 +44,7 @@ EXPORTS = (
     "altxs_scale_cum_f64",
     "altxs_softmax_cdf",
     "altxs_dequant",
+    "altxs_expand_codes",
     "altxs_qgemm",
     "altxs_qgemm_stream",
     "altxs_qgemv",
@@ -73,7 +74,8 @@ class AltxsLibraryError(RuntimeError):
 class QTensor(ctypes.Structure):
     _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
                 ("N", ctypes.c_int64), ("K", ctypes.c_int64),
-                ("bits", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("bits", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("expanded", ctypes.c_void_p)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -166,6 +168,8 @@ def load():
     L.altxs_softmax_cdf.argtypes = [p, i64, i64, i32, p, p, p]
     L.altxs_dequant.restype = i32
     L.altxs_dequant.argtypes = [ctypes.POINTER(QTensor), p, p]
+    L.altxs_expand_codes.restype = i32
+    L.altxs_expand_codes.argtypes = [ctypes.POINTER(QTensor), p, p]
     L.altxs_qgemm.restype = i32
     L.altxs_qgemm.argtypes = [ctypes.POINTER(QTensor), p, i32, i64, p, p]
     L.altxs_qgemm_stream.restype = i32

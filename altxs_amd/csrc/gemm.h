@@ -57,6 +57,16 @@ template <> struct Planes<16> { static constexpr int P0 = 16, P1 = 0; };
 // v = 3 * kb + plane: one plane in registers at a time, the A slice of block
 // kb applied to each.
 template <> struct Planes<32> { static constexpr int P0 = 16, P1 = 0; };
+// BITS == kExpBits (8; internal, not a C-ABI width): the expanded form of a
+// packed tensor -- the bf16 values (code - centre), exact, N*K*2 bytes written
+// by altxs_expand_codes -- with the packed tensor's group scales.  Each 16 x
+// 256 block is stored k-step-major: k-step s's 1 KB holds lane l's 16-byte B
+// operand at 16 l, so one wave load reads 1 KB of consecutive bytes.  The MFMAs see exactly the operands the packed path
+// builds from the codes, so results are the same bits; the large-tile kernels
+// read them straight into B operands instead of decoding codes once per 64
+// rows (the decode is most of their VALU work).
+constexpr int kExpBits = 8;
+template <> struct Planes<8> { static constexpr int P0 = 16, P1 = 0; };
 // virtual blocks per 16 x 256 block of weights
 template <int BITS> __host__ __device__ constexpr int vpb() { return BITS == 32 ? 3 : 1; }
 
@@ -211,7 +221,7 @@ __device__ __forceinline__ float ubyte_f32(uint32_t x) {
 // (planes_to6 already applied).
 template <int BITS>
 __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
-  if constexpr (BITS == 16 || BITS == 32)
+  if constexpr (BITS == 16 || BITS == 32 || BITS == kExpBits)
     return __builtin_bit_cast(bf16x8, u32x4{p0[4 * s], p0[4 * s + 1], p0[4 * s + 2], p0[4 * s + 3]});
   if constexpr (BITS == 2 || BITS == 3) {
     static_assert(Planes<BITS>::P0 == 2, "2-bit low plane: k-step s is bits 16 (s & 1) + 2i of p0[s >> 1]");
@@ -255,7 +265,7 @@ __device__ __forceinline__ bf16x8 b_op_bf16(const uint32_t* p0, const uint32_t* 
 
 template <int BITS>
 __device__ __forceinline__ f16x8 b_op_f16(const uint32_t* p0, const uint32_t* p1, int s, int bits) {
-  static_assert(BITS != 16, "dense bf16 weights take bf16 or fp32 activations");
+  static_assert(BITS != 16 && BITS != kExpBits, "bf16 weight values take bf16 or fp32 activations");
   if constexpr (BITS == 2 || BITS == 3) {  // the bf16 path's byte table, with fp16 bytes
     const uint32_t f0 = (p0[s >> 1] >> (16 * (s & 1))) & 0xFFFFu;
     uint32_t ca = spread2to8(f0 & 0xFFu), cb = spread2to8(f0 >> 8);
@@ -351,15 +361,21 @@ __device__ __forceinline__ void load_w(Blk<BITS, AM, ADIRECT>& b, const QT& w, i
     for (int i = 0; i < 4; ++i) { b.p0[i] = x[i]; b.p0[4 + i] = y[i]; b.p1[i] = z[i]; }
     const u32x2 sv = *(const u32x2*)(w.scales + bi * 64 + (lane & 15) * 4);
     b.sc[0] = sv[0]; b.sc[1] = sv[1];
-  } else if constexpr (BITS == 16) {
-    const u32x4* a0 = (const u32x4*)(w.codes + bi * (512 * 16)) + lane * 8;
+  } else if constexpr (BITS == 16 || BITS == kExpBits) {
+    // bits 16: lane-major (a lane's 128 bytes together); expanded: k-step-major
+    const u32x4* a0 = (const u32x4*)(w.codes + bi * (512 * 16)) + (BITS == 16 ? lane * 8 : lane);
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const u32x4 x = a0[v];
+      const u32x4 x = a0[BITS == 16 ? v : 64 * v];
 #pragma unroll
       for (int i = 0; i < 4; ++i) b.p0[4 * v + i] = x[i];
     }
-    b.sc[0] = b.sc[1] = 0u;
+    if constexpr (BITS == kExpBits) {
+      const u32x2 sv = *(const u32x2*)(w.scales + bi * 64 + (lane & 15) * 4);
+      b.sc[0] = sv[0]; b.sc[1] = sv[1];
+    } else {
+      b.sc[0] = b.sc[1] = 0u;
+    }
   } else {
     constexpr int P0 = Planes<BITS>::P0, P1 = Planes<BITS>::P1;
     const uint8_t* blk = w.codes + bi * (512 * BITS);
@@ -815,9 +831,41 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = tot[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  Blk<BITS, A_BF16, false> wb[2], wn[2];
-  load_w(wb[0], w, nb0, 0, lane);
-  load_w(wb[1], w, nb0 + 1, 0, lane);
+  constexpr bool EXP = BITS == kExpBits;
+  static_assert(!EXP || AM == A_BF16, "expanded codes are bf16 values");
+  Blk<EXP ? 4 : BITS, A_BF16, false> wb[2], wn[2];
+  // expanded codes: B operands stream from memory one group ahead through a
+  // ring of two register slots (group g of every k-block in slot g % 2; a
+  // deeper ring spills here, next to the K-slice totals)
+  constexpr int NSLOT = 2, PF = 1;
+  u32x4 eb[EXP ? NSLOT : 1][2][2];  // [slot][j][ss]
+  uint32_t esc[2][2], escn[2][2];   // [j]: this / the next k-block's group scales
+  auto load_grp = [&](int slot, int kb, int g) {
+    if constexpr (EXP) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const u32x4* p = (const u32x4*)(w.codes + ((size_t)(nb0 + j) * KB + kb) * 8192) + lane;
+        eb[slot][j][0] = p[64 * (2 * g)];
+        eb[slot][j][1] = p[64 * (2 * g + 1)];
+      }
+    }
+  };
+  auto load_sc = [&](uint32_t (&d)[2][2], int kb) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x2 sv = *(const u32x2*)(w.scales + ((size_t)(nb0 + j) * KB + kb) * 64 + (lane & 15) * 4);
+      d[j][0] = sv[0];
+      d[j][1] = sv[1];
+    }
+  };
+  if constexpr (EXP) {
+    load_sc(esc, 0);
+#pragma unroll
+    for (int g = 0; g < PF; ++g) load_grp(g, 0, g);
+  } else {
+    load_w(wb[0], w, nb0, 0, lane);
+    load_w(wb[1], w, nb0 + 1, 0, lane);
+  }
 
   // A rows m0.. of k-block kb into LDS buffer kb & 1 by global->LDS DMA: one
   // instruction moves two rows (lane i: row 2q + i / 32, its LDS chunk i % 32
@@ -842,15 +890,20 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
   for (int kb = 0; kb < KB; ++kb) {
     if (kb + 1 < KB) {  // next k-block's A rows and weights fly during this one's MFMAs
       dma_a_blk(kb + 1);
-      load_w(wn[0], w, nb0, kb + 1, lane);
-      load_w(wn[1], w, nb0 + 1, kb + 1, lane);
+      if constexpr (EXP) {
+        load_sc(escn, kb + 1);
+      } else {
+        load_w(wn[0], w, nb0, kb + 1, lane);
+        load_w(wn[1], w, nb0 + 1, kb + 1, lane);
+      }
     }
     const uint16_t* Ab = As + (kb & 1) * (BIG_M * 256);
     float scale[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      scale[j][0] = half_lo(wb[j].sc[0]); scale[j][1] = half_hi(wb[j].sc[0]);
-      scale[j][2] = half_lo(wb[j].sc[1]); scale[j][3] = half_hi(wb[j].sc[1]);
+      const uint32_t s0 = EXP ? esc[j][0] : wb[j].sc[0], s1 = EXP ? esc[j][1] : wb[j].sc[1];
+      scale[j][0] = half_lo(s0); scale[j][1] = half_hi(s0);
+      scale[j][2] = half_lo(s1); scale[j][3] = half_hi(s1);
     }
     using BOp = std::conditional_t<AM == A_F16, f16x8, bf16x8>;
     auto mfma = [](u32x4 a, BOp b, f32x4 c) {
@@ -862,13 +915,23 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       BOp bo[2][2];
+      if constexpr (EXP) {
+        // group g + PF of this k-block, or group g + PF - 4 of the next one
+        if (g + PF < 4) load_grp((g + PF) % NSLOT, kb, g + PF);
+        else if (kb + 1 < KB) load_grp((g + PF) % NSLOT, kb + 1, g + PF - 4);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int ss = 0; ss < 2; ++ss) {
-          if constexpr (AM == A_F16) bo[j][ss] = b_op_f16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
-          else bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
-        }
+          for (int ss = 0; ss < 2; ++ss) bo[j][ss] = __builtin_bit_cast(BOp, eb[g % NSLOT][j][ss]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int ss = 0; ss < 2; ++ss) {
+            if constexpr (AM == A_F16) bo[j][ss] = b_op_f16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+            else bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+          }
+      }
       // the 2*MB independent MFMA chains of the group first, then the scaled
       // accumulation (the same per-block arithmetic as compute_blk; issuing the
       // chains back to back keeps the matrix pipe busy instead of waiting on
@@ -915,8 +978,16 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(QT w, int R, const uin
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (kb + 1 < KB) {
-      wb[0] = wn[0];
-      wb[1] = wn[1];
+      if constexpr (EXP) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          esc[j][0] = escn[j][0];
+          esc[j][1] = escn[j][1];
+        }
+      } else {
+        wb[0] = wn[0];
+        wb[1] = wn[1];
+      }
     }
   }
   // (the last barrier above also frees As for the output tiles)
@@ -1009,16 +1080,55 @@ __global__ __launch_bounds__(256, 2) void gemm_band_kernel(QT w, int R, const ui
   const int m0 = ry * BIG_M, NT = w.N / BIG_N, GX = gridDim.x;
   auto nblk = [&](int ct) { return ct * (BIG_N / 16) + 2 * wave; };  // this wave's first weight block
   // the first column tile's weights fly while the band arrives
-  using WBlk = Blk<BITS, A_BF16, false>;
-  WBlk wt[KB][2];  // a column tile's weights, both k-blocks
-  auto load_tile_w = [&](WBlk(&d)[KB][2], int ct) {
+  constexpr bool EXP = BITS == kExpBits;
+  static_assert(!EXP || AM == A_BF16, "expanded codes are bf16 values");
+  using WBlk = Blk<EXP ? 4 : BITS, A_BF16, false>;
+  WBlk wt[EXP ? 1 : KB][2];  // a column tile's weights, both k-blocks (packed codes)
+  auto load_tile_w = [&](WBlk(&d)[EXP ? 1 : KB][2], int ct) {
+    if constexpr (!EXP) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      load_w(d[kb][0], w, nblk(ct), kb, lane);
-      load_w(d[kb][1], w, nblk(ct) + 1, kb, lane);
+      for (int kb = 0; kb < KB; ++kb) {
+        load_w(d[kb][0], w, nblk(ct), kb, lane);
+        load_w(d[kb][1], w, nblk(ct) + 1, kb, lane);
+      }
+    }
+  };
+  // Expanded codes: a tile's eight groups (k-block kb, group g: q = 4 kb + g)
+  // of B operands stream from memory PF groups ahead through a ring of NSLOT
+  // register slots (slot q % NSLOT); the next tile's scales and first groups
+  // are issued in the epilogue, as the packed weights are.
+  constexpr int GPT = KB * 4, NSLOT = 4, PF = 3;
+  u32x4 eb[EXP ? NSLOT : 1][2][2];  // [slot][j][ss]
+  uint32_t esc[EXP ? KB : 1][2][2];   // [kb][j]: the group scales (fp16 pairs)
+  auto load_grp = [&](int slot, int ct, int q) {
+    if constexpr (EXP) {
+      const int kb = q / 4, g = q % 4;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const u32x4* p = (const u32x4*)(w.codes + ((size_t)(nblk(ct) + j) * KB + kb) * 8192) + lane;
+        eb[slot][j][0] = p[64 * (2 * g)];
+        eb[slot][j][1] = p[64 * (2 * g + 1)];
+      }
+    }
+  };
+  auto load_scales = [&](int ct) {
+    if constexpr (EXP) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const u32x2 sv = *(const u32x2*)(w.scales + ((size_t)(nblk(ct) + j) * KB + kb) * 64 + (lane & 15) * 4);
+          esc[kb][j][0] = sv[0];
+          esc[kb][j][1] = sv[1];
+        }
     }
   };
   load_tile_w(wt, cx);
+  if constexpr (EXP) {
+    load_scales(cx);
+#pragma unroll
+    for (int q = 0; q < PF; ++q) load_grp(q, cx, q);
+  }
 
   if constexpr (Pro::kStage) {
     // the stage's prologue in place of a separate row-normalisation launch:
@@ -1066,23 +1176,34 @@ __global__ __launch_bounds__(256, 2) void gemm_band_kernel(QT w, int R, const ui
       for (int j = 0; j < 2; ++j) acc[i][j] = tot[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      const WBlk(&wb)[2] = wt[kb];
+      const WBlk(&wb)[2] = wt[EXP ? 0 : kb];
       float scale[2][4];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        scale[j][0] = half_lo(wb[j].sc[0]); scale[j][1] = half_hi(wb[j].sc[0]);
-        scale[j][2] = half_lo(wb[j].sc[1]); scale[j][3] = half_hi(wb[j].sc[1]);
+        const uint32_t s0 = EXP ? esc[EXP ? kb : 0][j][0] : wb[j].sc[0];
+        const uint32_t s1 = EXP ? esc[EXP ? kb : 0][j][1] : wb[j].sc[1];
+        scale[j][0] = half_lo(s0); scale[j][1] = half_hi(s0);
+        scale[j][2] = half_lo(s1); scale[j][3] = half_hi(s1);
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         BOp bo[2][2];
+        if constexpr (EXP) {
+          const int q = 4 * kb + g, qn = q + PF;
+          if (qn < GPT) load_grp(qn % NSLOT, ct, qn);  // (the next tile's first groups: in the epilogue)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int ss = 0; ss < 2; ++ss) {
-            if constexpr (AM == A_F16) bo[j][ss] = b_op_f16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
-            else bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
-          }
+            for (int ss = 0; ss < 2; ++ss) bo[j][ss] = __builtin_bit_cast(BOp, eb[q % NSLOT][j][ss]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int ss = 0; ss < 2; ++ss) {
+              if constexpr (AM == A_F16) bo[j][ss] = b_op_f16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+              else bo[j][ss] = b_op_bf16<BITS>(wb[j].p0, wb[j].p1, 2 * g + ss, BITS);
+            }
+        }
         f32x4 t[MB][2];
 #pragma unroll
         for (int ss = 0; ss < 2; ++ss) {
@@ -1136,7 +1257,14 @@ __global__ __launch_bounds__(256, 2) void gemm_band_kernel(QT w, int R, const ui
       __syncthreads();
       // the next column tile's weights fly during the epilogue (issued behind
       // the barrier so they do not compete with this tile's operands)
-      if (mb == 0 && ct + GX < NT) load_tile_w(wt, ct + GX);
+      if (mb == 0 && ct + GX < NT) {
+        load_tile_w(wt, ct + GX);
+        load_scales(ct + GX);
+        if constexpr (EXP) {
+#pragma unroll
+          for (int q = 0; q < PF; ++q) load_grp(q, ct + GX, q);
+        }
+      }
       if (r0 < R) {  // uniform
         bool done = false;
         if constexpr (epi_has_strip<Epi>::value) {
@@ -1212,7 +1340,9 @@ hipError_t launch_gemm_big_t(const QT& w, int R, const uint16_t* A, const Epi& e
 }
 
 // Usable for a tensor when its shape fits the tiling (else use gemm_task).
-inline bool big_gemm_fits(const QT& w) { return w.bits <= 6 && w.N % BIG_N == 0 && w.K % 256 == 0; }
+inline bool big_gemm_fits(const QT& w) {
+  return (w.bits <= 6 || w.bits == kExpBits) && w.N % BIG_N == 0 && w.K % 256 == 0;
+}
 
 // (NB, KS) must be the 16-row path's choice for this tensor (pick_ks).
 template <int NB, int KS, class Epi>
@@ -1223,6 +1353,7 @@ hipError_t launch_gemm_big(int bits, const QT& w, int R, const uint16_t* A, cons
     case 3: return launch_gemm_big_t<3, NB, KS>(w, R, A, epi, s);
     case 4: return launch_gemm_big_t<4, NB, KS>(w, R, A, epi, s);
     case 6: return launch_gemm_big_t<6, NB, KS>(w, R, A, epi, s);
+    case kExpBits: return launch_gemm_big_t<kExpBits, NB, KS>(w, R, A, epi, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1251,6 +1382,8 @@ hipError_t launch_gemm_band_norm(int bits, const QT& w, int R, const Pro& pro, c
     case 3: return launch_gemm_band_t<3, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
     case 4: return launch_gemm_band_t<4, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
     case 6: return launch_gemm_band_t<6, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
+    case kExpBits:
+      return launch_gemm_band_t<kExpBits, NB, KS, Epi, A_BF16, Pro>(w, R, nullptr, epi, s, 1, 0, 0, pro);
     default: return hipErrorInvalidValue;
   }
 }

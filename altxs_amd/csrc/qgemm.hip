@@ -29,6 +29,21 @@ __global__ __launch_bounds__(64) void dequant_kernel(QT w, float* __restrict__ o
   }
 }
 
+// One wave per 16x256 block: lane l writes the bf16 B operands of its eight
+// k-steps (the packed path's b_op_bf16, so the very values its MFMAs see),
+// k-step s at 16-byte slot 64 s + l of the block.
+template <int BITS>
+__global__ __launch_bounds__(64) void expand_kernel(QT w, u32x4* __restrict__ out) {
+  const int lane = threadIdx.x;
+  const int KB = w.K >> 8;
+  const int nb = blockIdx.x / KB, kb = blockIdx.x % KB;
+  Blk<BITS, A_BF16, false> b;
+  load_w(b, w, nb, kb, lane);
+  u32x4* o = out + (size_t)blockIdx.x * 512 + lane;  // 8 KB per block
+#pragma unroll
+  for (int s = 0; s < 8; ++s) o[64 * s] = __builtin_bit_cast(u32x4, b_op_bf16<BITS>(b.p0, b.p1, s, BITS));
+}
+
 int check_qt(const AltxsQTensor* w, const char* who, bool dense_ok) {
   ALTXS_REQUIRE(w && w->codes && (w->scales || w->bits == 16 || w->bits == 32), "%s: null tensor", who);
   ALTXS_REQUIRE(w->bits == 2 || w->bits == 3 || w->bits == 4 || w->bits == 6 ||
@@ -122,6 +137,23 @@ extern "C" int32_t altxs_dequant(const AltxsQTensor* w, float* out, altxs_stream
     case 3: hipLaunchKernelGGL(dequant_kernel<3>, grid, block, 0, s, q, out); break;
     case 4: hipLaunchKernelGGL(dequant_kernel<4>, grid, block, 0, s, q, out); break;
     case 6: hipLaunchKernelGGL(dequant_kernel<6>, grid, block, 0, s, q, out); break;
+  }
+  ALTXS_CHECK_HIP(hipGetLastError());
+  return ALTXS_OK;
+}
+
+extern "C" int32_t altxs_expand_codes(const AltxsQTensor* w, void* out, altxs_stream_t stream) {
+  int rc = check_qt(w, "altxs_expand_codes", false);
+  if (rc) return rc;
+  ALTXS_REQUIRE(out && ((uintptr_t)out & 15) == 0, "altxs_expand_codes: out must be 16-byte aligned");
+  QT q = to_qt(w);
+  dim3 grid((unsigned)((q.N / 16) * (q.K / 256))), block(64);
+  hipStream_t s = (hipStream_t)stream;
+  switch (w->bits) {
+    case 2: hipLaunchKernelGGL(expand_kernel<2>, grid, block, 0, s, q, (u32x4*)out); break;
+    case 3: hipLaunchKernelGGL(expand_kernel<3>, grid, block, 0, s, q, (u32x4*)out); break;
+    case 4: hipLaunchKernelGGL(expand_kernel<4>, grid, block, 0, s, q, (u32x4*)out); break;
+    case 6: hipLaunchKernelGGL(expand_kernel<6>, grid, block, 0, s, q, (u32x4*)out); break;
   }
   ALTXS_CHECK_HIP(hipGetLastError());
   return ALTXS_OK;

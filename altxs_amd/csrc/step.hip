@@ -161,7 +161,27 @@ int check_tensor(const AltxsQTensor& t, int64_t N, int64_t K, const char* what, 
                 "fp32 activations", li, what);
   ALTXS_REQUIRE(((uintptr_t)t.codes & 15) == 0 && ((uintptr_t)t.scales & 7) == 0,
                 "altxs_step: layer %d %s: misaligned", li, what);
+  ALTXS_REQUIRE(!t.expanded || (!dense && ((uintptr_t)t.expanded & 15) == 0),
+                "altxs_step: layer %d %s: expanded values need a packed width and 16-byte alignment", li,
+                what);
   return ALTXS_OK;
+}
+
+// A tensor as the large-tile kernels read it: its expanded values (the same
+// operands, without the decoding) when the caller supplies them.  Used by the
+// K = 512 row-band stages QKV, out-projection and MLP up, whose expanded
+// weights (<= 1.5 MB) stay in an XCD's L2 (cfg4: 585 / 174 / 419 us against
+// 640 / 180 / 495 packed).  The MLP down-projection (K = 2048 tiles, whose
+// k-block barriers leave one group of loads in flight: 943 against 628 us)
+// and the LM head (16 MB expanded, re-read from the memory-side cache by
+// every row band: 5.10 against 4.71 ms) stay on the packed codes.
+QT qt_big(const AltxsQTensor& t) {
+  QT q = qt_of(t);
+  if (t.expanded) {
+    q.codes = (const uint8_t*)t.expanded;
+    q.bits = kExpBits;
+  }
+  return q;
 }
 
 int validate(const AltxsStepDesc* d) {
@@ -356,12 +376,12 @@ struct StepRun {
     EpiQKV epi{};
     qkv_parts(G, s, pro, epi);
     if (big(R, L.qkv) && !S.lora_q_a) {
-      const QT q = qt_of(L.qkv);
-      if (band_norm_fits(q)) return launch_gemm_band_norm<4, 1>(L.qkv.bits, q, R, pro, epi, st);
+      const QT q = qt_big(L.qkv);
+      if (band_norm_fits(q)) return launch_gemm_band_norm<4, 1>(q.bits, q, R, pro, epi, st);
       // normalised rows in Y (free until the attention)
       hipError_t e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st);
       if (e != hipSuccess) return e;
-      return launch_gemm_big<4, 1>(L.qkv.bits, qt_of(L.qkv), R, (const uint16_t*)w.Y, epi, st);
+      return launch_gemm_big<4, 1>(q.bits, q, R, (const uint16_t*)w.Y, epi, st);
     }
     return launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
                                       pro, epi, 0, st);
@@ -419,7 +439,7 @@ struct StepRun {
     {  // out-projection + attention residual
       EpiO epi{base_s, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
       if (big(R, L.o))
-        e = launch_gemm_big4(kKsO, L.o.bits, qt_of(L.o), R, (const uint16_t*)w.Y, epi, st);
+        e = launch_gemm_big4(kKsO, qt_big(L.o).bits, qt_big(L.o), R, (const uint16_t*)w.Y, epi, st);
       else
         // two K-slices (K = 512) on one 16-column block per task: twice the
         // workgroups of (2, 2) at half the size, same per-block arithmetic, so
@@ -435,10 +455,10 @@ struct StepRun {
       ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       EpiUp epi{w.HB, d->F, hb16};
       if (big(R, L.up) && band_norm_fits(qt_of(L.up))) {
-        e = launch_gemm_band_norm4(kKsUp, L.up.bits, qt_of(L.up), R, pro, epi, st);
+        e = launch_gemm_band_norm4(kKsUp, qt_big(L.up).bits, qt_big(L.up), R, pro, epi, st);
       } else if (big(R, L.up)) {  // normalised rows in Y (the out-projection has read it)
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
-        e = launch_gemm_big4(kKsUp, L.up.bits, qt_of(L.up), R, (const uint16_t*)w.Y, epi, st);
+        e = launch_gemm_big4(kKsUp, qt_big(L.up).bits, qt_big(L.up), R, (const uint16_t*)w.Y, epi, st);
       } else {
         e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0, st,
                              xr(G));

@@ -66,6 +66,11 @@ def _stream_ptr(device) -> int:
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 
+# Steps of at least this many rows (B x W) run the large-tile GEMMs (the
+# library's threshold), which read the expanded weight values when present.
+BIG_ROWS = 1024
+
+
 class StaticState:
     """Caller-owned device buffers of a B x W step (addresses stay fixed)."""
 
@@ -104,6 +109,8 @@ class StaticState:
         self.aux_stream = torch.cuda.Stream(device=dev) if self.split else None
         self.sync_events = (hiprt.EventArray(2 * model.n_slots + 2, timing=False)
                             if self.split else None)
+        if R >= BIG_ROWS and model.act_bf16 and model.expand is not False:
+            model.expand_codes()  # the large-tile GEMMs of this state read the expanded values
         self._descs: dict[int, _lib.StepDesc] = {}
         desc = self._desc(0)
         nbytes = _lib.load().altxs_step_workspace_bytes(ctypes.byref(desc))
@@ -163,7 +170,12 @@ class StepModel:
     """Packed weights + small params resident in HBM."""
 
     def __init__(self, synth: SynthModel, *, device="cuda", act: str = "bf16",
-                 kv: str | None = None):
+                 kv: str | None = None, expand: bool | None = None):
+        """``expand``: expanded copies of the packed tensors (altxs_expand_codes,
+        N*K*2 bytes each) for steps of at least BIG_ROWS rows, whose large-tile
+        GEMMs then read them instead of decoding codes -- the same operands, the
+        same bits.  None: made when the first such state is; False: never;
+        True: now."""
         cfg = synth.cfg
         cfg.validate()
         if act not in ("bf16", "fp32"):
@@ -204,6 +216,27 @@ class StepModel:
         self.synth = synth
         self._cos_cache: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         self._disabled = False
+        self.expand = expand
+        self._expanded = False
+        if expand:
+            self.expand_codes()
+
+    def expand_codes(self) -> None:
+        """Expanded copies of the packed QKV, out-projection and MLP-up tensors
+        (the stages whose large-row GEMMs read them; bits 2/3/4/6), once; each
+        QTensor's ``expanded`` then points at its copy."""
+        if self._expanded:
+            return
+        stream = ctypes.c_void_p(_stream_ptr(self.device))
+        for name, qt in self.qt.items():
+            if qt.bits not in (2, 3, 4, 6) or not name.endswith((".qkv", ".o", ".up")):
+                continue
+            out = torch.empty(qt.N * qt.K, dtype=torch.bfloat16, device=self.device)
+            _lib.check(self.lib.altxs_expand_codes(ctypes.byref(qt), out.data_ptr(), stream),
+                       "altxs_expand_codes")
+            self._keep.append(out)
+            qt.expanded = out.data_ptr()
+        self._expanded = True
 
     def rope(self, max_len: int, rope_len: int | None = None):
         """cos/sin rows [0, max_len) of the table warmed at ``rope_len`` (default

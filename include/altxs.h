@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define ALTXS_ABI_VERSION 6
+#define ALTXS_ABI_VERSION 7
 
 enum {
   ALTXS_OK = 0,
@@ -66,6 +66,12 @@ typedef struct AltxsQTensor {
   int64_t N, K;
   int32_t bits;
   int32_t reserved;
+  /* Optional (NULL = none; packed widths 2/3/4/6 only): the same tensor
+   * expanded by altxs_expand_codes.  In steps of at least 1024 rows (W-token
+   * windows, prefill-style scoring) the QKV, out-projection and MLP-up GEMMs
+   * read its values instead of decoding codes once per 64 rows: the same
+   * operands, the same bits (other tensors' copies are not read). */
+  const void *expanded;
 } AltxsQTensor;
 
 /*
@@ -102,6 +108,15 @@ int32_t altxs_softmax_cdf(const float *logits, int64_t rows, int64_t V, int32_t 
 /* Dense fp32 copy of a packed tensor (bits in {2,3,4,6}): out[N, K].  Replaces
  * dequantize_channels (mixed_bit_delta.py:172-229) for the group-64 format. */
 int32_t altxs_dequant(const AltxsQTensor *w, float *out, altxs_stream_t stream);
+
+/* The expanded form of a packed tensor (bits in {2,3,4,6}): out holds the
+ * bf16 values code - (2^bits - 1)/2 (exact), N*K*2 bytes, for
+ * AltxsQTensor.expanded (scales stay the packed tensor's).  Per 16 x 256
+ * block (8 KB), the 16-byte MFMA B operand of k-step s and lane l (the values
+ * a bits-16 block keeps at lane l's bytes 16 s ..) sits at 16 (64 s + l).
+ * No reference counterpart: a layout the large-row GEMMs read in place of
+ * decoding codes. */
+int32_t altxs_expand_codes(const AltxsQTensor *w, void *out, altxs_stream_t stream);
 
 /*
  * y[rows, N] = x[rows, K] . W^T with the dequantisation fused into an MFMA
