@@ -30,7 +30,11 @@ The line also carries:
 * ``step_roofline``: algorithmic bytes of the whole step / step time;
 * ``cpu_baseline``: the CPU oracle (op-for-op fp32 PyTorch restatement of the
   reference eager step, B=1 per segment as the reference runs) timed on this
-  host on a bounded sample of the same workload.
+  host on a bounded sample of the same workload;
+* ``secondary`` (default workload only; ``--no-secondary`` skips it): the other
+  regimes of the benchmark set measured in the same run, after the timed
+  region -- the batch-1 decode step at ctx 2048, cfg4 chunk scoring (64 x 2048
+  tokens) and the cfg2 batch-1 row GEMV over >= 2 GB streams.
 """
 
 from __future__ import annotations
@@ -127,6 +131,91 @@ def attn_kernel_ms(model, st, reps: int = 20, replays: int = 5) -> float:
     return e0.elapsed_time(e1) / (reps * replays)
 
 
+def decode_measure(sm, B: int, ctx: int, steps: int = 50, gs: int = 10, warmup: int = 5) -> dict:
+    """The decode step of B segments at context ctx (bf16): ms per step over
+    steps // gs replays of a graph of gs steps, and the attention kernel's own
+    launch time (attn_kernel_ms)."""
+    import numpy as np
+    import torch
+
+    from altxs_amd import synth
+    from altxs_amd.model import StepModel
+
+    cfg = sm.cfg
+    model = StepModel(sm, act="bf16", kv="bf16")
+    st = model.make_static_state((ctx + 255) // 256 * 256, win=1, batch=B, want_probs=False, want_cdf=True)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    st.kv.normal_(generator=g)
+    st.pos.fill_(ctx - 1)
+    st.token.copy_(torch.from_numpy(synth.zipf_tokens(cfg.vocab_size, (B, 1)).astype(np.int32)))
+    for _ in range(warmup):
+        model.step(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(gs):
+            model.step(st)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps // gs):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (steps // gs * gs)
+    st.check_errors()
+    attn_ms = attn_kernel_ms(model, st)
+    ab = synth.algorithmic_step_bytes(sm, B, ctx, kv_bytes=2)
+    attn_bytes = ab["kv_read"] // ab["n_slots"] + B * cfg.num_heads * cfg.head_dim * 6 + B * cfg.num_heads * 4
+    del graph, st, model
+    torch.cuda.empty_cache()
+    return {"segments": B, "ctx": ctx, "ms_per_step": round(ms, 4), "value": round(B / (ms * 1e-3), 1),
+            "unit": "sym/s", "steps": steps // gs * gs, "graph_steps": gs,
+            "attn_us_per_launch": round(attn_ms * 1e3, 2),
+            "attn_GBps": round(attn_bytes / (attn_ms * 1e-3) / 1e9, 1)}
+
+
+def secondary_measures(sm) -> dict:
+    """The other regimes of the benchmark set, measured in the same run (each
+    a few seconds): the batch-1 decode step (the reference's production
+    regime), cfg4 chunk scoring (64 x 2048 tokens from position 0) and the
+    cfg2 batch-1 row GEMV over >= 2 GB streams."""
+    import numpy as np
+
+    from altxs_amd import synth
+    from altxs_amd.config import make_config
+
+    out = {}
+    try:
+        out["b1_decode_step"] = decode_measure(sm, 1, 2048)
+        log(f"secondary: batch-1 decode step {out['b1_decode_step']['ms_per_step']:.3f} ms")
+    except Exception as exc:  # noqa: BLE001
+        out["b1_decode_step"] = {"error": repr(exc)}
+    try:
+        sm4 = synth.make_model(make_config("cfg4"))
+        ms, flops = window_measure(sm4, 64, 2048, 0, "bf16", "bf16", steps=3, warmup=1)
+        tf = flops / (ms * 1e-3) / 1e12
+        out["cfg4_window"] = {"workload": "cfg4: 64 segments x 2048 tokens from position 0, bf16",
+                              "ms_per_step": round(ms, 3), "value": round(64 * 2048 / (ms * 1e-3), 1),
+                              "unit": "sym/s", "TFLOPs": round(tf, 1), "mfma_frac": round(tf / 2500.0, 4),
+                              "steps": 3}
+        log(f"secondary: cfg4 {ms:.2f} ms/step, {tf:.0f} TFLOP/s")
+    except Exception as exc:  # noqa: BLE001
+        out["cfg4_window"] = {"error": repr(exc)}
+    try:
+        res = cfg2_measure(2.0, (("qgemv", 1),))
+        gbs = float(np.mean([r["GBps"] for r in res]))
+        out["cfg2_gemv_b1"] = {"workload": "cfg2 B=1 row GEMV (altxs_qgemv_stream), >= 2 GB streams, "
+                                           "512x2048 / 2048x512 x 2/3/4/6 bits",
+                               "mean_GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                               "lines": [{k: r[k] for k in ("N", "K", "bits", "GBps")} for r in res]}
+        log(f"secondary: cfg2 row GEMV {gbs:.0f} GB/s")
+    except Exception as exc:  # noqa: BLE001
+        out["cfg2_gemv_b1"] = {"error": repr(exc)}
+    return out
+
+
 def cpu_model() -> str:
     """The host CPU's model name (lscpu "Model name", else /proc/cpuinfo)."""
     import subprocess
@@ -197,35 +286,8 @@ def window_bench(a) -> int:
     max_len = (p0 + W + 255) // 256 * 256
     cfg = make_config(a.profile)
     sm = synth.make_model(cfg, dense=a.dense)
-    model = StepModel(sm, act=a.act, kv=a.kv)
-    st = model.make_static_state(max_len, win=W, batch=B, want_probs=False, want_cdf=True)
-    if p0:
-        g = torch.Generator(device="cuda").manual_seed(0)
-        st.kv.normal_(generator=g)
-    st.pos.fill_(p0)
-    st.token.copy_(torch.from_numpy(synth.zipf_tokens(cfg.vocab_size, (B, W)).astype(np.int32)))
-    for _ in range(a.warmup):
-        model.step(st)
-    torch.cuda.synchronize()
-    st.check_errors()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        model.step(st)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(a.steps):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / a.steps
-    st.check_errors()
+    ms, flops = window_measure(sm, B, W, p0, a.act, a.kv, a.steps, a.warmup)
     R = B * W
-    body = sum(p.codes.size for n, p in sm.packed.items() if n != "emb")
-    n_slots = model.n_slots
-    attn = 4 * 64 * (W * (W + 1) // 2 + W * p0) * cfg.num_heads * B * n_slots
-    flops = 2 * R * body + 2 * R * cfg.vocab_size * cfg.model_dim + attn
     tflops = flops / (ms * 1e-3) / 1e12
     peak = 2500.0 if a.act == "bf16" else 157.3
     log(f"window W={W} x {B} segments at position {p0}: {ms:.3f} ms/step, "
@@ -261,6 +323,50 @@ def window_bench(a) -> int:
     return 0
 
 
+def window_measure(sm, B: int, W: int, p0: int, act: str, kv: str, steps: int, warmup: int):
+    """(ms per window step, useful flops per step) of B segments x W tokens
+    from position p0, timed over ``steps`` replays of a one-step HIP graph."""
+    import numpy as np
+    import torch
+
+    from altxs_amd import synth
+    from altxs_amd.model import StepModel
+
+    cfg = sm.cfg
+    max_len = (p0 + W + 255) // 256 * 256
+    model = StepModel(sm, act=act, kv=kv)
+    st = model.make_static_state(max_len, win=W, batch=B, want_probs=False, want_cdf=True)
+    if p0:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        st.kv.normal_(generator=g)
+    st.pos.fill_(p0)
+    st.token.copy_(torch.from_numpy(synth.zipf_tokens(cfg.vocab_size, (B, W)).astype(np.int32)))
+    for _ in range(warmup):
+        model.step(st)
+    torch.cuda.synchronize()
+    st.check_errors()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model.step(st)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    st.check_errors()
+    R = B * W
+    body = sum(p.codes.size for n, p in sm.packed.items() if n != "emb")
+    attn = 4 * 64 * (W * (W + 1) // 2 + W * p0) * cfg.num_heads * B * model.n_slots
+    flops = 2 * R * body + 2 * R * cfg.vocab_size * cfg.model_dim + attn
+    del graph, st, model
+    torch.cuda.empty_cache()
+    return ms, flops
+
+
 def cfg2_bench(a) -> int:
     """--cfg2: the fused dequant-GEMV/GEMM microbenchmark (benchmark config 2).
 
@@ -277,9 +383,35 @@ def cfg2_bench(a) -> int:
     runs altxs_qgemm.  The single-call latency is one matrix, replayed from a
     HIP graph (cache-resident, launch included).  MFMA figures count the
     useful 2*N*K*B flops against the dense fp16 peak (2.5 PFLOP/s)."""
+    import numpy as np
+
+    results = cfg2_measure(a.cfg2_gb, (("qgemv", 1), ("qgemm", 1), ("qgemm", 64)))
+    b1 = [r for r in results if r["B"] == 1 and r["api"] == "qgemv"]
+    value = float(np.mean([r["GBps"] for r in b1]))
+    mfma_b1 = float(np.mean([r["GBps"] for r in results if r["B"] == 1 and r["api"] == "qgemm"]))
+    out = {
+        "metric": "cfg2 fused dequant-GEMV HBM throughput (B=1, >=2 GB of distinct packed matrices, "
+                  "mean over 512x2048 / 2048x512 and 2/3/4/6 bits)",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": 5, "warmup": 1,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: packed group-64 weights, fp16 scales, fp16 activations, B in {1, 64}",
+                   "stream_gb": a.cfg2_gb},
+        "roofline": {"kernel": "qgemv_kernel (altxs_qgemv_stream), B=1", "bound": "hbm",
+                     "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+        "mfma_tile_b1_GBps": round(mfma_b1, 1),
+        "results": results,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cfg2_measure(gb: float, runs) -> list:
+    """cfg2 lines for ``runs`` = ((api, B), ...) over >= ``gb`` GB streams of
+    each shape and width (each launch checked against dequant + fp64 matmul)."""
     import ctypes
 
-    import numpy as np
     import torch
 
     from altxs_amd import _lib
@@ -287,7 +419,7 @@ def cfg2_bench(a) -> int:
     L = _lib.load()
     stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
     g = torch.Generator(device="cuda").manual_seed(2)
-    target = float(a.cfg2_gb) * 1e9
+    target = float(gb) * 1e9
     results = []
     for (N, K) in ((512, 2048), (2048, 512)):
         for bits in (2, 3, 4, 6):
@@ -298,7 +430,7 @@ def cfg2_bench(a) -> int:
             codes = torch.randint(0, 256, (count * cs,), dtype=torch.uint8, device="cuda", generator=g)
             scales = (torch.rand(count * ss // 2, device="cuda", generator=g) * 0.05 + 0.001).half()
             qt = _lib.QTensor(codes.data_ptr(), scales.data_ptr(), N, K, bits, 0)
-            for api, B in (("qgemv", 1), ("qgemm", 1), ("qgemm", 64)):
+            for api, B in runs:
                 x = torch.randn(B, K, device="cuda", generator=g).half()
                 y = torch.empty(count, B, N, dtype=torch.float32, device="cuda")
                 fn_stream = L.altxs_qgemv_stream if api == "qgemv" else L.altxs_qgemm_stream
@@ -358,25 +490,7 @@ def cfg2_bench(a) -> int:
                 del y, y1, gr
             del codes, scales
             torch.cuda.empty_cache()
-    b1 = [r for r in results if r["B"] == 1 and r["api"] == "qgemv"]
-    value = float(np.mean([r["GBps"] for r in b1]))
-    mfma_b1 = float(np.mean([r["GBps"] for r in results if r["B"] == 1 and r["api"] == "qgemm"]))
-    out = {
-        "metric": "cfg2 fused dequant-GEMV HBM throughput (B=1, >=2 GB of distinct packed matrices, "
-                  "mean over 512x2048 / 2048x512 and 2/3/4/6 bits)",
-        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": 5, "warmup": 1,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
-        "data": "synthetic",
-        "config": {"workload": "cfg2: packed group-64 weights, fp16 scales, fp16 activations, B in {1, 64}",
-                   "stream_gb": a.cfg2_gb},
-        "roofline": {"kernel": "qgemv_kernel (altxs_qgemv_stream), B=1", "bound": "hbm",
-                     "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
-        "mfma_tile_b1_GBps": round(mfma_b1, 1),
-        "results": results,
-    }
-    print(json.dumps(out), flush=True)
-    return 0
+    return results
 
 
 def coder_bench(a) -> int:
@@ -495,6 +609,9 @@ def main() -> int:
                     help="only run a plain device copy of MIB MiB five times (the known-size "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE), then exit")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the batch-1 step, cfg4 window and cfg2 row-GEMV lines the default "
+                         "workload adds under \"secondary\"")
     a = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -648,6 +765,13 @@ def main() -> int:
         log(f"cpu baseline: {cpu['value']:.1f} sym/s on {cpu['cores']} cores")
 
     value = B / (ms * 1e-3)
+    graphed = graph is not None
+    secondary = None
+    if not a.no_secondary and (a.profile, B, ctx, a.act, a.kv, a.dense, a.persistent, a.streams) == (
+            "cfg3", 64, 2048, "bf16", "bf16", False, False, 1):
+        del graph, st, model
+        torch.cuda.empty_cache()
+        secondary = secondary_measures(sm)
     out = {
         "metric": decode_metric(a.profile, B, ctx, None if a.dense else sm.bits_summary()["bpw"]),
         "value": round(value, 1),
@@ -668,8 +792,8 @@ def main() -> int:
                          + ("dense bf16 weights, " if a.dense else
                             f"{sm.bits_summary()['bpw']:.3f} bpw group-64 weights, ")
                          + f"{a.act} activations, {a.kv} KV"),
-            "segments": B, "ctx": ctx, "timing": "hip-graph" if graph is not None else "eager",
-            "graph_steps": gs if graph is not None else 0,
+            "segments": B, "ctx": ctx, "timing": "hip-graph" if graphed else "eager",
+            "graph_steps": gs if graphed else 0,
             "streams": groups, "persistent": bool(a.persistent),
             "eager_ms_per_step": round(eager_ms, 4), "kernel_event_timing": event_timing,
         },
@@ -697,6 +821,8 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    if secondary is not None:
+        out["secondary"] = secondary
     print(json.dumps(out), flush=True)
     return 0
 
