@@ -185,25 +185,55 @@ __device__ __forceinline__ void split_parts(const float (&x)[8], bf16x8 (&out)[N
   }
 }
 
+// Natural-order bf16 cache (NAT = 1): a wave stages each V tile in LDS, rows
+// of kVstRow elements (64 dims + 8 padding: the four lane groups of an operand
+// read then fall on different banks), and reads its V operands back from there.
+constexpr int kVstRow = HD + 8;
+
 // One (query row r, kv head g) of the bf16-cache attention: ATT_WAVES waves.
 // PF = 1: each wave keeps its next tile's loads in flight while it computes the
 // current one (two register buffers), for launches with one workgroup per CU;
 // the arithmetic, and so the result, is the same for PF = 0 and 1.
-template <int G, int NP, int YBF16, int PF = 0>
-__device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, MergeLds<G>& sm) {
+// NAT = 1: the cache in the natural [key][64] order (ALTXS_KV_BF16_NATURAL,
+// with the tail placement of AttnP::kv_tail): the K operand of a lane is 16
+// consecutive bytes of one key there as well; the V operand (8 keys of one
+// dim) is gathered from the wave's LDS copy of the tile (vst: ATT_WAVES x 64 x
+// kVstRow elements).  The MFMAs see the operands of the tiled layout, so both
+// layouts give the same bits for the same cache values.
+template <int G, int NP, int YBF16, int PF = 0, int NAT = 0>
+__device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, MergeLds<G>& sm,
+                                               uint16_t* vst = nullptr) {
   static_assert(TILE == 64, "the MFMA tiling below assumes 64-key tiles");
   const int b = r / a.W, t = r % a.W;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const int lg = lane >> 4, col = lane & 15;
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.seg_stride + (int64_t)g * a.max_len * HD;
+  int nat_pb = 0, nat_p = 0;  // NAT: the window's first position and the query's (key_row)
   auto load = [&](u32x4 (&kr)[8], u32x4 (&vr)[8], int T) {
-    const u32x4* kt = (const u32x4*)(kb + (int64_t)T * (TILE * HD)) + lane;
-    const u32x4* vt = (const u32x4*)(vb + (int64_t)T * (TILE * HD)) + lane;
+    if constexpr (NAT) {
+      // K operand kr[2 blk + ks]: key 16 blk + (lane & 15), dims 32 ks + 8 lg .. +8
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = __builtin_nontemporal_load(kt + 64 * i);
+      for (int blk = 0; blk < 4; ++blk) {
+        const int64_t row = key_row(a, T * TILE + 16 * blk + col, nat_pb, nat_p);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vr[i] = __builtin_nontemporal_load(vt + 64 * i);
+        for (int ks = 0; ks < 2; ++ks)
+          kr[2 * blk + ks] = __builtin_nontemporal_load((const u32x4*)(kb + row * HD + 32 * ks + 8 * lg));
+      }
+      // V rows as stored: vr[i] = key 8 i + (lane >> 3), dims 8 (lane & 7) .. +8
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t row = key_row(a, T * TILE + 8 * i + (lane >> 3), nat_pb, nat_p);
+        vr[i] = __builtin_nontemporal_load((const u32x4*)(vb + row * HD + 8 * (lane & 7)));
+      }
+    } else {
+      const u32x4* kt = (const u32x4*)(kb + (int64_t)T * (TILE * HD)) + lane;
+      const u32x4* vt = (const u32x4*)(vb + (int64_t)T * (TILE * HD)) + lane;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kr[i] = __builtin_nontemporal_load(kt + 64 * i);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vr[i] = __builtin_nontemporal_load(vt + 64 * i);
+    }
   };
   // Every workgroup of a decode launch starts (and ends) at the same time, so
   // a memory round trip after the last tile costs the whole launch: the
@@ -216,7 +246,7 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   // row had more than two keys, cause not found; with the first tile peeled
   // into a buffer of its own the rows are right but the step is slower,
   // 0.693 against 0.668 ms.  Neither is in the build.)
-  const int p_raw = a.pos[b];
+  int p_raw = a.pos[b];
   f32x4 qraw[2][2];
   {
     const float* qh = a.q + ((int64_t)r * a.H + g * G + (col % G)) * HD;
@@ -226,14 +256,21 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
       qraw[ks][1] = *(const f32x4*)(qh + 32 * ks + 8 * lg + 4);
     }
   }
+  if (NAT && a.kv_tail >= 0 && p_raw > a.kv_tail) {  // the prefix would run into the window rows
+    if (threadIdx.x == 0) flag_err(a.err, ALTXS_EDEV_POS);
+    p_raw = a.kv_tail;
+  }
   const int p = clamp_pos(a, b, t, p_raw);
+  nat_pb = p_raw;
+  nat_p = p;
   const int nkeys = p + 1;
   const int ntiles = (nkeys + TILE - 1) / TILE;
   // unconditional loads (a load on one path only would leave the compiler
   // unsure how many are in flight, and it would then wait for all of them);
   // waves past G read a valid word they do not use
   const int hx = g * G + (wave < G ? wave : G - 1);
-  const uint16_t v_raw = vb[(int64_t)(p / TILE) * (TILE * HD) + kv_tile_v(p % TILE, lane)];
+  const uint16_t v_raw = NAT ? vb[(int64_t)key_row(a, p, nat_pb, nat_p) * HD + lane]
+                             : vb[(int64_t)(p / TILE) * (TILE * HD) + kv_tile_v(p % TILE, lane)];
   const float g_raw = *(a.gate ? a.gate + (int64_t)r * a.H + hx : &kNoGate);
 
   // q operand (B of the score MFMA): column col holds head col % G; k-step ks
@@ -297,6 +334,34 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
     // k-step s covers keys of blocks 2s and 2s+1 (this lane's own scores); the
     // V register of a lane is its A operand (dims x keys) as it is the B operand
     // of P x V, and the P operand likewise
+    u32x4 vnat[NAT ? 8 : 1];
+    if constexpr (NAT) {
+      // the wave's tile into LDS as stored, then lane (lg, col)'s operand of
+      // (k-step s, dim block nb): dim 16 nb + col of keys 32 s + 16 jb + 4 lg + jr
+      // at element 4 jb + jr (the tiled layout's order)
+      uint16_t* vw = vst + wave * (TILE * kVstRow);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *(u32x4*)(vw + (8 * i + (lane >> 3)) * kVstRow + 8 * (lane & 7)) = vr[i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          uint32_t w[4];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const int e0 = 2 * h, e1 = 2 * h + 1;
+            const int k0 = 32 * s + 16 * (e0 >> 2) + 4 * lg + (e0 & 3);
+            const int k1 = 32 * s + 16 * (e1 >> 2) + 4 * lg + (e1 & 3);
+            w[h] = (uint32_t)vw[k0 * kVstRow + 16 * nb + col] | ((uint32_t)vw[k1 * kVstRow + 16 * nb + col] << 16);
+          }
+          vnat[4 * s + nb] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+      // every lane's reads are done before the next tile is stored over them
+      __builtin_amdgcn_wave_barrier();
+    }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       float pv[8];
@@ -306,7 +371,7 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
       split_parts<NP>(pv, pop);
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
-        const bf16x8 vop = __builtin_bit_cast(bf16x8, vr[4 * s + nb]);
+        const bf16x8 vop = __builtin_bit_cast(bf16x8, NAT ? vnat[NAT ? 4 * s + nb : 0] : vr[4 * s + nb]);
 #pragma unroll
         for (int k = 0; k < NP; ++k)
           acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[k], acc[nb], 0, 0, 0);

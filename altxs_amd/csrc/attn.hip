@@ -18,7 +18,10 @@
 // accumulator by its own query's alpha, with no cross-lane shuffle).
 // The K and V tiles are stored pre-swizzled (kv_tile_index below) so that every
 // lane's MFMA operand is one 16-byte load and a wave's load instruction reads
-// 1 KB of consecutive bytes.  Operand precision:
+// 1 KB of consecutive bytes.  The natural-order bf16 cache (the reference's
+// own k_pack layout) runs the same kernel with K operands read in place and
+// each V tile staged through LDS (attn_mfma_task, NAT): the same operands,
+// the same bits.  Operand precision:
 //   * OPS_BF16: q and P rounded to bf16 (the reference's production arithmetic);
 //   * fp32-faithful: q split into three bf16 parts and P into three, each part
 //     multiplied separately (sum of parts reproduces fp32 to ~2^-24).
@@ -88,10 +91,11 @@ inline int attn_helpers(unsigned pairs) {
   return pairs < kAttnSmallGrid ? (int)(kAttnSmallGrid / pairs < 16 ? kAttnSmallGrid / pairs : 16) : 0;
 }
 
-template <int G, int NP, int YBF16, int PF>
+template <int G, int NP, int YBF16, int PF, int NAT = 0>
 __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
-  if constexpr (G == 1 && PF == 1) {
+  __shared__ __attribute__((aligned(16))) uint16_t vst[NAT ? ATT_WAVES * TILE * kVstRow : 8];
+  if constexpr ((G == 1 && PF == 1) || NAT) {
     const int pairs = a.B * a.W * a.Hkv;
     if (a.helpers > 0 && (int)blockIdx.x >= pairs) {
       const int id = blockIdx.x - pairs;
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   }
   // GQA launches have G times fewer workgroups, and small launches (PF = 1)
   // too few to cover the load latency: keep two tiles per wave in flight
-  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : PF)>(a, r, g, sm);
+  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : PF), NAT>(a, r, g, sm, vst);
 }
 
 // Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
@@ -152,26 +156,16 @@ __device__ __forceinline__ float transpose_reduce(float (&v)[N], int lane) {
   return v[0];
 }
 
-// Four consecutive dims of cache row `row` (natural layout) as fp32.
-template <class KVT>
-__device__ __forceinline__ f32x4 load4(const KVT* base, int64_t row, int d) {
-  if constexpr (std::is_same<KVT, float>::value) {
-    return __builtin_nontemporal_load((const f32x4*)(base + row * HD + d));
-  } else {
-    const u32x2 w = __builtin_nontemporal_load((const u32x2*)(base + row * HD + d));
-    return f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
-  }
+// Four consecutive dims of cache row `row` (natural layout).
+__device__ __forceinline__ f32x4 load4(const float* base, int64_t row, int d) {
+  return __builtin_nontemporal_load((const f32x4*)(base + row * HD + d));
 }
-template <class KVT>
-__device__ __forceinline__ float load1(const KVT* base, int64_t row, int d) {
-  if constexpr (std::is_same<KVT, float>::value) return base[row * HD + d];
-  else return bf16_to_f32(base[row * HD + d]);
-}
+__device__ __forceinline__ float load1(const float* base, int64_t row, int d) { return base[row * HD + d]; }
 
-// KVT = float (fp32 cache) or uint16_t (bf16 values in the natural order; the
-// arithmetic is the fp32 kernel's on the widened values).
-template <int G, int YBF16, class KVT>
+// The fp32 cache (natural order; the bf16 natural order runs the MFMA kernel).
+template <int G, int YBF16>
 __global__ __launch_bounds__(ATT_THREADS) void attn_valu_kernel(AttnP a) {
+  using KVT = float;
   __shared__ MergeLds<G> sm;
   {
     const int pairs = a.B * a.W * a.Hkv;
@@ -325,19 +319,29 @@ hipError_t launch_y(const AttnP& p, int group, int kv_layout, bool ops_bf16, boo
   }
   // natural layouts: prefetch workgroups beside small launches as above
   AttnP ph = p;
-  ph.helpers = p.xcd_rows ? 0 : attn_helpers(grid.x);
+  const unsigned pairs = grid.x;
+  ph.helpers = p.xcd_rows ? 0 : attn_helpers(pairs);
   grid.x *= 1 + ph.helpers;
 #undef ATT_GO
 #define ATT_GO(K) \
   do { hipLaunchKernelGGL(K, grid, block, 0, s, ph); return hipGetLastError(); } while (0)
   if (kv_layout == ALTXS_KV_BF16_NATURAL) {
-    if (group == 1) ATT_GO((attn_valu_kernel<1, YBF16, uint16_t>));
-    if (group == 2) ATT_GO((attn_valu_kernel<2, YBF16, uint16_t>));
-    if (group == 4) ATT_GO((attn_valu_kernel<4, YBF16, uint16_t>));
+    // the MFMA kernel on the natural order (V staged through LDS): the bits
+    // of the tiled layout; one query row per workgroup at every window width
+    const bool pf = pairs < kAttnSmallGrid;  // (GQA launches keep two tiles in flight anyway)
+    if (ops_bf16) {
+      if (group == 1) { if (pf) ATT_GO((attn_mfma_kernel<1, 1, YBF16, 1, 1>)); ATT_GO((attn_mfma_kernel<1, 1, YBF16, 0, 1>)); }
+      if (group == 2) ATT_GO((attn_mfma_kernel<2, 1, YBF16, 1, 1>));
+      if (group == 4) ATT_GO((attn_mfma_kernel<4, 1, YBF16, 1, 1>));
+    } else {
+      if (group == 1) { if (pf) ATT_GO((attn_mfma_kernel<1, 3, YBF16, 1, 1>)); ATT_GO((attn_mfma_kernel<1, 3, YBF16, 0, 1>)); }
+      if (group == 2) ATT_GO((attn_mfma_kernel<2, 3, YBF16, 1, 1>));
+      if (group == 4) ATT_GO((attn_mfma_kernel<4, 3, YBF16, 1, 1>));
+    }
   } else {
-    if (group == 1) ATT_GO((attn_valu_kernel<1, YBF16, float>));
-    if (group == 2) ATT_GO((attn_valu_kernel<2, YBF16, float>));
-    if (group == 4) ATT_GO((attn_valu_kernel<4, YBF16, float>));
+    if (group == 1) ATT_GO((attn_valu_kernel<1, YBF16>));
+    if (group == 2) ATT_GO((attn_valu_kernel<2, YBF16>));
+    if (group == 4) ATT_GO((attn_valu_kernel<4, YBF16>));
   }
 #undef ATT_GO
   return hipErrorInvalidValue;

@@ -161,8 +161,8 @@ def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Te
     decode kernel) instead of the window kernel; the bits are the same.
     ``xcd_rows`` places the one-row kernel's workgroups in 8-row tiles, tile t
     on XCD t % 8 (B*W a multiple of 64; otherwise ignored); the bits are the same.
-    ``natural`` keeps bf16 k/v in their natural order (the VALU kernel reads
-    them; fp32 products of the bf16 values).  ``kv_tail_end`` (natural
+    ``natural`` keeps bf16 k/v in their natural order (the reference's k_pack
+    layout; the MFMA kernel reads them in place, with the tiled layout's bits).  ``kv_tail_end`` (natural
     layouts): window token t's K/V sit in row kv_tail_end - W + t and query t
     attends to rows [0, pos) and then to those rows (the reference's
     StaticKV tail, model.py:259-461).

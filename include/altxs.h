@@ -184,8 +184,8 @@ int32_t altxs_rms_qgemm(const AltxsQTensor *w, const float *x, int64_t rows, flo
  *   ALTXS_KV_BF16_NATURAL (2), bf16 cache in the same natural order: the
  *   reference's own packed layout k_pack[slot][kv_head][max_len][head_dim]
  *   (src/xsa_ttt/persistent_step.py:472-479), so a reference StaticKV can be a
- *   view of it.  Attention reads it with the VALU kernel (fp32 products of
- *   the bf16 values).
+ *   view of it.  Attention runs the MFMA kernel of the tiled layout on it
+ *   (V tiles transposed through LDS): the same operands, the same bits.
  *   ALTXS_KV_BF16 (1), bf16 cache: each 4096-element tile is stored in MFMA operand order so one
  *   16-byte load per lane feeds v_mfma_f32_16x16x32_bf16.  For key kt = key % 64
  *   of tile key / 64 and dim d (tile base + offset):
