@@ -185,9 +185,9 @@ __device__ __forceinline__ void split_parts(const float (&x)[8], bf16x8 (&out)[N
   }
 }
 
-// Natural-order bf16 cache (NAT = 1): a wave stages each V tile in LDS, rows
-// of kVstRow elements (64 dims + 8 padding: the four lane groups of an operand
-// read then fall on different banks), and reads its V operands back from there.
+// Natural-order bf16 cache (NAT = 1): a wave stages each V tile in LDS as
+// stored, rows of kVstRow elements (64 dims + 8 padding), and reads its V
+// operands back transposed (ds_read_b64_tr_b16).
 constexpr int kVstRow = HD + 8;
 
 // One (query row r, kv head g) of the bf16-cache attention: ATT_WAVES waves.
@@ -197,8 +197,8 @@ constexpr int kVstRow = HD + 8;
 // NAT = 1: the cache in the natural [key][64] order (ALTXS_KV_BF16_NATURAL,
 // with the tail placement of AttnP::kv_tail): the K operand of a lane is 16
 // consecutive bytes of one key there as well; the V operand (8 keys of one
-// dim) is gathered from the wave's LDS copy of the tile (vst: ATT_WAVES x 64 x
-// kVstRow elements).  The MFMAs see the operands of the tiled layout, so both
+// dim) comes from the wave's LDS copy of the tile (vst: ATT_WAVES x 64 x
+// kVstRow elements) by two transposed reads.  The MFMAs see the operands of the tiled layout, so both
 // layouts give the same bits for the same cache values.
 template <int G, int NP, int YBF16, int PF = 0, int NAT = 0>
 __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, MergeLds<G>& sm,
@@ -345,19 +345,26 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // ds_read_b64_tr_b16: lane i of a 16-lane group receives element i & 3 of
+      // the 8-byte chunks that lanes (i >> 2) + 4 j of the group address, j =
+      // 0..3.  Lane m of group lg addresses key 32 s + 16 jb + 4 lg + (m >> 2),
+      // dims 16 nb + 4 (m & 3) .. +3, so lane (lg, col) gets dim 16 nb + col of
+      // keys 32 s + 16 jb + 4 lg + j: operand elements 4 jb + j, in order.
+      typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+      const __attribute__((address_space(3))) uint16_t* vl = (const __attribute__((address_space(3))) uint16_t*)vw;
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
-          uint32_t w[4];
+          u32x2 h[2];
 #pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            const int e0 = 2 * h, e1 = 2 * h + 1;
-            const int k0 = 32 * s + 16 * (e0 >> 2) + 4 * lg + (e0 & 3);
-            const int k1 = 32 * s + 16 * (e1 >> 2) + 4 * lg + (e1 & 3);
-            w[h] = (uint32_t)vw[k0 * kVstRow + 16 * nb + col] | ((uint32_t)vw[k1 * kVstRow + 16 * nb + col] << 16);
+          for (int jb = 0; jb < 2; ++jb) {
+            const int key = 32 * s + 16 * jb + 4 * lg + (col >> 2), dim = 16 * nb + 4 * (col & 3);
+            h[jb] = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                           (__attribute__((address_space(3))) bf16x4_t*)(vl + key * kVstRow + dim)));
           }
-          vnat[4 * s + nb] = u32x4{w[0], w[1], w[2], w[3]};
+          vnat[4 * s + nb] = u32x4{h[0][0], h[0][1], h[1][0], h[1][1]};
         }
       // every lane's reads are done before the next tile is stored over them
       __builtin_amdgcn_wave_barrier();
