@@ -246,7 +246,10 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   // row had more than two keys, cause not found; with the first tile peeled
   // into a buffer of its own the rows are right but the step is slower,
   // 0.693 against 0.668 ms.  Neither is in the build.)
+  // NAT: one row per workgroup, so its position is uniform (scalar), and so
+  // are the tile loop's bounds
   int p_raw = a.pos[b];
+  if (NAT) p_raw = __builtin_amdgcn_readfirstlane(p_raw);
   f32x4 qraw[2][2];
   {
     const float* qh = a.q + ((int64_t)r * a.H + g * G + (col % G)) * HD;
@@ -393,15 +396,21 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
       process(kr, vr, T);
     }
   } else {
-    // two buffers: A holds tiles wave + 2j*W, B tiles wave + (2j+1)*W
+    // two buffers: A holds tiles wave + 2j*W, B tiles wave + (2j+1)*W.  NAT:
+    // the loads are unconditional (a tile past the end re-reads the last one),
+    // so the compiler knows how many are in flight and waits for the computed
+    // tile's loads only (B = 1: 19.6 -> 17.1 us); the tiled form keeps its
+    // conditional loads, which measured faster there (9.0 against 9.9 us).
     u32x4 ka[8], va[8], kb2[8], vb2[8];
     int T = wave;
     if (T < ntiles) load(ka, va, T);
     for (; T < ntiles; T += 2 * ATT_WAVES) {
       const int T1 = T + ATT_WAVES, T2 = T + 2 * ATT_WAVES;
-      if (T1 < ntiles) load(kb2, vb2, T1);
+      if (NAT) load(kb2, vb2, T1 < ntiles ? T1 : ntiles - 1);
+      else if (T1 < ntiles) load(kb2, vb2, T1);
       process(ka, va, T);
-      if (T2 < ntiles) load(ka, va, T2);
+      if (NAT) load(ka, va, T2 < ntiles ? T2 : ntiles - 1);
+      else if (T2 < ntiles) load(ka, va, T2);
       if (T1 < ntiles) process(kb2, vb2, T1);
     }
   }
