@@ -12,7 +12,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libaltxs_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 MAX_LAYERS = 32
 MAX_SLOTS = 64
@@ -50,6 +50,8 @@ EXPORTS = (
     "altxs_qgemv",
     "altxs_qgemv_stream",
     "altxs_rms_qgemm",
+    "altxs_ffn_stage_rows",
+    "altxs_attn_gate",
     "altxs_decode_attn",
     "altxs_step_workspace_bytes",
     "altxs_step_plan_bytes",
@@ -88,6 +90,15 @@ class AttnArgs(ctypes.Structure):
                 ("gate", ctypes.c_void_p), ("use_xsa", ctypes.c_int32),
                 ("flags", ctypes.c_int32), ("kv_tail_end", ctypes.c_int32),
                 ("reserved", ctypes.c_int32), ("y", ctypes.c_void_p), ("err", ctypes.c_void_p)]
+
+
+class FfnStageArgs(ctypes.Structure):
+    _fields_ = [("win", ctypes.c_int32), ("d", ctypes.c_int32), ("mlp", ctypes.c_int32),
+                ("act_dtype", ctypes.c_int32), ("parallel", ctypes.c_int32),
+                ("skip_dst", ctypes.c_int32), ("eps", ctypes.c_float), ("reserved", ctypes.c_int32),
+                ("out_w", QTensor), ("up_w", QTensor), ("down_w", QTensor)] + [
+                    (n, ctypes.c_void_p) for n in ("y", "hid", "a_sc", "xin", "attn_s", "src", "ln", "scr",
+                                                   "m_sc", "x", "lane0", "lane1", "pr", "pp", "skips")]
 
 
 class Layer(ctypes.Structure):
@@ -180,6 +191,10 @@ def load():
     L.altxs_qgemv_stream.argtypes = [ctypes.POINTER(QTensor), i64, i64, i64, p, i32, i64, p, p]
     L.altxs_rms_qgemm.restype = i32
     L.altxs_rms_qgemm.argtypes = [ctypes.POINTER(QTensor), p, i64, ctypes.c_float, ctypes.c_float, i32, p, p]
+    L.altxs_ffn_stage_rows.restype = i32
+    L.altxs_ffn_stage_rows.argtypes = [ctypes.POINTER(FfnStageArgs), p]
+    L.altxs_attn_gate.restype = i32
+    L.altxs_attn_gate.argtypes = [p, i32, i64, p, i32, i32, i32, p, p]
     L.altxs_decode_attn.restype = i32
     L.altxs_decode_attn.argtypes = [ctypes.POINTER(AttnArgs), p]
     L.altxs_step_workspace_bytes.restype = i64

@@ -21,8 +21,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libaltxs_hip.so")
 BUILD_DIR = os.path.join(ROOT, "_build", "altxs_hip")
-SOURCES = ("api.cpp", "cdf.hip", "qgemm.hip", "qgemv.hip", "attn.hip", "step.hip", "persist.hip", "coder.hip",
-           "codec.hip")
+SOURCES = ("api.cpp", "cdf.hip", "qgemm.hip", "qgemv.hip", "stages.hip", "attn.hip", "step.hip", "persist.hip",
+           "coder.hip", "codec.hip")
 ARCH = os.environ.get("ALTXS_ARCH", "gfx950")
 
 

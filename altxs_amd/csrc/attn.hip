@@ -374,7 +374,7 @@ extern "C" int32_t altxs_decode_attn(const AltxsAttnArgs* a, altxs_stream_t stre
                 "altxs_decode_attn: H/Hkv=%d not in {1,2,4}", group);
   ALTXS_REQUIRE(a->max_len >= TILE && a->max_len % TILE == 0,
                 "altxs_decode_attn: max_len=%d must be a positive multiple of %d", a->max_len, TILE);
-  ALTXS_REQUIRE(a->kv_seg_stride >= (int64_t)a->Hkv * a->max_len * HD,
+  ALTXS_REQUIRE(a->kv_seg_stride == 0 || a->kv_seg_stride >= (int64_t)a->Hkv * a->max_len * HD,
                 "altxs_decode_attn: kv_seg_stride too small");
   ALTXS_REQUIRE((a->flags & ~(ALTXS_ATTN_OPS_BF16 | ALTXS_ATTN_ROWS | ALTXS_ATTN_XCD_ROWS)) == 0,
                 "altxs_decode_attn: unknown flags 0x%x", a->flags);

@@ -30,12 +30,11 @@ library raises).
   included (altxs_amd.init_seed).
 * :func:`gemv_rows` / :func:`gemv_vec` / :func:`logits_stage_rows` <-
   src/xsa_ttt/ac_gemv.py:391-420, 562-582.
-
-The reference's per-stage helpers ``ffn_stage_rows`` (ac_gemv.py:455-550) and
-``run_split_attn`` (split_attn.py:341-425) act on the internal workspace of
-the persistent tier (``_PersistWS``: its scratch rows and its packed KV
-layout); ``try_persistent_extend`` replaces that tier whole, so they have no
-standalone counterpart here.
+* :func:`ffn_stage_rows` <- ac_gemv.py:455-550 (the persistent tier's
+  out-projection + MLP stages, with its rounding points) and
+  :func:`run_split_attn` <- split_attn.py:341-425 (its decode / encode
+  attention over ``ws.k_pack`` / ``ws.v_pack``), for callers that keep the
+  reference's own workspace and swap only these stages.
 """
 
 from __future__ import annotations
@@ -547,3 +546,150 @@ def logits_stage_rows(src: torch.Tensor, weight: torch.Tensor, logit_buf: torch.
     _lib.check(rc, "altxs_rms_qgemm")
     if y is not logit_buf:
         logit_buf.copy_(y)
+
+
+# ---- stage-level helpers of the stage-fused row path ----------------------------
+
+def _act_code(t: torch.Tensor, what: str) -> int:
+    if t.dtype == torch.float32:
+        return _lib.F32
+    if t.dtype == torch.bfloat16:
+        return _lib.BF16
+    raise ValueError(f"{what} must be fp32 or bf16, got {t.dtype}")
+
+
+def ffn_stage_rows(*, y: torch.Tensor, out_w: torch.Tensor, hid: torch.Tensor, a_sc: torch.Tensor,
+                   xin: torch.Tensor, attn_s: torch.Tensor, src: torch.Tensor, up_w: torch.Tensor,
+                   ln: torch.Tensor, scr: torch.Tensor, down_w: torch.Tensor, m_sc: torch.Tensor,
+                   x: torch.Tensor, lane0: torch.Tensor, lane1: torch.Tensor, pr: torch.Tensor,
+                   pp: torch.Tensor, skips: torch.Tensor, skip_dst: int, par: bool,
+                   eps: float = 1e-6) -> None:
+    """Out-projection -> MLP up/activation -> MLP down/commit for ``win`` rows
+    as three stream-ordered launches (ac_gemv.py:455-550; stage kernels
+    89-310), with the reference's rounding to the workspace dtype at every
+    point its kernels round.  Activations and parameters (a_sc, m_sc, ln, pr,
+    pp) share one dtype, fp32 or bf16; weights are dense bf16 or fp32 [N, K]
+    tensors (tiled once and cached, like :func:`gemv_rows`).  ``src`` is
+    ``xin`` for sequential slots and ``lane1`` for parallel ones
+    (persistent_step.py:760-766)."""
+    win, d = int(y.shape[0]), int(y.shape[1])
+    mlp = int(scr.shape[1])
+    if int(ln.numel()) != 1:
+        raise ValueError(f"ln must be the per-layer scalar ln_scale_factor, got {ln.numel()} values")
+    if tuple(hid.shape) != (win, d) or tuple(xin.shape) != (win, d):
+        raise ValueError("stage-fused FFN hidden shape mismatch")
+    act = _act_code(y, "y")
+    named = dict(y=y, hid=hid, a_sc=a_sc, xin=xin, attn_s=attn_s, src=src, ln=ln, scr=scr, m_sc=m_sc,
+                 x=x, lane0=lane0, lane1=lane1, pr=pr, pp=pp, skips=skips)
+    for name, t in named.items():
+        if t is None:
+            continue
+        if t.dtype != y.dtype or not t.is_contiguous() or t.device != y.device:
+            raise ValueError(f"{name} must be a contiguous {y.dtype} tensor on {y.device}")
+    for name, t, shape in (("a_sc", a_sc, (d,)), ("m_sc", m_sc, (d,)), ("scr", scr, (win, mlp)),
+                           ("src", src, (win, d))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {shape}")
+    if par:
+        if int(pr.numel()) != 2 or int(pp.numel()) != 4:
+            raise ValueError("pr must hold 2 and pp 4 values (the layer's parallel lambdas)")
+        if attn_s.data_ptr() == y.data_ptr():
+            raise ValueError("attn_s must not alias y (stage 1 reads every column of y)")
+    elif skip_dst >= 0 and (skips is None or int(skips.shape[0]) <= skip_dst):
+        raise ValueError(f"skip_dst={skip_dst} outside skips")
+    a = _lib.FfnStageArgs()
+    a.win, a.d, a.mlp, a.act_dtype = win, d, mlp, act
+    a.parallel, a.skip_dst, a.eps = int(bool(par)), int(skip_dst) if not par else -1, float(eps)
+    a.out_w, a.up_w, a.down_w = _tiled(out_w), _tiled(up_w), _tiled(down_w)
+    for name, t in named.items():
+        setattr(a, name, None if t is None else t.data_ptr())
+    _lib.check(_lib.load().altxs_ffn_stage_rows(ctypes.byref(a), _stream(y)), "altxs_ffn_stage_rows")
+
+
+_SPLIT_NORM_EPS = 1e-12  # the XSA norm floor the attention kernels use (persistent_step.py:36)
+
+
+def run_split_attn(*, ws, pos: torch.Tensor, slot: int, rows: int, layer: int, use_xsa: int,
+                   use_gate: int, v_cur: torch.Tensor, v_cur_row_stride: int, tail_at_pos: bool,
+                   norm_eps: float, block_l: int) -> bool:
+    """Decode / encode attention of one slot over ``ws.k_pack`` / ``ws.v_pack``
+    ([slots, n_kv, max_len, hd], the reference's packed layout) into ``ws.y``
+    (split_attn.py:341-425): row r attends to keys [0, pos + r) and then to
+    the current key (row max_len - 1, or pos + r with ``tail_at_pos``), then
+    XSA and the sparse gate sigmoid(attn_in[r, :gate_n] . gate_w[layer, h]).
+
+    The natural-order MFMA decode kernel runs it (the key splits, ``block_l``
+    and the split workspace are the reference kernel's own launch shape and
+    have no role here; its work split is fixed, so its bits do not depend on
+    them).  bf16 caches: q and the softmax weights enter the products in bf16
+    as the reference's tl.dot operands; the current key is scored with the
+    same bf16 q (the reference scores it with the fp32 q).  fp32 caches: fp32
+    products.  ``v_cur`` equals the cache's current value row at both
+    reference call sites (mega_step.py:1006, mega_encode.py:345-372); XSA
+    reads it there.  Always True (the reference's False asks for its serial
+    kernel)."""
+    if abs(float(norm_eps) - _SPLIT_NORM_EPS) > 0:
+        raise ValueError(f"norm_eps={norm_eps}: the attention kernels use {_SPLIT_NORM_EPS}")
+    k_pack, v_pack = ws.k_pack, ws.v_pack
+    if k_pack.shape != v_pack.shape or k_pack.dtype != v_pack.dtype or k_pack.dim() != 4:
+        raise ValueError("k_pack/v_pack must be equal [slots, n_kv, max_len, hd] tensors")
+    if not (k_pack.is_contiguous() and v_pack.is_contiguous()):
+        raise ValueError("k_pack/v_pack must be contiguous")
+    n_slots, n_kv, max_len, hd = (int(s) for s in k_pack.shape)
+    H = int(ws.n_heads)
+    if int(ws.n_kv) != n_kv or int(ws.hd) != hd or int(ws.max_len) != max_len:
+        raise ValueError("ws.n_kv / hd / max_len disagree with k_pack")
+    if not 0 <= int(slot) < n_slots:
+        raise ValueError(f"slot {slot} outside k_pack's {n_slots} slots")
+    rows = int(rows)
+    if use_xsa and v_cur is None:
+        raise ValueError("use_xsa needs v_cur")
+    q = ws.q.reshape(-1, H, hd)[:rows].float().contiguous()
+    p0 = pos.reshape(-1)[:1].to(device=q.device, dtype=torch.int32)
+    a = _lib.AttnArgs()
+    a.H, a.Hkv, a.head_dim, a.max_len = H, n_kv, hd, max_len
+    if tail_at_pos or rows == 1:
+        # one sequence window: row r at pos + r (in place, or the tail row)
+        a.B, a.W, pvec = 1, rows, p0
+        a.kv_seg_stride = n_kv * max_len * hd
+        a.kv_tail_end = 0 if tail_at_pos else max_len
+    else:
+        # every row scores the shared tail row: rows as segments of one cache
+        a.B, a.W = rows, 1
+        pvec = p0 + torch.arange(rows, dtype=torch.int32, device=q.device)
+        a.kv_seg_stride = 0
+        a.kv_tail_end = max_len
+    a.kv_bf16 = _lib.KV_BF16_NATURAL if k_pack.dtype == torch.bfloat16 else _lib.KV_F32
+    if k_pack.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("k_pack must be bf16 or fp32")
+    off = int(slot) * n_kv * max_len * hd * k_pack.element_size()
+    a.q, a.k, a.v = q.data_ptr(), k_pack.data_ptr() + off, v_pack.data_ptr() + off
+    a.pos = pvec.data_ptr()
+    a.use_xsa = int(bool(use_xsa))
+    a.flags = _lib.ATTN_OPS_BF16
+    gate = None
+    if use_gate:
+        attn_in, gw = ws.attn_in, ws.gate_w[layer]
+        gate_n = int(ws.gate_n)
+        if attn_in.dtype != gw.dtype or not gw.is_contiguous() or attn_in.stride(-1) != 1:
+            raise ValueError("attn_in and gate_w must share a dtype, unit-stride rows")
+        if tuple(gw.shape) != (H, gate_n):
+            raise ValueError(f"gate_w[layer] has shape {tuple(gw.shape)}, expected {(H, gate_n)}")
+        gate = torch.empty(rows, H, dtype=torch.float32, device=q.device)
+        rc = _lib.load().altxs_attn_gate(attn_in.data_ptr(), _act_code(attn_in, "attn_in"),
+                                         attn_in.stride(0), gw.data_ptr(), H, gate_n, rows,
+                                         gate.data_ptr(), _stream(q))
+        _lib.check(rc, "altxs_attn_gate")
+    a.gate = None if gate is None else gate.data_ptr()
+    y_out = ws.y
+    if y_out.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("ws.y must be fp32 or bf16")
+    a.y_bf16 = int(y_out.dtype == torch.bfloat16)
+    direct = y_out.is_contiguous() and y_out.numel() >= rows * H * hd
+    y = y_out if direct else torch.empty(rows, H * hd, dtype=y_out.dtype, device=q.device)
+    a.y = y.data_ptr()
+    a.err = None
+    _lib.check(_lib.load().altxs_decode_attn(ctypes.byref(a), _stream(q)), "altxs_decode_attn")
+    if not direct:
+        y_out.reshape(-1, H * hd)[:rows].copy_(y)
+    return True

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define ALTXS_ABI_VERSION 7
+#define ALTXS_ABI_VERSION 8
 
 enum {
   ALTXS_OK = 0,
@@ -177,6 +177,59 @@ int32_t altxs_rms_qgemm(const AltxsQTensor *w, const float *x, int64_t rows, flo
                         float eps, int32_t act_bf16, float *y, altxs_stream_t stream);
 
 /*
+ * The stage-fused FFN of one slot over `win` rows, as three stream-ordered
+ * launches: (1) hid = y . out_w^T; scaled = hid * a_sc; parallel: attn_s =
+ * scaled, else xin += scaled.  (2) scr = leaky(RMS(src) * ln . up_w^T)^2
+ * with leaky(v) = v >= 0 ? v : v / 2.  (3) hid = scr . down_w^T; mlp_s = hid
+ * * m_sc; parallel: lane0 = pr0 lane0 + pp0 attn_s + pp2 mlp_s and lane1 =
+ * pr1 lane1 + pp1 attn_s + pp3 mlp_s; else x = xin + mlp_s, also stored to
+ * skips[skip_dst] when skip_dst >= 0.  Activations and parameters (a_sc,
+ * m_sc, ln, pr, pp) share act_dtype (fp32 or bf16); each value is rounded to
+ * it where the reference rounds (`.to(dtype)`, bf16 arithmetic).  Weights are
+ * dense tiles (bits 16, or 32 with fp32 activations); d in {256, 512}, mlp a
+ * multiple of 256 up to 8192; y and scr 16-byte aligned; hid and attn_s must
+ * not alias y.  Replaces ffn_stage_rows(...) (src/xsa_ttt/ac_gemv.py:455-550;
+ * stage kernels 89-310).
+ */
+typedef struct AltxsFfnStageArgs {
+  int32_t win, d, mlp;
+  int32_t act_dtype;  /* ALTXS_F32 or ALTXS_BF16 */
+  int32_t parallel;   /* 1: parallel-lane slot (lane0/lane1/attn_s/pr/pp) */
+  int32_t skip_dst;   /* sequential: skip buffer written with x, or -1 */
+  float eps;          /* RMS epsilon of stage 2 */
+  int32_t reserved;
+  AltxsQTensor out_w; /* [d, d] */
+  AltxsQTensor up_w;  /* [mlp, d] */
+  AltxsQTensor down_w;/* [d, mlp] */
+  const void *y;      /* [win, d] attention output */
+  void *hid;          /* [win, d] out: stage 1's projection, then stage 3's */
+  const void *a_sc;   /* [d] attn_scale */
+  void *xin;          /* [win, d] sequential residual, updated by stage 1 */
+  void *attn_s;       /* [win, d] parallel: scaled attention */
+  const void *src;    /* [win, d] stage 2 input: xin (sequential) or lane1 */
+  const void *ln;     /* [1] the layer's ln_scale_factor */
+  void *scr;          /* [win, mlp] activation */
+  const void *m_sc;   /* [d] mlp_scale */
+  void *x;            /* [win, d] sequential: slot output */
+  void *lane0;        /* [win, d] parallel lanes, updated in place */
+  void *lane1;
+  const void *pr;     /* [2] parallel_resid_lambdas of the layer */
+  const void *pp;     /* [4] parallel_post_lambdas of the layer, [2, 2] row-major */
+  void *skips;        /* [n_skips, win, d] */
+} AltxsFfnStageArgs;
+int32_t altxs_ffn_stage_rows(const AltxsFfnStageArgs *a, altxs_stream_t stream);
+
+/*
+ * gate[r, h] = 1 / (1 + exp(-(x[r, :gw] . w[h, :gw]))) in fp32, for r < rows,
+ * h < H; x (row stride x_stride) and w share x_dtype (fp32 or bf16).  The
+ * sparse-gate multiplier of the split attention's reduce step
+ * (src/xsa_ttt/split_attn.py:291-303; w already carries the gate scale,
+ * persistent_step.py:349-357), in the form altxs_decode_attn takes.
+ */
+int32_t altxs_attn_gate(const void *x, int32_t x_dtype, int64_t x_stride, const void *w, int32_t H,
+                        int32_t gw, int32_t rows, float *gate, altxs_stream_t stream);
+
+/*
  * KV cache layout.  Per (segment, kv head) the cache holds max_len keys of
  * head_dim = 64 in 64-key tiles (ALTXS_KV_TILE); max_len % 64 == 0.  The
  * kv_bf16 field of the descriptors selects one of three layouts:
@@ -244,7 +297,9 @@ typedef struct AltxsAttnArgs {
   const void *k;    /* [B, Hkv, max_len, head_dim] in the cache layout above,
                        seg stride kv_seg_stride elems; 16-byte aligned */
   const void *v;
-  int64_t kv_seg_stride; /* elements between segments (both K and V) */
+  int64_t kv_seg_stride; /* elements between segments (both K and V); 0: every
+                            segment reads the same cache (rows of one sequence
+                            at positions pos[b]) */
   const int32_t *pos;    /* [B] */
   const float *gate;     /* [B*W, H] multiplier (sparse attention gate) or NULL */
   int32_t use_xsa;       /* subtract the current value direction (model.py:760-768) */

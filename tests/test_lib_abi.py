@@ -61,6 +61,16 @@ def test_bad_arguments_return_errors_without_gpu():
         qt.bits = bits
         assert L.altxs_qgemv(ctypes.byref(qt), fake, xdt, rows, fake, None) == -1
         assert what in L.altxs_last_error(), L.altxs_last_error()
+    # the stage entry points check shapes and pointers before any launch
+    a = _lib.FfnStageArgs()
+    a.win, a.d, a.mlp, a.act_dtype = 4, 384, 2048, _lib.BF16
+    assert L.altxs_ffn_stage_rows(ctypes.byref(a), None) == -1
+    assert b"d=384" in L.altxs_last_error()
+    a.d = 512
+    assert L.altxs_ffn_stage_rows(ctypes.byref(a), None) == -1
+    assert b"out_w" in L.altxs_last_error()
+    assert L.altxs_attn_gate(fake, _lib.F16, 16, fake, 8, 12, 1, fake, None) == -1
+    assert b"x_dtype" in L.altxs_last_error()
     qt.bits = 4
     assert L.altxs_qgemv_stream(ctypes.byref(qt), 2, 512 * 1024, 16, fake, _lib.F16, 1, fake, None) == -1
     assert b"strides" in L.altxs_last_error()
@@ -94,6 +104,8 @@ int main(void) {{
          offsetof(AltxsCoderState, err));
   printf("%zu %zu %zu\\n", sizeof(AltxsCodecGroups), offsetof(AltxsCodecGroups, n_codes),
          offsetof(AltxsCodecGroups, mode));
+  printf("%zu %zu %zu %zu\\n", sizeof(AltxsFfnStageArgs), offsetof(AltxsFfnStageArgs, out_w),
+         offsetof(AltxsFfnStageArgs, y), offsetof(AltxsFfnStageArgs, skips));
   return 0;
 }}
 """)
@@ -106,5 +118,6 @@ int main(void) {{
           _lib.StepDesc.layers.offset, _lib.StepDesc.emb.offset, _lib.StepDesc.tokens.offset,
           _lib.StepDesc.err.offset, ctypes.sizeof(_lib.CoderState), _lib.CoderState.nbytes.offset,
           _lib.CoderState.err.offset, ctypes.sizeof(_lib.CodecGroups), _lib.CodecGroups.n_codes.offset,
-          _lib.CodecGroups.mode.offset]
+          _lib.CodecGroups.mode.offset, ctypes.sizeof(_lib.FfnStageArgs), _lib.FfnStageArgs.out_w.offset,
+          _lib.FfnStageArgs.y.offset, _lib.FfnStageArgs.skips.offset]
     assert c_sizes == py
