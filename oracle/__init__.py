@@ -15,6 +15,9 @@ Contents (each function cites the reference file:line it restates):
   symmetric variant, numpy.
 * :mod:`oracle.model_ref` -- the fp32 eager step of the reference GPT
   (src/xsa_ttt/model.py), PyTorch on CPU, B=1 per segment.
+* :mod:`oracle.stages_ref` -- the stage-fused FFN kernels with their bf16
+  rounding points (src/xsa_ttt/ac_gemv.py:89-310) and the split attention's
+  result (src/xsa_ttt/split_attn.py), numpy.
 
 Pinning (what fixes each function beyond retyping the formula) is listed in
 each module's docstring; see also tests/golden/.
