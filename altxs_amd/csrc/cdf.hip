@@ -243,9 +243,10 @@ __global__ __launch_bounds__(CDF_THREADS) void cdf_f64_kernel(const double* __re
   }
 }
 
-// ---- row-parallel softmax -> CDF from per-tile statistics -------------------
+// ---- row-parallel softmax -> CDF ---------------------------------------------
 //
-// The LM head leaves, for every (row, 64-column tile), the tile max m_t and
+// Chunked form (vocabularies the one-row kernel below does not tile): the LM
+// head leaves, for every (row, 64-column tile), the tile max m_t and
 // s_t = sum exp(l - m_t).  Workgroup (chunk c, row) first forms the row's
 // M = max m_t and S = sum s_t * exp(m_t - M) in a fixed order (identical in
 // every workgroup of the row), then p_i = exp(l_i - M) * (1 / S).  Its CDF offset is
@@ -366,24 +367,23 @@ __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
 }
 
 // One workgroup per row, the row in registers: wave w holds the 64-column
-// tiles w, w + 16, ... (TPW of them), column c of a tile on lane c -- the
-// layout of the LM-head epilogue's tile statistics, which (stats == NULL) the
-// kernel forms itself with the same wave_max / wave_sum.  M and S come from
-// the tile statistics exactly as in cdf_chunk_kernel; each count is the same
-// elementwise function of its logit; the table is the exact integer prefix
-// (in-tile wave scans plus the exclusive prefix of the tile totals), so the
-// tables equal the chunk kernel's.  Loads and stores are 64 consecutive words
-// per wave instruction; LDS holds only the tile statistics and totals.
+// tiles w, w + 16, ... (TPW of them), column c of a tile on lane c.  The row
+// max M and S = sum exp(l - M) come from the registers in one fixed order
+// (each lane over its tiles in order, then the wave's DPP tree, then the 16
+// waves in order), so a row's probabilities and table depend on its logits
+// alone, whatever launch produced them; each exponential serves both S and
+// the row's probability p = exp(l - M) / S (one exponential per element).  The
+// table is the exact integer prefix (in-tile wave scans plus the exclusive
+// prefix of the tile totals).  Loads and stores are 64 consecutive words per
+// wave instruction; LDS holds only the reductions and tile totals.
 template <int TPW>
-__global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __restrict__ logits,
-                                                              const float2* __restrict__ stats,
-                                                              int V, float* __restrict__ probs,
+__global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __restrict__ logits, int V,
+                                                              float* __restrict__ probs,
                                                               uint32_t* __restrict__ cum,
                                                               int xcd_rows) {
   constexpr int NT = CH_WAVES * TPW;  // tiles of the row (V / 64, host check)
   static_assert(NT <= 4 * WAVE, "one wave forms the prefix of the tile totals");
   __shared__ float red[CH_WAVES];
-  __shared__ float2 sst[NT];
   __shared__ uint32_t tex[NT];
   int64_t row = blockIdx.x;
   if (xcd_rows) {  // row tile rt of 8 rows on XCD rt % 8
@@ -396,30 +396,22 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __rest
   float v[TPW];
 #pragma unroll
   for (int j = 0; j < TPW; ++j) v[j] = __builtin_nontemporal_load(x + 64 * (w + CH_WAVES * j) + l);
-  const float2* st = stats ? stats + row * (int64_t)NT : sst;
-  if (!stats) {
+  float mt = v[0];
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const float m = wave_max(v[j]);
-      const float e = wave_sum(v[j] == -INFINITY ? 0.f : __expf(v[j] - m));
-      if (l == 0) sst[w + CH_WAVES * j] = make_float2(m, e);
-    }
-    __syncthreads();
-  }
-  float mt = -INFINITY;
-  for (int i = t; i < NT; i += CH_THREADS) mt = fmaxf(mt, st[i].x);
+  for (int j = 1; j < TPW; ++j) mt = fmaxf(mt, v[j]);
   const float M = block_max_n(mt, red);
   float sp = 0.f;
-  for (int i = t; i < NT; i += CH_THREADS) {
-    const float2 q = st[i];
-    sp += q.y * __expf(q.x - M);
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    v[j] = __expf(v[j] - M);
+    sp += v[j];
   }
   const float S = block_sum_n(sp, red);
   const float iS = 1.f / S;
   uint32_t inc[TPW];
 #pragma unroll
   for (int j = 0; j < TPW; ++j) {
-    const float p = __expf(v[j] - M) * iS;
+    const float p = v[j] * iS;
     if (probs) probs[row * (int64_t)V + 64 * (w + CH_WAVES * j) + l] = p;
     inc[j] = wave_incl_scan_u32(scale_count(p));
     if (l == WAVE - 1) tex[w + CH_WAVES * j] = inc[j];
@@ -485,15 +477,15 @@ hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int6
   if (rows <= 0) return hipSuccess;
   if (V % 64) return hipErrorInvalidValue;
   if (altxs_cdf_rows_kernel(rows, V)) {
-    // many rows: one workgroup per row (bit-identical tables, no recount); with
-    // stats == NULL it forms the tile statistics itself
+    // one workgroup per row, the statistics from its own registers (the tile
+    // statistics are not read)
     const dim3 grid((unsigned)rows), block(CH_THREADS);
     const int xr = (xcd_rows && rows % 64 == 0) ? 1 : 0;
     switch (V / (64 * CH_WAVES)) {  // tiles per wave
-      case 4: hipLaunchKernelGGL(cdf_row_kernel<4>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
-      case 8: hipLaunchKernelGGL(cdf_row_kernel<8>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
-      case 12: hipLaunchKernelGGL(cdf_row_kernel<12>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
-      case 16: hipLaunchKernelGGL(cdf_row_kernel<16>, grid, block, 0, s, logits, stats, V, probs, cum, xr); break;
+      case 4: hipLaunchKernelGGL(cdf_row_kernel<4>, grid, block, 0, s, logits, V, probs, cum, xr); break;
+      case 8: hipLaunchKernelGGL(cdf_row_kernel<8>, grid, block, 0, s, logits, V, probs, cum, xr); break;
+      case 12: hipLaunchKernelGGL(cdf_row_kernel<12>, grid, block, 0, s, logits, V, probs, cum, xr); break;
+      case 16: hipLaunchKernelGGL(cdf_row_kernel<16>, grid, block, 0, s, logits, V, probs, cum, xr); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

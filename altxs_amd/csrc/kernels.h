@@ -6,10 +6,10 @@
 hipError_t altxs_launch_cdf(const float* in, int64_t rows, int V, int flags, bool from_logits,
                             float* probs, uint32_t* cum, hipStream_t s);
 
-// Row-parallel softmax -> CDF from the LM head's per-64-column tile statistics
-// (no renormalisation); V % 64 == 0.
+// Row-parallel softmax -> CDF (no renormalisation); V % 64 == 0.  The chunked
+// form reads the LM head's per-64-column tile statistics.
 // Whether altxs_launch_cdf_stats uses one workgroup per row for this shape
-// (it then also accepts stats == NULL and forms the tile statistics itself).
+// (it then forms the row statistics itself and does not read stats).
 bool altxs_cdf_rows_kernel(int64_t rows, int V);
 // xcd_rows (row kernel, rows % 64 == 0): row tile t of 8 rows on XCD t % 8.
 hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int64_t rows, int V,

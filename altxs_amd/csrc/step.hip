@@ -502,16 +502,15 @@ struct StepRun {
     const int R = G.nb * d->W;
     const int64_t Rp = align_up(R, 16), D = d->D;
     const bool fast_cdf = !(d->flags & ALTXS_F_RENORM) && d->V % 64 == 0;
-    bool own_stats = false;
     hipError_t e;
+    // the one-row-per-workgroup CDF forms its row statistics itself; only the
+    // chunked CDF (other vocabularies) reads the LM head's tile statistics
+    const bool tile_stats = fast_cdf && G.cum && !altxs_cdf_rows_kernel(R, d->V);
     {
       const int n = d->n_slots, fm = final_mode(d);
       const float* xf = (fm == 2 ? w.X1 : w.X0) + n * Rp * D;
       ProNorm pro{xf, fm == 1 ? w.X1 + n * Rp * D : nullptr, fm == 1 ? 1 : 0, 1.0f, d->norm_eps, d->D};
-      // with the large-tile head and the one-row-per-workgroup CDF, the CDF
-      // kernel forms the tile statistics itself (same arithmetic, off the GEMM)
-      own_stats = big(R, d->emb) && fast_cdf && G.cum && altxs_cdf_rows_kernel(R, d->V);
-      EpiLogits epi{G.logits, (fast_cdf && !own_stats) ? w.STATS : nullptr, d->V,
+      EpiLogits epi{G.logits, tile_stats ? w.STATS : nullptr, d->V,
                     (d->flags & ALTXS_F_ASYM_SOFTCAP) ? 1 : 0, d->logit_softcap, d->softcap_pn};
       if (big(R, d->emb) && band_norm_fits(qt_of(d->emb))) {
         e = launch_gemm_band_norm<4, 1>(d->emb.bits, qt_of(d->emb), R, pro, epi, st);
@@ -526,7 +525,7 @@ struct StepRun {
     }
     if (G.probs || G.cum) {
       if (fast_cdf && G.cum) {
-        if ((e = altxs_launch_cdf_stats(G.logits, own_stats ? nullptr : w.STATS, R, d->V, G.probs,
+        if ((e = altxs_launch_cdf_stats(G.logits, tile_stats ? w.STATS : nullptr, R, d->V, G.probs,
                                         G.cum, st, xr(G))) != hipSuccess)
           return e;
       } else {

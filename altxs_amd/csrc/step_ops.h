@@ -897,7 +897,7 @@ __device__ __forceinline__ float softcap_el(float l, float cp, float cn, float i
 }
 
 // Softcapped logits, plus per (row, 64-column tile) softmax statistics
-// (tile max m and sum of exp(l - m)) for the row-parallel CDF kernel.
+// (tile max m and sum of exp(l - m)) for the chunked CDF kernel.
 struct EpiLogits {
   float* logits;
   float2* stats;  // [R][V/64] or NULL
@@ -946,7 +946,7 @@ struct EpiLogits {
       }
     }
   }
-  // strips only without tile statistics (the CDF kernel then forms them)
+  // strips only without tile statistics (the one-row CDF kernel reads none)
   static constexpr bool kStrip = true;
   __device__ bool strip_ok() const { return stats == nullptr; }
   template <class Cfg>
