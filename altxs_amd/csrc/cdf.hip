@@ -395,7 +395,7 @@ __global__ __launch_bounds__(CH_THREADS) void cdf_row_kernel(const float* __rest
   const float* x = logits + row * (int64_t)V;
   float v[TPW];
 #pragma unroll
-  for (int j = 0; j < TPW; ++j) v[j] = __builtin_nontemporal_load(x + 64 * (w + CH_WAVES * j) + l);
+  for (int j = 0; j < TPW; ++j) v[j] = x[64 * (w + CH_WAVES * j) + l];
   float mt = v[0];
 #pragma unroll
   for (int j = 1; j < TPW; ++j) mt = fmaxf(mt, v[j]);
