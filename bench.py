@@ -33,8 +33,10 @@ The line also carries:
   host on a bounded sample of the same workload;
 * ``secondary`` (default workload only; ``--no-secondary`` skips it): the other
   regimes of the benchmark set measured in the same run, after the timed
-  region -- the batch-1 decode step at ctx 2048, cfg4 chunk scoring (64 x 2048
-  tokens) and the cfg2 batch-1 row GEMV over >= 2 GB streams.
+  region -- the batch-1 decode step at ctx 2048, the headline step with fp32
+  activations (the mode within 2e-3 of the fp32 oracle's logits), cfg4 chunk
+  scoring (64 x 2048 tokens) and the cfg2 batch-1 row GEMV over >= 2 GB
+  streams.
 """
 
 from __future__ import annotations
@@ -131,10 +133,11 @@ def attn_kernel_ms(model, st, reps: int = 20, replays: int = 5) -> float:
     return e0.elapsed_time(e1) / (reps * replays)
 
 
-def decode_measure(sm, B: int, ctx: int, steps: int = 50, gs: int = 10, warmup: int = 5) -> dict:
-    """The decode step of B segments at context ctx (bf16): ms per step over
-    steps // gs replays of a graph of gs steps, and the attention kernel's own
-    launch time (attn_kernel_ms)."""
+def decode_measure(sm, B: int, ctx: int, steps: int = 50, gs: int = 10, warmup: int = 5,
+                   act: str = "bf16") -> dict:
+    """The decode step of B segments at context ctx (``act`` activations, bf16
+    KV): ms per step over steps // gs replays of a graph of gs steps, and the
+    attention kernel's own launch time (attn_kernel_ms)."""
     import numpy as np
     import torch
 
@@ -142,7 +145,7 @@ def decode_measure(sm, B: int, ctx: int, steps: int = 50, gs: int = 10, warmup: 
     from altxs_amd.model import StepModel
 
     cfg = sm.cfg
-    model = StepModel(sm, act="bf16", kv="bf16")
+    model = StepModel(sm, act=act, kv="bf16")
     st = model.make_static_state((ctx + 255) // 256 * 256, win=1, batch=B, want_probs=False, want_cdf=True)
     g = torch.Generator(device="cuda").manual_seed(0)
     st.kv.normal_(generator=g)
@@ -170,7 +173,8 @@ def decode_measure(sm, B: int, ctx: int, steps: int = 50, gs: int = 10, warmup: 
     attn_bytes = ab["kv_read"] // ab["n_slots"] + B * cfg.num_heads * cfg.head_dim * 6 + B * cfg.num_heads * 4
     del graph, st, model
     torch.cuda.empty_cache()
-    return {"segments": B, "ctx": ctx, "ms_per_step": round(ms, 4), "value": round(B / (ms * 1e-3), 1),
+    return {"segments": B, "ctx": ctx, "act": act, "ms_per_step": round(ms, 4),
+            "value": round(B / (ms * 1e-3), 1),
             "unit": "sym/s", "steps": steps // gs * gs, "graph_steps": gs,
             "attn_us_per_launch": round(attn_ms * 1e3, 2),
             "attn_GBps": round(attn_bytes / (attn_ms * 1e-3) / 1e9, 1)}
@@ -179,8 +183,10 @@ def decode_measure(sm, B: int, ctx: int, steps: int = 50, gs: int = 10, warmup: 
 def secondary_measures(sm) -> dict:
     """The other regimes of the benchmark set, measured in the same run (each
     a few seconds): the batch-1 decode step (the reference's production
-    regime), cfg4 chunk scoring (64 x 2048 tokens from position 0) and the
-    cfg2 batch-1 row GEMV over >= 2 GB streams."""
+    regime), the headline step with fp32 activations (the mode whose logits
+    stay within 2e-3 of the fp32 oracle), cfg4 chunk scoring (64 x 2048
+    tokens from position 0) and the cfg2 batch-1 row GEMV over >= 2 GB
+    streams."""
     import numpy as np
 
     from altxs_amd import synth
@@ -192,6 +198,11 @@ def secondary_measures(sm) -> dict:
         log(f"secondary: batch-1 decode step {out['b1_decode_step']['ms_per_step']:.3f} ms")
     except Exception as exc:  # noqa: BLE001
         out["b1_decode_step"] = {"error": repr(exc)}
+    try:
+        out["fp32_act_decode_step"] = decode_measure(sm, 64, 2048, act="fp32")
+        log(f"secondary: fp32-activation decode step {out['fp32_act_decode_step']['ms_per_step']:.3f} ms")
+    except Exception as exc:  # noqa: BLE001
+        out["fp32_act_decode_step"] = {"error": repr(exc)}
     try:
         sm4 = synth.make_model(make_config("cfg4"))
         ms, flops = window_measure(sm4, 64, 2048, 0, "bf16", "bf16", steps=3, warmup=1)
