@@ -35,8 +35,8 @@ The line also carries:
   regimes of the benchmark set measured in the same run, after the timed
   region -- the batch-1 decode step at ctx 2048, the headline step with fp32
   activations (the mode within 2e-3 of the fp32 oracle's logits), cfg4 chunk
-  scoring (64 x 2048 tokens) and the cfg2 batch-1 row GEMV over >= 2 GB
-  streams.
+  scoring (64 x 2048 tokens), the cfg5 LoRA step (256 segments at ctx 4096)
+  and the cfg2 batch-1 row GEMV over >= 2 GB streams.
 """
 
 from __future__ import annotations
@@ -185,8 +185,8 @@ def secondary_measures(sm) -> dict:
     a few seconds): the batch-1 decode step (the reference's production
     regime), the headline step with fp32 activations (the mode whose logits
     stay within 2e-3 of the fp32 oracle), cfg4 chunk scoring (64 x 2048
-    tokens from position 0) and the cfg2 batch-1 row GEMV over >= 2 GB
-    streams."""
+    tokens from position 0), the cfg5 LoRA step (256 segments at ctx 4096)
+    and the cfg2 batch-1 row GEMV over >= 2 GB streams."""
     import numpy as np
 
     from altxs_amd import synth
@@ -214,6 +214,18 @@ def secondary_measures(sm) -> dict:
         log(f"secondary: cfg4 {ms:.2f} ms/step, {tf:.0f} TFLOP/s")
     except Exception as exc:  # noqa: BLE001
         out["cfg4_window"] = {"error": repr(exc)}
+    try:
+        sm5 = synth.make_model(make_config("cfg5"))
+        r5 = decode_measure(sm5, 256, 4096, steps=20)
+        ab5 = synth.algorithmic_step_bytes(sm5, 256, 4096, kv_bytes=2)
+        gbs5 = ab5["total"] / (r5["ms_per_step"] * 1e-3) / 1e9
+        r5.update({"workload": "cfg5: 256 segments at ctx 4096, rank-16 q/v LoRA on every slot, bf16",
+                   "step_GBps": round(gbs5, 1), "step_hbm_frac": round(gbs5 / HBM_PEAK_GBS, 4)})
+        out["cfg5_decode_step"] = r5
+        log(f"secondary: cfg5 {r5['ms_per_step']:.3f} ms/step, {gbs5:.0f} GB/s")
+        del sm5
+    except Exception as exc:  # noqa: BLE001
+        out["cfg5_decode_step"] = {"error": repr(exc)}
     try:
         res = cfg2_measure(2.0, (("qgemv", 1),))
         gbs = float(np.mean([r["GBps"] for r in res]))
