@@ -71,7 +71,11 @@ template <> struct Planes<8> { static constexpr int P0 = 16, P1 = 0; };
 template <int BITS> __host__ __device__ constexpr int vpb() { return BITS == 32 ? 3 : 1; }
 
 // A-operand modes
-enum AMode : int { A_F32 = 0, A_BF16 = 1, A_F16 = 2 };
+// A_F32S: fp32 rows staged (by a prologue) as their three bf16 parts --
+// split3's hi, mid and lo, each a plane of K + 8 elements inside the row -- so
+// the k-loop reads the MFMA operands that A_F32 forms in the loop, without
+// splitting them again in every wave.  The same operands: the same bits.
+enum AMode : int { A_F32 = 0, A_BF16 = 1, A_F16 = 2, A_F32S = 3 };
 
 struct QT {
   const uint8_t* codes;
@@ -80,7 +84,9 @@ struct QT {
   int bits;  // read only by the run-time-width specialisation (BITS == 0)
 };
 
-__host__ __device__ constexpr int lds_stride(int K, int am) { return K + (am == A_F32 ? 4 : 8); }
+__host__ __device__ constexpr int lds_stride(int K, int am) {
+  return am == A_F32 ? K + 4 : am == A_F32S ? 3 * (K + 8) : K + 8;
+}
 __host__ __device__ constexpr int a_esz(int am) { return am == A_F32 ? 4 : 2; }
 
 // Store four consecutive fp32 values (col % 4 == 0) into an LDS A tile.
@@ -89,6 +95,26 @@ __device__ __forceinline__ void a_store4(void* As, int row, int col, int K, cons
   if constexpr (AM == A_F32) {
     f32x4 o = {v[0], v[1], v[2], v[3]};
     *(f32x4*)((float*)As + row * lds_stride(K, AM) + col) = o;
+  } else if constexpr (AM == A_F32S) {  // split3 (below) of each value, one plane per part
+    // (the residuals from the rounded values, as split3 sees them after an
+    // fp32 store: no product of the caller's may fuse into them)
+#pragma clang fp contract(off)
+    uint16_t h[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const __bf16 h0 = (__bf16)v[i];
+      const float r1 = v[i] - (float)h0;
+      const __bf16 h1 = (__bf16)r1;
+      const float r2 = r1 - (float)h1;
+      h[0][i] = __builtin_bit_cast(uint16_t, h0);
+      h[1][i] = __builtin_bit_cast(uint16_t, h1);
+      h[2][i] = __builtin_bit_cast(uint16_t, (__bf16)r2);
+    }
+    uint16_t* base = (uint16_t*)As + row * lds_stride(K, AM) + col;
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      *(u32x2*)(base + p * (K + 8)) =
+          u32x2{(uint32_t)h[p][0] | ((uint32_t)h[p][1] << 16), (uint32_t)h[p][2] | ((uint32_t)h[p][3] << 16)};
   } else {
     uint16_t h[4];
 #pragma unroll
@@ -489,20 +515,28 @@ __device__ __forceinline__ void compute_blk(const Blk<BITS, AM, ADIRECT>& b, con
     for (int ss = 0; ss < 2; ++ss) {
       const int s = 2 * g + ss;
       const int kc = kb * 256 + 32 * s + 8 * (lane >> 4);
-      if constexpr (AM == A_F32) {
-        float x[8];
-        if constexpr (ADIRECT) {
-          const u32x4 lo = b.a[2 * s], hi = b.a[2 * s + 1];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) { x[i] = __uint_as_float(lo[i]); x[4 + i] = __uint_as_float(hi[i]); }
-        } else {
-          const float* a = (const float*)As + row * lds_stride(K, AM) + kc;
-          const f32x4 lo = *(const f32x4*)a, hi = *(const f32x4*)(a + 4);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) { x[i] = lo[i]; x[4 + i] = hi[i]; }
-        }
+      if constexpr (AM == A_F32 || AM == A_F32S) {
         bf16x8 a0, a1, a2;
-        split3(x, a0, a1, a2);
+        if constexpr (AM == A_F32S) {
+          static_assert(!ADIRECT, "pre-split rows are staged by a prologue");
+          const uint16_t* a = (const uint16_t*)As + row * lds_stride(K, AM) + kc;
+          a0 = __builtin_bit_cast(bf16x8, *(const u32x4*)a);
+          a1 = __builtin_bit_cast(bf16x8, *(const u32x4*)(a + (K + 8)));
+          a2 = __builtin_bit_cast(bf16x8, *(const u32x4*)(a + 2 * (K + 8)));
+        } else {
+          float x[8];
+          if constexpr (ADIRECT) {
+            const u32x4 lo = b.a[2 * s], hi = b.a[2 * s + 1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { x[i] = __uint_as_float(lo[i]); x[4 + i] = __uint_as_float(hi[i]); }
+          } else {
+            const float* a = (const float*)As + row * lds_stride(K, AM) + kc;
+            const f32x4 lo = *(const f32x4*)a, hi = *(const f32x4*)(a + 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { x[i] = lo[i]; x[4 + i] = hi[i]; }
+          }
+          split3(x, a0, a1, a2);
+        }
         const bf16x8 bo = b_op_bf16<BITS>(q0, q1, s, bits);
         t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bo, t, 0, 0, 0);
         t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bo, t, 0, 0, 0);
@@ -725,7 +759,7 @@ hipError_t launch_gemm_bits(int bits, const QT& w, int R, int batch, int64_t cod
         return launch_gemm<16, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
       return hipErrorInvalidValue;
     case 32:  // fp32 dense weights: the fp32-activation path only
-      if constexpr (AM == A_F32)
+      if constexpr (AM == A_F32 || AM == A_F32S)
         return launch_gemm<32, AM, NB, KS>(w, R, batch, codes_stride, scales_stride, ad, pro, epi, col_wgs, s, rows8);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;

@@ -383,6 +383,12 @@ struct StepRun {
       if (e != hipSuccess) return e;
       return launch_gemm_big<4, 1>(q.bits, q, R, (const uint16_t*)w.Y, epi, st);
     }
+    // fp32 rows: staged pre-split (A_F32S) unless the LoRA epilogue reads them
+    if constexpr (AM == A_F32) {
+      if (!S.lora_q_a)
+        return launch_gemm_bits<A_F32S, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
+                                              pro, epi, 0, st);
+    }
     return launch_gemm_bits<AM, 4, 1>(L.qkv.bits, qt_of(L.qkv), R, 1, 0, 0, ADirect{nullptr, 0},
                                       pro, epi, 0, st);
   }
@@ -460,8 +466,8 @@ struct StepRun {
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
         e = launch_gemm_big4(kKsUp, qt_big(L.up).bits, qt_big(L.up), R, (const uint16_t*)w.Y, epi, st);
       } else {
-        e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, pro, epi, 0, st,
-                             xr(G));
+        e = launch_gemm4<AM == A_F32 ? A_F32S : AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0},
+                                                    pro, epi, 0, st, xr(G));
       }
       if (e != hipSuccess) return e;
     }
@@ -518,8 +524,8 @@ struct StepRun {
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
         e = launch_gemm_big<4, 1>(d->emb.bits, qt_of(d->emb), R, (const uint16_t*)w.Y, epi, st);
       } else {
-        e = launch_gemm_bits<AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0, ADirect{nullptr, 0},
-                                       pro, epi, kLmHeadColWgs, st);
+        e = launch_gemm_bits<AM == A_F32 ? A_F32S : AM, 4, 1>(d->emb.bits, qt_of(d->emb), R, 1, 0, 0,
+                                                              ADirect{nullptr, 0}, pro, epi, kLmHeadColWgs, st);
       }
       if (e != hipSuccess) return e;
     }
