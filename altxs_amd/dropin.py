@@ -593,10 +593,17 @@ def ffn_stage_rows(*, y: torch.Tensor, out_w: torch.Tensor, hid: torch.Tensor, a
     if par:
         if int(pr.numel()) != 2 or int(pp.numel()) != 4:
             raise ValueError("pr must hold 2 and pp 4 values (the layer's parallel lambdas)")
+        for name, t in (("attn_s", attn_s), ("lane0", lane0), ("lane1", lane1)):
+            if t is None or tuple(t.shape) != (win, d):
+                raise ValueError(f"{name} must be a [{win}, {d}] tensor in a parallel slot")
         if attn_s.data_ptr() == y.data_ptr():
             raise ValueError("attn_s must not alias y (stage 1 reads every column of y)")
-    elif skip_dst >= 0 and (skips is None or int(skips.shape[0]) <= skip_dst):
-        raise ValueError(f"skip_dst={skip_dst} outside skips")
+    else:
+        if x is None or tuple(x.shape) != (win, d):
+            raise ValueError(f"x must be a [{win}, {d}] tensor in a sequential slot")
+        if skip_dst >= 0 and (skips is None or skips.dim() != 3 or tuple(skips.shape[1:]) != (win, d)
+                              or int(skips.shape[0]) <= skip_dst):
+            raise ValueError(f"skip_dst={skip_dst}: skips must be [n > skip_dst, {win}, {d}]")
     a = _lib.FfnStageArgs()
     a.win, a.d, a.mlp, a.act_dtype = win, d, mlp, act
     a.parallel, a.skip_dst, a.eps = int(bool(par)), int(skip_dst) if not par else -1, float(eps)
@@ -641,10 +648,17 @@ def run_split_attn(*, ws, pos: torch.Tensor, slot: int, rows: int, layer: int, u
         raise ValueError("ws.n_kv / hd / max_len disagree with k_pack")
     if not 0 <= int(slot) < n_slots:
         raise ValueError(f"slot {slot} outside k_pack's {n_slots} slots")
+    if k_pack.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("k_pack must be bf16 or fp32")
     rows = int(rows)
+    if rows < 1:
+        raise ValueError(f"rows={rows}")
     if use_xsa and v_cur is None:
         raise ValueError("use_xsa needs v_cur")
-    q = ws.q.reshape(-1, H, hd)[:rows].float().contiguous()
+    q_all = ws.q.reshape(-1, H, hd)
+    if int(q_all.shape[0]) < rows or int(pos.numel()) < 1:
+        raise ValueError(f"ws.q holds {q_all.shape[0]} rows of {H} heads, {rows} asked; pos must be set")
+    q = q_all[:rows].float().contiguous()
     p0 = pos.reshape(-1)[:1].to(device=q.device, dtype=torch.int32)
     a = _lib.AttnArgs()
     a.H, a.Hkv, a.head_dim, a.max_len = H, n_kv, hd, max_len
@@ -660,8 +674,6 @@ def run_split_attn(*, ws, pos: torch.Tensor, slot: int, rows: int, layer: int, u
         a.kv_seg_stride = 0
         a.kv_tail_end = max_len
     a.kv_bf16 = _lib.KV_BF16_NATURAL if k_pack.dtype == torch.bfloat16 else _lib.KV_F32
-    if k_pack.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("k_pack must be bf16 or fp32")
     off = int(slot) * n_kv * max_len * hd * k_pack.element_size()
     a.q, a.k, a.v = q.data_ptr(), k_pack.data_ptr() + off, v_pack.data_ptr() + off
     a.pos = pvec.data_ptr()
@@ -675,6 +687,8 @@ def run_split_attn(*, ws, pos: torch.Tensor, slot: int, rows: int, layer: int, u
             raise ValueError("attn_in and gate_w must share a dtype, unit-stride rows")
         if tuple(gw.shape) != (H, gate_n):
             raise ValueError(f"gate_w[layer] has shape {tuple(gw.shape)}, expected {(H, gate_n)}")
+        if attn_in.dim() != 2 or int(attn_in.shape[0]) < rows or int(attn_in.shape[1]) < gate_n:
+            raise ValueError(f"attn_in must hold {rows} rows of at least {gate_n} features")
         gate = torch.empty(rows, H, dtype=torch.float32, device=q.device)
         rc = _lib.load().altxs_attn_gate(attn_in.data_ptr(), _act_code(attn_in, "attn_in"),
                                          attn_in.stride(0), gw.data_ptr(), H, gate_n, rows,
