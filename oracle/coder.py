@@ -28,7 +28,8 @@ _lib = None
 
 
 def build() -> str:
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    """Compile the C restatement (always, even when a built library exists)."""
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
     return _LIB_PATH
 
 
