@@ -27,6 +27,7 @@ F_COMMIT = 1 << 4
 F_RENORM = 1 << 5
 F_FINAL_ATTN = 1 << 6
 F_FINAL_MLP = 1 << 7
+F_FUSE_O = 1 << 8  # decode: the out-projection inside the attention launch (same bits)
 CDF_RENORM = 1
 ATTN_OPS_BF16 = 1
 ATTN_ROWS = 2
@@ -54,6 +55,7 @@ EXPORTS = (
     "altxs_attn_gate",
     "altxs_decode_attn",
     "altxs_step_workspace_bytes",
+    "altxs_step_fuses_out_proj",
     "altxs_step_plan_bytes",
     "altxs_step_plan_build",
     "altxs_step",
@@ -199,6 +201,8 @@ def load():
     L.altxs_decode_attn.argtypes = [ctypes.POINTER(AttnArgs), p]
     L.altxs_step_workspace_bytes.restype = i64
     L.altxs_step_workspace_bytes.argtypes = [ctypes.POINTER(StepDesc)]
+    L.altxs_step_fuses_out_proj.restype = i32
+    L.altxs_step_fuses_out_proj.argtypes = [ctypes.POINTER(StepDesc), i32]
     L.altxs_step_plan_bytes.restype = i64
     L.altxs_step_plan_bytes.argtypes = [ctypes.POINTER(StepDesc)]
     L.altxs_step_plan_build.restype = i32

@@ -4,6 +4,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "gemm.h"
 
 #ifndef ALTXS_ATT_WAVES
 #define ALTXS_ATT_WAVES 4  // waves per workgroup (tile T goes to wave T % waves)
@@ -32,6 +33,13 @@ struct AttnP {
   int xcd_rows;  // one-row kernel: rows in tiles of 8, tile t on XCD t % 8
   int kv_tail = -1;  // natural layouts: first row of the window's K/V (-1: at pos + t)
   int helpers = 0;   // small MHA decode launches: prefetch workgroups per (row, kv head)
+  // Out-projection terms (attn_mfma_task with OP = 1): o_part[(r * H + h) *
+  // o_n + n] is the sum over head h's 64 features of row r's output y times
+  // the codes of column n of the out-projection (o_codes, o_bits: its packed
+  // tiled tensor, K = H * 64), before the column's group scale.
+  const uint8_t* o_codes = nullptr;
+  float* o_part = nullptr;
+  int o_bits = 0, o_n = 0;
 };
 
 // Row of the cache that holds key j of a query of segment b whose window starts
@@ -90,7 +98,7 @@ __device__ __forceinline__ float row_dims_sum(const float (&x)[NK]) {
 template <int NK, int YBF16>
 __device__ __forceinline__ void finish_query(const AttnP& a, const float* m, const float* l, int ms,
                                              const float* acc, int as, int r, int h, int c,
-                                             const RowExtras<NK>& e) {
+                                             const RowExtras<NK>& e, uint16_t* ylds = nullptr) {
 #pragma clang fp contract(off)
   float M = -INFINITY;
 #pragma unroll
@@ -130,8 +138,13 @@ __device__ __forceinline__ void finish_query(const AttnP& a, const float* m, con
   const int64_t o = ((int64_t)r * a.H + h) * HD + c;
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
-    if (YBF16) ((uint16_t*)a.y)[o + 16 * k] = f32_to_bf16(y[k]);
-    else ((float*)a.y)[o + 16 * k] = y[k];
+    if (YBF16) {
+      const uint16_t yb = f32_to_bf16(y[k]);
+      ((uint16_t*)a.y)[o + 16 * k] = yb;
+      if (ylds) ylds[c + 16 * k] = yb;
+    } else {
+      ((float*)a.y)[o + 16 * k] = y[k];
+    }
   }
 }
 
@@ -150,11 +163,12 @@ __device__ __forceinline__ void merge_and_store(const AttnP& a, const MergeLds<G
 // start, so the finish step waits on no memory).
 template <int G, int YBF16>
 __device__ __forceinline__ void merge_and_store(const AttnP& a, const MergeLds<G>& sm, int r, int g,
-                                                int wave, int lane, const RowExtras<1>& e) {
+                                                int wave, int lane, const RowExtras<1>& e,
+                                                uint16_t* ylds = nullptr) {
   static_assert(G <= ATT_WAVES, "one wave per query head of the group");
   if (wave >= G) return;
   finish_query<1, YBF16>(a, &sm.m[0][wave], &sm.l[0][wave], G, &sm.acc[0][wave][0], G * HD, r,
-                         g * G + wave, lane, e);
+                         g * G + wave, lane, e, ylds);
 }
 
 __device__ __forceinline__ int clamp_pos(const AttnP& a, int b, int t, int pos_b) {
@@ -200,9 +214,22 @@ constexpr int kVstRow = HD + 8;
 // dim) comes from the wave's LDS copy of the tile (vst: ATT_WAVES x 64 x
 // kVstRow elements) by two transposed reads.  The MFMAs see the operands of the tiled layout, so both
 // layouts give the same bits for the same cache values.
-template <int G, int NP, int YBF16, int PF = 0, int NAT = 0>
+//
+// OP = the out-projection's code width (2, 3, 4 or 6; 0: none), for MHA
+// decode rows on the tiled cache with bf16 operands: the tail also forms this
+// head's terms of the out-projection (AttnP::o_part), so the out-projection
+// needs no launch of its own.  The GEMM (gemm_task, K-slices of 256 features
+// = four heads) computes, per output column n, t_h = the MFMA sum over head
+// h's features (two k-steps from zero) and then acc += scale * t_h head by
+// head; here the same two MFMAs run on the same operands -- the row's bf16 y
+// in every MFMA row, the column's codes as the B operand -- so t_h has the
+// GEMM's bits, and the reader applies the scales in the GEMM's order
+// (OutFin).  ys: 64 bf16 of LDS for the row.
+template <int G, int NP, int YBF16, int PF = 0, int NAT = 0, int OP = 0>
 __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, MergeLds<G>& sm,
-                                               uint16_t* vst = nullptr) {
+                                               uint16_t* vst = nullptr, uint16_t* ys = nullptr) {
+  static_assert(OP == 0 || OP == 2 || OP == 3 || OP == 4 || OP == 6, "out-projection width");
+  static_assert(!OP || (G == 1 && NP == 1 && YBF16 && !NAT), "out-projection terms: MHA, bf16, tiled");
   static_assert(TILE == 64, "the MFMA tiling below assumes 64-key tiles");
   const int b = r / a.W, t = r % a.W;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -275,6 +302,29 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   const uint16_t v_raw = NAT ? vb[(int64_t)key_row(a, p, nat_pb, nat_p) * HD + lane]
                              : vb[(int64_t)(p / TILE) * (TILE * HD) + kv_tile_v(p % TILE, lane)];
   const float g_raw = *(a.gate ? a.gate + (int64_t)r * a.H + hx : &kNoGate);
+  // OP: this lane's out-projection codes, loaded now and used in the tail.
+  // Column block nb = wave + ATT_WAVES q of weight block (nb, h / 4), k-steps
+  // 2 (h % 4) and 2 (h % 4) + 1: the low plane's word(s) of those steps and
+  // the word of the high plane that holds them (6 and 3 bits).  Every load is
+  // issued on every path (a column block past o_n reads block 0).
+  constexpr int kOpQ = 512 / (16 * ATT_WAVES);  // o_n <= 512
+  uint32_t ow[OP ? kOpQ : 1][3];
+  if constexpr (OP) {
+    constexpr bool wide = OP >= 4;
+    const int KB = (a.H * HD) >> 8, kb = g >> 2, gq = g & 3;
+    const int off0 = wide ? lane * 32 + 8 * gq : lane * 16 + 4 * gq;
+    const int off1 = wide ? off0 + 4 : off0;
+    const int off2 = OP == 6 ? 512 * 4 + lane * 16 + 4 * gq
+                     : OP == 3 ? 512 * 2 + lane * 8 + 4 * (gq >> 1) : off0;
+#pragma unroll
+    for (int qi = 0; qi < kOpQ; ++qi) {
+      const int nb = wave + ATT_WAVES * qi;
+      const uint8_t* blk = a.o_codes + ((int64_t)(16 * nb < a.o_n ? nb : 0) * KB + kb) * (512 * OP);
+      ow[qi][0] = *(const uint32_t*)(blk + off0);
+      ow[qi][1] = *(const uint32_t*)(blk + off1);
+      ow[qi][2] = *(const uint32_t*)(blk + off2);
+    }
+  }
 
   // q operand (B of the score MFMA): column col holds head col % G; k-step ks
   // covers dims 32*ks + 8*lg + [0, 8).  Scaled by 1/sqrt(64) (exact).
@@ -429,7 +479,35 @@ __device__ __forceinline__ void attn_mfma_task(const AttnP& a, int r, int g, Mer
   RowExtras<1> ex;
   ex.vv[0] = a.use_xsa ? bf16_to_f32(v_raw) : 0.f;
   ex.gv = g_raw;
-  merge_and_store<G, YBF16>(a, sm, r, g, wave, lane, ex);
+  merge_and_store<G, YBF16>(a, sm, r, g, wave, lane, ex, OP ? ys : nullptr);
+  if constexpr (OP) {
+    __syncthreads();  // the row's bf16 y is in ys
+    const int gq = g & 3;
+    // A operand of k-step ss: features 32 ss + 8 lg .. +8 of the head, the
+    // same in all 16 MFMA rows (so every row of t is the row's sum)
+    bf16x8 ya[2];
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) ya[ss] = __builtin_bit_cast(bf16x8, *(const u32x4*)(ys + 32 * ss + 8 * lg));
+    float* dst = a.o_part + ((int64_t)r * a.H + g) * a.o_n;
+#pragma unroll
+    for (int qi = 0; qi < kOpQ; ++qi) {
+      const int nb = wave + ATT_WAVES * qi;
+      if (16 * nb >= a.o_n) break;
+      // the steps' words where b_op_bf16<OP> reads k-steps 0 and 1: low-plane
+      // word(s) at p0[0] (and p0[1]), the high-plane word at p1[0] (3 bits:
+      // shifted so that the steps' bytes are its bytes 0 and 1)
+      uint32_t q0[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u}, q1[4] = {0u, 0u, 0u, 0u};
+      q0[0] = ow[qi][0];
+      if constexpr (OP >= 4) q0[1] = ow[qi][1];
+      if constexpr (OP == 6) q1[0] = ow[qi][2];
+      if constexpr (OP == 3) q1[0] = ow[qi][2] >> (16 * (gq & 1));
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss)
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ya[ss], altxs::b_op_bf16<OP>(q0, q1, ss, OP), t, 0, 0, 0);
+      if (lane < 16) dst[16 * nb + lane] = t[0];  // row 0, column lane of the block
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------

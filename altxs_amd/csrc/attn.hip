@@ -91,10 +91,11 @@ inline int attn_helpers(unsigned pairs) {
   return pairs < kAttnSmallGrid ? (int)(kAttnSmallGrid / pairs < 16 ? kAttnSmallGrid / pairs : 16) : 0;
 }
 
-template <int G, int NP, int YBF16, int PF, int NAT = 0>
+template <int G, int NP, int YBF16, int PF, int NAT = 0, int OP = 0>
 __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   __shared__ MergeLds<G> sm;
   __shared__ __attribute__((aligned(16))) uint16_t vst[NAT ? ATT_WAVES * TILE * kVstRow : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t ys[OP ? HD : 8];
   if constexpr ((G == 1 && PF == 1) || NAT) {
     const int pairs = a.B * a.W * a.Hkv;
     if (a.helpers > 0 && (int)blockIdx.x >= pairs) {
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_mfma_kernel(AttnP a) {
   }
   // GQA launches have G times fewer workgroups, and small launches (PF = 1)
   // too few to cover the load latency: keep two tiles per wave in flight
-  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : PF), NAT>(a, r, g, sm, vst);
+  attn_mfma_task<G, NP, YBF16, (G > 1 ? 1 : PF), NAT, OP>(a, r, g, sm, vst, ys);
 }
 
 // Windows (W > 1) on the bf16 cache: 16*NG query rows of one (segment, head)
@@ -361,6 +362,42 @@ hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s) {
   p.kv_tail = a.kv_tail_end > 0 ? a.kv_tail_end - a.W : -1;
   return a.y_bf16 ? launch_y<1>(p, group, a.kv_bf16, ops_bf16, rows_only, s)
                   : launch_y<0>(p, group, a.kv_bf16, ops_bf16, rows_only, s);
+}
+
+// The decode launch with the out-projection terms (attn_mfma_task, OP = 1):
+// W = 1 rows, MHA, the tiled bf16 cache, bf16 operands and output; o_bits in
+// {2, 3, 4, 6}, o_n a multiple of 16 up to 512, H a multiple of 4.  The
+// kernel variant and placement are those altxs_launch_attn picks.
+hipError_t altxs_launch_attn_o(const AltxsAttnArgs& a, const uint8_t* o_codes, int o_bits, int o_n,
+                               float* o_part, hipStream_t s) {
+  if (a.W != 1 || a.H != a.Hkv || a.kv_bf16 != ALTXS_KV_BF16 || !a.y_bf16 ||
+      (a.flags & ALTXS_ATTN_OPS_BF16) == 0 || a.kv_tail_end != 0 || a.H % 4 != 0 ||
+      !(o_bits == 2 || o_bits == 3 || o_bits == 4 || o_bits == 6) || o_n < 16 || o_n > 512 ||
+      o_n % 16 != 0 || !o_codes || !o_part)
+    return hipErrorInvalidValue;
+  AttnP p;
+  p.B = a.B; p.W = a.W; p.H = a.H; p.Hkv = a.Hkv; p.max_len = a.max_len;
+  p.q = a.q; p.k = a.k; p.v = a.v; p.seg_stride = a.kv_seg_stride;
+  p.pos = a.pos; p.gate = a.gate; p.use_xsa = a.use_xsa; p.y = a.y; p.err = a.err;
+  p.xcd_rows = ((a.flags & ALTXS_ATTN_XCD_ROWS) != 0 && (int64_t)a.B % 64 == 0) ? 1 : 0;
+  p.o_codes = o_codes; p.o_bits = o_bits; p.o_n = o_n; p.o_part = o_part;
+  const dim3 grid((unsigned)(p.B * p.Hkv)), block(ATT_THREADS);
+  const bool small = grid.x < kAttnSmallGrid && !p.xcd_rows;  // as launch_y: prefetch workgroups beside
+  if (small) p.helpers = attn_helpers(grid.x);
+  const dim3 g2(small ? grid.x * (1 + p.helpers) : grid.x);
+#define OP_GO(B)                                                                                \
+  do {                                                                                          \
+    if (small) hipLaunchKernelGGL((attn_mfma_kernel<1, 1, 1, 1, 0, B>), g2, block, 0, s, p);      \
+    else hipLaunchKernelGGL((attn_mfma_kernel<1, 1, 1, ALTXS_ATT_PF, 0, B>), g2, block, 0, s, p); \
+    return hipGetLastError();                                                                   \
+  } while (0)
+  switch (o_bits) {
+    case 2: OP_GO(2);
+    case 3: OP_GO(3);
+    case 4: OP_GO(4);
+    default: OP_GO(6);
+  }
+#undef OP_GO
 }
 
 extern "C" int32_t altxs_decode_attn(const AltxsAttnArgs* a, altxs_stream_t stream) {

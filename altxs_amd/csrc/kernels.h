@@ -17,3 +17,9 @@ hipError_t altxs_launch_cdf_stats(const float* logits, const float2* stats, int6
 
 struct AltxsAttnArgs;
 hipError_t altxs_launch_attn(const AltxsAttnArgs& a, hipStream_t s);
+// The same decode launch also forming the out-projection's per-head terms
+// (o_part[(r * H + h) * o_n + n], before the group scales); hipErrorInvalidValue
+// for the shapes it does not cover (W = 1, MHA, tiled bf16 cache, bf16
+// operands and output, o_bits in {2, 3, 4, 6}, o_n % 16 == 0, o_n <= 512).
+hipError_t altxs_launch_attn_o(const AltxsAttnArgs& a, const uint8_t* o_codes, int o_bits, int o_n,
+                               float* o_part, hipStream_t s);

@@ -15,6 +15,7 @@ struct WS {
   float2* STATS;
   int* SYNC;  // step counters (zeroed by the embedding kernel)
   int nsync;
+  float* OPART;  // decode: the out-projection's per-head terms [Rp][H][D]
 };
 
 // One slot of the layer plan: everything a slot's tasks read besides the

@@ -110,11 +110,14 @@ int64_t carve(const AltxsStepDesc* d, int nb, WS* w, char* base) {
   // 64-byte group of completion counters per (slot, row tile)
   const int nsync = kTicketPad + (int)(n * (Rp / 16)) * kCtrStride;
   char* sync = take(nsync * 4);
+  // ALTXS_F_FUSE_O decode steps: the out-projection's per-head terms
+  char* opart = take(d->W == 1 && (d->flags & ALTXS_F_FUSE_O) ? Rp * d->H * D * 4 : 0);
   if (w) {
     w->X0 = (float*)x0; w->X1 = (float*)x1; w->XIN = (float*)xin; w->QIN = (float*)qin;
     w->XOUT = (float*)xout;
     w->Q = (float*)q; w->GATE = (float*)gate; w->Y = y; w->HB = hb;
     w->STATS = (float2*)stats; w->SYNC = (int*)sync; w->nsync = nsync;
+    w->OPART = (float*)opart;
   }
   return off;
 }
@@ -129,6 +132,25 @@ int split_fork_stage() {
     if (f < 0 || f > 2) f = 0;
   }
   return f;
+}
+
+// ALTXS_F_FUSE_O, for decode steps (R rows) on the tiled bf16 cache with
+// bf16 activations and a packed MHA out-projection: the attention launch also
+// forms the out-projection's per-head terms, and the out-projection is
+// finished where its result is read -- the MLP-up prologue of a sequential
+// slot (ProOutNorm), the MLP-down epilogue of a parallel one (OutFin) -- one
+// launch fewer per slot, the same bits.  Not the default: every MLP-up
+// column task of a sequential slot then reads H terms per element instead of
+// one, and each attention workgroup decodes the out-projection's codes of its
+// head for its one row (the GEMM decodes them once per 8-row tile); cfg3,
+// per slot: attention +2.5 us, MLP up +6.4 us (B = 64) / +2.5 us (B = 1),
+// against the 4.4-4.6 us launch saved.
+bool out_proj_fused(const AltxsStepDesc* d, int s, int R) {
+  const AltxsLayer& L = d->layers[d->slots[s].layer];
+  return d->act_bf16 && (d->flags & ALTXS_F_FUSE_O) && d->W == 1 && R < kBigRows &&
+         !d->plan_dev && d->kv_bf16 == ALTXS_KV_BF16 && d->kv_tail_end == 0 && d->H == d->Hkv &&
+         d->H % 4 == 0 && d->D <= 512 && d->D % 16 == 0 && L.o.N == d->D && L.o.K == (int64_t)d->H * HD &&
+         (L.o.bits == 2 || L.o.bits == 3 || L.o.bits == 4 || L.o.bits == 6);
 }
 
 // Two segment groups (split mode) when the caller hands in a second stream.
@@ -421,11 +443,24 @@ struct StepRun {
     return a;
   }
 
+  bool fuse_o(const Group& G, int s) const { return out_proj_fused(d, s, G.nb * d->W); }
+  OutFin out_fin(const AltxsLayer& L) const {
+    OutFin f;
+    f.osc = (const uint16_t*)L.o.scales; f.attn_scale = L.attn_scale; f.H = d->H; f.ks = pick_ks(L.o.K, kKsO);
+    return f;
+  }
+
   hipError_t attn(const Group& G, int s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) const {
     const AltxsAttnArgs a = attn_args(G, s);
     hipError_t e;
     if (ev0 && (e = hipEventRecord(ev0, st)) != hipSuccess) return e;
-    if ((e = altxs_launch_attn(a, st)) != hipSuccess) return e;
+    if (fuse_o(G, s)) {
+      const AltxsQTensor& o = d->layers[d->slots[s].layer].o;
+      if ((e = altxs_launch_attn_o(a, (const uint8_t*)o.codes, o.bits, d->D, G.w.OPART, st)) != hipSuccess)
+        return e;
+    } else if ((e = altxs_launch_attn(a, st)) != hipSuccess) {
+      return e;
+    }
     if (ev1 && (e = hipEventRecord(ev1, st)) != hipSuccess) return e;
     return hipSuccess;
   }
@@ -442,7 +477,8 @@ struct StepRun {
     const float* lane1_in = par ? (S.first_parallel ? xin_slot : w.X1 + s * Rp * D) : nullptr;
     float* base_s = w.XIN + (s & 1) * Rp * D;      // x_in (seq) / lane0 after skip (par)
     hipError_t e;
-    {  // out-projection + attention residual
+    const bool fo = fuse_o(G, s);
+    if (!fo) {  // out-projection + attention residual
       EpiO epi{base_s, L.attn_scale, w.XOUT, d->D, par ? 1 : 0};
       if (big(R, L.o))
         e = launch_gemm_big4(kKsO, qt_big(L.o).bits, qt_big(L.o), R, (const uint16_t*)w.Y, epi, st);
@@ -460,7 +496,15 @@ struct StepRun {
     {  // MLP up + LeakyReLU(0.5)^2
       ProNorm pro{par ? lane1_in : w.XOUT, nullptr, 0, L.ln_scale, d->norm_eps, d->D};
       EpiUp epi{w.HB, d->F, hb16};
-      if (big(R, L.up) && band_norm_fits(qt_of(L.up))) {
+      if (fo && !par) {  // sequential slot: the out-projection finished in the prologue
+        if constexpr (AM == A_BF16) {
+          ProOutNorm po{out_fin(L), base_s, w.XOUT, L.ln_scale, d->norm_eps, d->D};
+          po.of.part = w.OPART;
+          e = launch_gemm4<AM>(kKsUp, L.up.bits, qt_of(L.up), R, ADirect{nullptr, 0}, po, epi, 0, st, xr(G));
+        } else {
+          e = hipErrorInvalidValue;
+        }
+      } else if (big(R, L.up) && band_norm_fits(qt_of(L.up))) {
         e = launch_gemm_band_norm4(kKsUp, qt_big(L.up).bits, qt_big(L.up), R, pro, epi, st);
       } else if (big(R, L.up)) {  // normalised rows in Y (the out-projection has read it)
         if ((e = launch_norm_rows(pro, R, d->D, (uint16_t*)w.Y, st)) != hipSuccess) return e;
@@ -472,31 +516,47 @@ struct StepRun {
       if (e != hipSuccess) return e;
     }
     {  // MLP down + residual / lanes
-      EpiDown epi;
-      epi.xout = w.XOUT; epi.mlp_scale = L.mlp_scale;
-      epi.out0 = w.X0 + (s + 1) * Rp * D; epi.out1 = w.X1 + (s + 1) * Rp * D;
-      epi.lane0 = base_s; epi.lane1 = lane1_in; epi.pr = L.par_resid; epi.pp = L.par_post;
-      epi.D = d->D; epi.parallel = par ? 1 : 0;
-      if (s + 1 < d->n_slots) {  // the next slot's residual base and attention input
-        const AltxsSlot& S1 = d->slots[s + 1];
-        const bool par1 = S1.kind == ALTXS_SLOT_PAR;
-        NextIn& nx = epi.next;
-        nx.x0 = w.X0;
-        nx.skip = S1.skip_src >= 0 ? w.X0 + (S1.skip_src + 1) * Rp * D : nullptr;
-        nx.skip_w = S1.skip_src >= 0 ? d->skip_weights + (int64_t)S1.skip_idx * D : nullptr;
-        nx.skip_g = (S1.skip_src >= 0 && (d->flags & ALTXS_F_SKIP_GATES) && d->skip_gates)
-                        ? d->skip_gates + (int64_t)S1.skip_idx * D : nullptr;
-        nx.mix = d->layers[S1.layer].resid_mix;
-        nx.base = w.XIN + ((s + 1) & 1) * Rp * D;
-        nx.attn = par1 ? w.QIN + ((s + 1) & 1) * Rp * D : nx.base;
-        nx.parallel = par1 ? 1 : 0;
-        nx.skip_self = S1.skip_src == s ? 1 : 0;
+      auto fill = [&](auto& epi) {
+        epi.xout = w.XOUT; epi.mlp_scale = L.mlp_scale;
+        epi.out0 = w.X0 + (s + 1) * Rp * D; epi.out1 = w.X1 + (s + 1) * Rp * D;
+        epi.lane0 = base_s; epi.lane1 = lane1_in; epi.pr = L.par_resid; epi.pp = L.par_post;
+        epi.D = d->D; epi.parallel = par ? 1 : 0;
+        if (s + 1 < d->n_slots) {  // the next slot's residual base and attention input
+          const AltxsSlot& S1 = d->slots[s + 1];
+          const bool par1 = S1.kind == ALTXS_SLOT_PAR;
+          NextIn& nx = epi.next;
+          nx.x0 = w.X0;
+          nx.skip = S1.skip_src >= 0 ? w.X0 + (S1.skip_src + 1) * Rp * D : nullptr;
+          nx.skip_w = S1.skip_src >= 0 ? d->skip_weights + (int64_t)S1.skip_idx * D : nullptr;
+          nx.skip_g = (S1.skip_src >= 0 && (d->flags & ALTXS_F_SKIP_GATES) && d->skip_gates)
+                          ? d->skip_gates + (int64_t)S1.skip_idx * D : nullptr;
+          nx.mix = d->layers[S1.layer].resid_mix;
+          nx.base = w.XIN + ((s + 1) & 1) * Rp * D;
+          nx.attn = par1 ? w.QIN + ((s + 1) & 1) * Rp * D : nx.base;
+          nx.parallel = par1 ? 1 : 0;
+          nx.skip_self = S1.skip_src == s ? 1 : 0;
+        }
+      };
+      if (fo && par) {  // parallel slot: the attention term from the out-projection's terms
+        if constexpr (AM == A_BF16) {
+          EpiDownT<true> epi;
+          fill(epi);
+          epi.ofin = out_fin(L);
+          epi.ofin.part = w.OPART;
+          e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
+                               epi, 0, st, xr(G));
+        } else {
+          e = hipErrorInvalidValue;
+        }
+      } else {
+        EpiDown epi;
+        fill(epi);
+        if (big(R, L.down))
+          e = launch_gemm_big4(kKsDown, L.down.bits, qt_of(L.down), R, (const uint16_t*)w.HB, epi, st);
+        else
+          e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
+                               epi, 0, st, xr(G));
       }
-      if (big(R, L.down))
-        e = launch_gemm_big4(kKsDown, L.down.bits, qt_of(L.down), R, (const uint16_t*)w.HB, epi, st);
-      else
-        e = launch_gemm4<AM>(kKsDown, L.down.bits, qt_of(L.down), R, ADirect{w.HB, 0}, ProNone{},
-                             epi, 0, st, xr(G));
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -713,6 +773,12 @@ hipError_t run_split(const AltxsStepDesc* d, const Group (&G)[2], hipStream_t s0
 extern "C" int64_t altxs_step_workspace_bytes(const AltxsStepDesc* d) {
   if (!d) return -1;
   return ws_bytes_needed(d);
+}
+
+extern "C" int32_t altxs_step_fuses_out_proj(const AltxsStepDesc* d, int32_t slot) {
+  if (!d || slot < 0 || slot >= d->n_slots || d->n_slots > ALTXS_MAX_SLOTS) return -1;
+  const int nb0 = (d->B + 1) / 2;
+  return out_proj_fused(d, slot, split_mode(d) ? nb0 : d->B * d->W) ? 1 : 0;
 }
 
 extern "C" int64_t altxs_step_plan_bytes(const AltxsStepDesc* d) {

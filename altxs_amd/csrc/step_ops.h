@@ -796,7 +796,60 @@ struct EpiUp {
   }
 };
 
-struct EpiDown {
+// The out-projection of a parallel slot, finished where its only reader is:
+// the attention launch formed part[(r * H + h) * D + n], head h's MFMA sum
+// for output column n (attn_mfma_task, OP); the GEMM (gemm_task on the packed
+// tensor with scales osc, ks K-slices of H / ks heads) forms acc += scale(n, h)
+// * t_h head by head from zero in each slice and adds the slices in order,
+// and EpiO's o_el scales by attn_scale -- the same operations here give the
+// value the separate launch stores in x_out.
+struct OutFin {
+  static constexpr int HMAX = 8;
+  const float* part = nullptr;  // NULL: x_out comes from the out-projection launch
+  const uint16_t* osc = nullptr;
+  const float* attn_scale = nullptr;
+  int H = 0, ks = 1;
+  struct El { float t[HMAX], s[HMAX], a; };
+  __device__ El load(int r, int c, int D) const {
+    El e;
+    const int KB = H >> 2;
+#pragma unroll
+    for (int kb = 0; kb < HMAX / 4; ++kb) {
+      if (kb < KB) {  // the column's four group scales of block kb
+        const u32x2 w = *(const u32x2*)(osc + ((int64_t)(c >> 4) * KB + kb) * 64 + (c & 15) * 4);
+        e.s[4 * kb] = half_lo(w[0]);
+        e.s[4 * kb + 1] = half_hi(w[0]);
+        e.s[4 * kb + 2] = half_lo(w[1]);
+        e.s[4 * kb + 3] = half_hi(w[1]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < HMAX; ++h)
+      if (h < H) e.t[h] = part[((int64_t)r * H + h) * D + c];
+    e.a = attn_scale[c];
+    return e;
+  }
+  __device__ float value(const El& e) const {
+    const int hps = H / ks;
+    float sum = 0.f, acc = 0.f;
+#pragma unroll
+    for (int h = 0; h < HMAX; ++h) {
+      if (h < H) {
+        acc += e.s[h] * e.t[h];
+        if ((h + 1) % hps == 0) {  // end of a K-slice: slices added in order
+          sum = h + 1 == hps ? acc : sum + acc;
+          acc = 0.f;
+        }
+      }
+    }
+    return o_el(sum, e.a, 0.f, 1);
+  }
+};
+
+// OF: a parallel slot whose out-projection the attention launch formed --
+// the attention term comes from OutFin instead of x_out.
+template <bool OF>
+struct EpiDownT {
   const float* xout;   // seq: x_out; par: attn term a
   const float* mlp_scale;
   float* out0;         // seq: slot output; par: lane0'
@@ -807,9 +860,11 @@ struct EpiDown {
   const float* pp;     // par: [2, 2]
   int D, parallel;
   NextIn next;  // inputs of the following slot (next.base == NULL: none)
+  OutFin ofin;  // OF: the out-projection's head terms
   template <class Cfg> struct Pre {
     float xo[EW<Cfg>::EPT], sc[EW<Cfg>::EPT], l0[EW<Cfg>::EPT], l1[EW<Cfg>::EPT];
     NextIn::El nx[EW<Cfg>::EPT];
+    OutFin::El of[OF ? EW<Cfg>::EPT : 1];
   };
   template <class Cfg>
   __device__ Pre<Cfg> prefetch(int m0, int n0, int R, int) const {
@@ -819,7 +874,11 @@ struct EpiDown {
       const int r = m0 + EW<Cfg>::row(j), c = n0 + EW<Cfg>::col(j);
       const bool ok = r < R && c < D;
       const int64_t idx = (int64_t)r * D + c;
-      o.xo[j] = ok ? xout[idx] : 0.f;
+      if constexpr (OF) {
+        if (ok) o.of[j] = ofin.load(r, c, D);
+      } else {
+        o.xo[j] = ok ? xout[idx] : 0.f;
+      }
       o.sc[j] = ok ? mlp_scale[c] : 0.f;
       o.l0[j] = (ok && parallel) ? lane0[idx] : 0.f;
       o.l1[j] = (ok && parallel) ? lane1[idx] : 0.f;
@@ -835,15 +894,17 @@ struct EpiDown {
       const int r = m0 + rr, c = n0 + cc;
       if (r >= R || c >= D) continue;
       const int64_t o = (int64_t)r * D + c;
-      const DownOut y = down_el(C[rr * Cfg::CS + cc], pre.sc[j], pre.xo[j], pre.l0[j], pre.l1[j],
-                                parallel, pr, pp);
+      float xo;
+      if constexpr (OF) xo = ofin.value(pre.of[OF ? j : 0]);
+      else xo = pre.xo[j];
+      const DownOut y = down_el(C[rr * Cfg::CS + cc], pre.sc[j], xo, pre.l0[j], pre.l1[j], parallel, pr, pp);
       out0[o] = y.x;
       if (parallel) out1[o] = y.x1;
       if (next.base) next.put(o, y.x, pre.nx[j]);
     }
   }
   static constexpr bool kStrip = true;
-  __device__ bool strip_ok() const { return true; }
+  __device__ bool strip_ok() const { return !OF; }  // strips read x_out
   template <class Cfg>
   __device__ void strip(const float* Cst, int r0, int n0, int R) const {
     const int rr = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8, r = r0 + rr;
@@ -890,6 +951,124 @@ struct EpiDown {
     }
   }
 };
+using EpiDown = EpiDownT<false>;
+
+// The MLP-up prologue of a sequential slot whose out-projection terms the
+// attention launch formed (attn_mfma_task, OP): every column task needs the
+// slot's whole x_out rows for the RMS norm, so each forms them (OutFin's
+// arithmetic, plus the residual base of EpiO) in LDS -- the first column task
+// also stores them for the MLP-down epilogue -- and then normalises them with
+// ProNorm's arithmetic and lane layout.
+struct ProOutNorm {
+  static constexpr bool kStage = true;
+  static constexpr int XS = 512 + 4;  // LDS row stride of the staged x_out (floats)
+  static constexpr size_t kScratch = (size_t)16 * XS * 4;
+  static constexpr int HMAX = OutFin::HMAX;
+  OutFin of;                // part, osc, attn_scale, H, ks
+  const float* xin;         // residual base
+  float* xout;              // [R, D], stored by the first column task
+  float scale, eps;
+  int D;
+  template <int AM, int NT>
+  __device__ void stage(void* As, void* scratch, int m0, int R, int K, int, bool first) const {
+    static_assert(NT == 16 * PTPR, "one row per 16 lanes, 16 rows per task");
+    float* xs = (float*)scratch;
+    const int t = threadIdx.x;
+    {  // x_out of the task's rows, four columns per thread
+      const int nq = D >> 2, rgs = NT / nq, cq = t % nq, rg = t / nq;
+      const int c0 = 4 * cq, KB = of.H >> 2, hps = of.H / of.ks, H = of.H;
+      float scl[HMAX][4];
+#pragma unroll
+      for (int kb = 0; kb < HMAX / 4; ++kb) {
+        if (kb < KB) {  // 16 scales: columns c0 .. c0+3 x the block's four groups
+          const uint16_t* sp = of.osc + ((int64_t)(c0 >> 4) * KB + kb) * 64 + (c0 & 15) * 4;
+          const u32x4 lo = *(const u32x4*)sp, hi = *(const u32x4*)(sp + 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const u32x4& w = e < 2 ? lo : hi;
+            const uint32_t w0 = w[2 * (e & 1)], w1 = w[2 * (e & 1) + 1];
+            scl[4 * kb + 0][e] = half_lo(w0);
+            scl[4 * kb + 1][e] = half_hi(w0);
+            scl[4 * kb + 2][e] = half_lo(w1);
+            scl[4 * kb + 3][e] = half_hi(w1);
+          }
+        }
+      }
+      const f32x4 asc = *(const f32x4*)(of.attn_scale + c0);
+      for (int i0 = 0; i0 < 16 / rgs; i0 += 2) {
+        if (m0 + rgs * i0 >= R) break;  // no row of this pair is below R in any thread
+        f32x4 tv[2][HMAX], base[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {  // every load on every path (rows past R read row R - 1)
+          const int r = m0 + rg + rgs * (i0 + u), rc = r < R ? r : R - 1;
+#pragma unroll
+          for (int h = 0; h < HMAX; ++h)
+            if (h < H) tv[u][h] = *(const f32x4*)(of.part + ((int64_t)rc * H + h) * D + c0);
+          base[u] = *(const f32x4*)(xin + (int64_t)rc * D + c0);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int row = rg + rgs * (i0 + u), r = m0 + row;
+          if (r >= R) continue;
+          float xo[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float sum = 0.f, acc = 0.f;
+#pragma unroll
+            for (int h = 0; h < HMAX; ++h) {
+              if (h < H) {
+                acc += scl[h][e] * tv[u][h][e];
+                if ((h + 1) % hps == 0) {  // end of a K-slice: slices added in order
+                  sum = h + 1 == hps ? acc : sum + acc;
+                  acc = 0.f;
+                }
+              }
+            }
+            xo[e] = o_el(sum, asc[e], base[u][e], 0);
+          }
+          const f32x4 o = {xo[0], xo[1], xo[2], xo[3]};
+          *(f32x4*)(xs + row * XS + c0) = o;
+          if (first) *(f32x4*)(xout + (int64_t)r * D + c0) = o;
+        }
+      }
+      __syncthreads();
+    }
+    // ProNorm (lane_mode 0, no gate, unrounded scale) on the staged rows
+    const int row = t / PTPR, li = t % PTPR;
+    const int r = m0 + row;
+    const int nch = D >> 2;
+    f32x4 v[PMAXJ];
+#pragma unroll
+    for (int j = 0; j < PMAXJ; ++j) {
+      const int c = li + PTPR * j;
+      if (c < nch && r < R) v[j] = *(const f32x4*)(xs + row * XS + 4 * c);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < PMAXJ; ++j) {
+      const int c = li + PTPR * j;
+      if (c >= nch) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y = r < R ? v[j][e] : 0.f;
+        v[j][e] = y;
+        ss += y * y;
+      }
+    }
+    ss = row16_sum(ss);
+    const float inv = r < R ? rsqrtf(ss / (float)D + eps) : 0.f;
+#pragma unroll
+    for (int j = 0; j < PMAXJ; ++j) {
+      const int c = li + PTPR * j;
+      if (c >= nch) continue;
+      float n[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) n[e] = (v[j][e] * inv) * scale;
+      a_store4<AM>(As, row, 4 * c, K, n);
+    }
+  }
+};
+
 
 __device__ __forceinline__ float softcap_el(float l, float cp, float cn, float icp, float icn) {
   const bool pos = l >= 0.f;

@@ -112,7 +112,8 @@ class StaticState:
         if R >= BIG_ROWS and model.act_bf16 and model.expand is not False:
             model.expand_codes()  # the large-tile GEMMs of this state read the expanded values
         self._descs: dict[int, _lib.StepDesc] = {}
-        desc = self._desc(0)
+        # decode states reserve the fused out-projection's terms (StepModel.fuse_o)
+        desc = self._desc(_lib.F_FUSE_O if win == 1 else 0)
         nbytes = _lib.load().altxs_step_workspace_bytes(ctypes.byref(desc))
         self.ws = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
         self._descs.clear()
@@ -216,6 +217,10 @@ class StepModel:
         self.synth = synth
         self._cos_cache: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         self._disabled = False
+        # True: decode steps form the out-projection inside the attention
+        # launch and finish it where it is read (ALTXS_F_FUSE_O; the same bits,
+        # slower on the benchmark model)
+        self.fuse_o = False
         self.expand = expand
         self._expanded = False
         if expand:
@@ -359,10 +364,21 @@ class StepModel:
         B*width rows; a commit advances pos by width.
         """
         flags = (_lib.F_COMMIT if commit else 0) | (_lib.F_RENORM if renorm else 0)
+        if self.fuse_o:
+            flags |= _lib.F_FUSE_O
         d = st._desc(flags, width)
         d.attn_events = attn_events
         rc = self.lib.altxs_step(ctypes.byref(d), ctypes.c_void_p(_stream_ptr(self.device)))
         _lib.check(rc, "altxs_step")
+
+    def fuses_out_proj(self, st: StaticState, slot: int = 0) -> bool:
+        """Whether a step on ``st`` forms slot ``slot``'s out-projection inside
+        its attention launch (altxs_step_fuses_out_proj)."""
+        flags = _lib.F_FUSE_O if self.fuse_o else 0
+        v = int(self.lib.altxs_step_fuses_out_proj(ctypes.byref(st._desc(flags)), int(slot)))
+        if v < 0:
+            raise ValueError(f"altxs_step_fuses_out_proj: bad slot {slot}")
+        return v == 1
 
     def static_extend(self, st: StaticState) -> None:
         """One W-token window at ``pos`` (logits, probs, CDFs); pos unchanged."""

@@ -91,18 +91,25 @@ class SynthModel:
 
 
 def make_model(cfg: AltxsConfig, *, seed: int = WEIGHT_SEED, std: float = 0.02,
-               softcap: tuple[float, float] | None = None, dense: bool | int = False) -> SynthModel:
+               softcap: tuple[float, float] | None = None, dense: bool | int = False,
+               bits: dict[str, int] | None = None) -> SynthModel:
     """``dense``: every matrix kept dense instead of the mixed-bit packing --
     True or 16: bf16 (the reference's runtime banks); 32: fp32 (its fp32
-    compute mode)."""
+    compute mode).  ``bits``: widths of named tensors (e.g. ``{"l0.o": 6}``)
+    in place of the allocation's."""
     cfg.validate()
     rng = np.random.default_rng(seed)
     d, kvd, f = cfg.model_dim, cfg.kv_dim, cfg.hidden_dim
     names = tensor_list(cfg)
+    override = dict(bits or {})
     if dense:
         bits = {nm: (32 if dense == 32 else 16) for nm, _, _ in names}
     else:
         bits = allocate_bits([(nm, nn * kk) for nm, nn, kk in names], cfg.bpw_target)
+    unknown = set(override) - set(bits)
+    if unknown:
+        raise ValueError(f"no tensors named {sorted(unknown)}")
+    bits.update(override)
     packed = {}
     for nm, nn, kk in names:
         w = rng.standard_normal((nn, kk), dtype=np.float32) * np.float32(std)

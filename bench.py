@@ -625,6 +625,9 @@ def main() -> int:
                     help="the fused dequant-GEMV/GEMM microbenchmark (512x2048 and 2048x512, 2/3/4/6 bits, "
                          "B=1 and 64) over >= --cfg2-gb GB of distinct packed matrices")
     ap.add_argument("--cfg2-gb", type=float, default=2.0)
+    ap.add_argument("--fuse-o", action="store_true",
+                    help="decode: form the out-projection inside the attention launch and finish "
+                         "it where it is read, instead of its own launch (the same bits)")
     ap.add_argument("--persistent", action="store_true",
                     help="run every slot in one persistent launch (tasks in dependency order)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -673,6 +676,7 @@ def main() -> int:
     sm = synth.make_model(cfg, dense=a.dense)
     log(f"model {a.profile}: {sm.bits_summary()['bpw']:.4f} bpw, built in {time.time() - t0:.1f}s")
     model = StepModel(sm, act=a.act, kv=a.kv)
+    model.fuse_o = a.fuse_o
     st = model.make_static_state(max_len, win=1, batch=B, want_probs=False, want_cdf=True,
                                  split=a.streams == 2, persistent=a.persistent)
     groups = 2 if st.split else 1

@@ -326,6 +326,9 @@ enum {
   ALTXS_F_RENORM = 1 << 5,      /* renormalise probs before the CDF (ALTXS_CDF_RENORM; V <= 16384) */
   ALTXS_F_FINAL_ATTN = 1 << 6,  /* parallel_final_lane = "attn" (default mean) */
   ALTXS_F_FINAL_MLP = 1 << 7,   /* parallel_final_lane = "mlp" */
+  ALTXS_F_FUSE_O = 1 << 8,      /* decode: form the out-projection inside the attention launch
+                                 * and finish it where it is read (the same bits; slower on
+                                 * the benchmark model, so off by default) */
 };
 
 enum { ALTXS_SLOT_SEQ = 0, ALTXS_SLOT_PAR = 1 };
@@ -425,6 +428,17 @@ typedef struct AltxsStepDesc {
 
 /* Workspace bytes altxs_step needs for this descriptor (host-only). */
 int64_t altxs_step_workspace_bytes(const AltxsStepDesc *d);
+
+/* Whether altxs_step forms slot `slot`'s out-projection inside the attention
+ * launch (per-head MFMA terms) and finishes it in the MLP-up prologue
+ * (sequential slot) or the MLP-down epilogue (parallel slot) instead of a
+ * launch of its own (host-only): 1 yes, 0 no, <0 bad arguments.  The
+ * reference runs the out-projection as one stage of its fused step
+ * (src/xsa_ttt/ac_gemv.py:89-310, persistent_step.py:777-811); here it is done
+ * when d->flags has ALTXS_F_FUSE_O, for decode steps (W = 1) with bf16
+ * activations, the tiled bf16 cache, MHA and a packed out-projection.  Either
+ * way the results are the same bits. */
+int32_t altxs_step_fuses_out_proj(const AltxsStepDesc *d, int32_t slot);
 
 /* Bytes of the persistent-kernel plan for this descriptor (host-only; <0 on error). */
 int64_t altxs_step_plan_bytes(const AltxsStepDesc *d);
