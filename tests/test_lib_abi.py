@@ -121,3 +121,35 @@ int main(void) {{
           _lib.CodecGroups.mode.offset, ctypes.sizeof(_lib.FfnStageArgs), _lib.FfnStageArgs.out_w.offset,
           _lib.FfnStageArgs.y.offset, _lib.FfnStageArgs.skips.offset]
     assert c_sizes == py
+
+
+def test_fused_out_projection_query_host_logic():
+    """altxs_step_fuses_out_proj reads only the descriptor (no GPU): the fused
+    out-projection is taken with ALTXS_F_FUSE_O for W = 1, bf16 activations,
+    the tiled bf16 cache, MHA and a packed out-projection, and not otherwise;
+    it also sizes the workspace for the head terms."""
+    L = _lib.load()
+    d = _lib.StepDesc()
+    d.abi_version = _lib.ABI_VERSION
+    d.B, d.W, d.D, d.H, d.Hkv, d.head_dim, d.F, d.V = 4, 1, 512, 8, 8, 64, 2048, 16384
+    d.n_layers, d.n_slots, d.max_len = 2, 2, 256
+    d.act_bf16, d.kv_bf16 = 1, _lib.KV_BF16
+    for i in range(2):
+        d.layers[i].o = _lib.QTensor(1 << 20, 1 << 20, 512, 512, 3, 0)
+        d.slots[i].layer = i
+    q = lambda s=0: L.altxs_step_fuses_out_proj(ctypes.byref(d), s)
+    assert q() == 0  # off by default
+    base = L.altxs_step_workspace_bytes(ctypes.byref(d))
+    d.flags = _lib.F_FUSE_O
+    assert q(0) == 1 and q(1) == 1
+    # Rp x H x D fp32 per segment group (the split layout's two groups of 16 rows are the larger)
+    assert L.altxs_step_workspace_bytes(ctypes.byref(d)) == base + 2 * 16 * 8 * 512 * 4
+    assert q(2) == -1 and q(-1) == -1
+    assert L.altxs_step_fuses_out_proj(None, 0) == -1
+    for field, value in (("W", 4), ("act_bf16", 0), ("kv_bf16", _lib.KV_BF16_NATURAL), ("Hkv", 4)):
+        old = getattr(d, field)
+        setattr(d, field, value)
+        assert q() == 0, field
+        setattr(d, field, old)
+    d.layers[0].o.bits = 16  # dense bf16 out-projection
+    assert q(0) == 0 and q(1) == 1
