@@ -149,7 +149,7 @@ bool out_proj_fused(const AltxsStepDesc* d, int s, int R) {
   const AltxsLayer& L = d->layers[d->slots[s].layer];
   return d->act_bf16 && (d->flags & ALTXS_F_FUSE_O) && d->W == 1 && R < kBigRows &&
          !d->plan_dev && d->kv_bf16 == ALTXS_KV_BF16 && d->kv_tail_end == 0 && d->H == d->Hkv &&
-         d->H % 4 == 0 && d->D <= 512 && d->D % 16 == 0 && L.o.N == d->D && L.o.K == (int64_t)d->H * HD &&
+         d->H % 4 == 0 && (d->D == 256 || d->D == 512) && L.o.N == d->D && L.o.K == (int64_t)d->H * HD &&
          (L.o.bits == 2 || L.o.bits == 3 || L.o.bits == 4 || L.o.bits == 6);
 }
 

@@ -969,6 +969,8 @@ struct ProOutNorm {
   float* xout;              // [R, D], stored by the first column task
   float scale, eps;
   int D;
+  // D = 256 or 512 (out_proj_fused): D / 4 column quads divide the NT threads
+  // into NT / (D / 4) row groups that cover the task's 16 rows exactly
   template <int AM, int NT>
   __device__ void stage(void* As, void* scratch, int m0, int R, int K, int, bool first) const {
     static_assert(NT == 16 * PTPR, "one row per 16 lanes, 16 rows per task");

@@ -151,5 +151,8 @@ def test_fused_out_projection_query_host_logic():
         setattr(d, field, value)
         assert q() == 0, field
         setattr(d, field, old)
+    d.D = 384  # the prologue's row mapping covers D = 256 and 512
+    assert q() == 0
+    d.D = 512
     d.layers[0].o.bits = 16  # dense bf16 out-projection
     assert q(0) == 0 and q(1) == 1
