@@ -143,7 +143,7 @@ int split_fork_stage() {
 // column task of a sequential slot then reads H terms per element instead of
 // one, and each attention workgroup decodes the out-projection's codes of its
 // head for its one row (the GEMM decodes them once per 8-row tile); cfg3,
-// per slot: attention +2.5 us, MLP up +6.4 us (B = 64) / +2.5 us (B = 1),
+// per slot: attention +2.5 us (B = 64) / +2.0 us (B = 1), MLP up +5.6 / +1.8 us,
 // against the 4.4-4.6 us launch saved.
 bool out_proj_fused(const AltxsStepDesc* d, int s, int R) {
   const AltxsLayer& L = d->layers[d->slots[s].layer];

@@ -809,20 +809,15 @@ struct OutFin {
   const uint16_t* osc = nullptr;
   const float* attn_scale = nullptr;
   int H = 0, ks = 1;
-  struct El { float t[HMAX], s[HMAX], a; };
+  // loaded in a prologue, used after the k-loop: the scales stay fp16 pairs
+  // as loaded (converted in value()), so nothing waits for them before it
+  struct El { float t[HMAX], a; u32x2 s[HMAX / 4]; };
   __device__ El load(int r, int c, int D) const {
     El e;
     const int KB = H >> 2;
 #pragma unroll
-    for (int kb = 0; kb < HMAX / 4; ++kb) {
-      if (kb < KB) {  // the column's four group scales of block kb
-        const u32x2 w = *(const u32x2*)(osc + ((int64_t)(c >> 4) * KB + kb) * 64 + (c & 15) * 4);
-        e.s[4 * kb] = half_lo(w[0]);
-        e.s[4 * kb + 1] = half_hi(w[0]);
-        e.s[4 * kb + 2] = half_lo(w[1]);
-        e.s[4 * kb + 3] = half_hi(w[1]);
-      }
-    }
+    for (int kb = 0; kb < HMAX / 4; ++kb)  // the column's four group scales of block kb
+      e.s[kb] = *(const u32x2*)(osc + ((int64_t)(c >> 4) * KB + (kb < KB ? kb : 0)) * 64 + (c & 15) * 4);
 #pragma unroll
     for (int h = 0; h < HMAX; ++h)
       if (h < H) e.t[h] = part[((int64_t)r * H + h) * D + c];
@@ -835,7 +830,8 @@ struct OutFin {
 #pragma unroll
     for (int h = 0; h < HMAX; ++h) {
       if (h < H) {
-        acc += e.s[h] * e.t[h];
+        const uint32_t w = e.s[h >> 2][(h & 3) >> 1];
+        acc += ((h & 1) ? half_hi(w) : half_lo(w)) * e.t[h];
         if ((h + 1) % hps == 0) {  // end of a K-slice: slices added in order
           sum = h + 1 == hps ? acc : sum + acc;
           acc = 0.f;
@@ -979,24 +975,23 @@ struct ProOutNorm {
     {  // x_out of the task's rows, four columns per thread
       const int nq = D >> 2, rgs = NT / nq, cq = t % nq, rg = t / nq;
       const int c0 = 4 * cq, KB = of.H >> 2, hps = of.H / of.ks, H = of.H;
-      float scl[HMAX][4];
+      // 16 scales per block: columns c0 .. c0+3 x the block's four groups,
+      // kept as loaded (fp16 pairs) until their first use, so that the first
+      // rows' term loads are issued before anything waits for them
+      u32x4 sraw[HMAX / 4][2];
 #pragma unroll
       for (int kb = 0; kb < HMAX / 4; ++kb) {
-        if (kb < KB) {  // 16 scales: columns c0 .. c0+3 x the block's four groups
-          const uint16_t* sp = of.osc + ((int64_t)(c0 >> 4) * KB + kb) * 64 + (c0 & 15) * 4;
-          const u32x4 lo = *(const u32x4*)sp, hi = *(const u32x4*)(sp + 8);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const u32x4& w = e < 2 ? lo : hi;
-            const uint32_t w0 = w[2 * (e & 1)], w1 = w[2 * (e & 1) + 1];
-            scl[4 * kb + 0][e] = half_lo(w0);
-            scl[4 * kb + 1][e] = half_hi(w0);
-            scl[4 * kb + 2][e] = half_lo(w1);
-            scl[4 * kb + 3][e] = half_hi(w1);
-          }
-        }
+        const int kbc = kb < KB ? kb : 0;
+        const uint16_t* sp = of.osc + ((int64_t)(c0 >> 4) * KB + kbc) * 64 + (c0 & 15) * 4;
+        sraw[kb][0] = *(const u32x4*)sp;
+        sraw[kb][1] = *(const u32x4*)(sp + 8);
       }
       const f32x4 asc = *(const f32x4*)(of.attn_scale + c0);
+      auto scl = [&](int h, int e) {  // scale of head h (block h / 4, group h % 4), column c0 + e
+        const u32x4& w = sraw[h >> 2][e >> 1];
+        const uint32_t v = w[2 * (e & 1) + ((h & 3) >> 1)];
+        return (h & 1) ? half_hi(v) : half_lo(v);
+      };
       for (int i0 = 0; i0 < 16 / rgs; i0 += 2) {
         if (m0 + rgs * i0 >= R) break;  // no row of this pair is below R in any thread
         f32x4 tv[2][HMAX], base[2];
@@ -1019,7 +1014,7 @@ struct ProOutNorm {
 #pragma unroll
             for (int h = 0; h < HMAX; ++h) {
               if (h < H) {
-                acc += scl[h][e] * tv[u][h][e];
+                acc += scl(h, e) * tv[u][h][e];
                 if ((h + 1) % hps == 0) {  // end of a K-slice: slices added in order
                   sum = h + 1 == hps ? acc : sum + acc;
                   acc = 0.f;
